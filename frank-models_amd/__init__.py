@@ -1,0 +1,56 @@
+"""frank-models_amd: the MoE FFN hot path of stellaraccident/frank-models,
+rebuilt for AMD MI355X (gfx950).
+
+Public API (same signatures as the reference's components/oracles):
+
+* ``moe_ffn_block(input, gate_inp_w, up_exps_w, gate_exps_w, down_exps_w,
+  n_expert, n_expert_used, n_embd, n_ff, normalize_weights)``
+* ``mul_mat_id(weights, input, ids)``
+* ``swiglu(gate, up)``
+
+plus ``router``, ``permute``, ``pack_expert_weights``,
+``quantize_expert_weights``, ``QuantizedExpertWeights``,
+``PackedExpertWeights`` and ``MoEFFNBlock`` (packed weights + reusable
+workspace for repeated calls).  All arithmetic runs in libfmoe.so; import
+fails loudly if it has not been built.
+
+The directory name is not a Python identifier; import it with
+``importlib.import_module("frank-models_amd")``.
+"""
+
+from ._lib import (  # noqa: F401
+    FmoeError,
+    NoDeviceError,
+    hip_runtimes_loaded,
+    lib as _load_lib,
+)
+from .api import (  # noqa: F401
+    MoEFFNBlock,
+    PackedExpertWeights,
+    QuantizedExpertWeights,
+    moe_ffn_block,
+    mul_mat_id,
+    pack_expert_weights,
+    permute,
+    quantize_expert_weights,
+    router,
+    swiglu,
+)
+from . import _lib as lowlevel  # noqa: F401
+
+_load_lib()
+
+__all__ = [
+    "moe_ffn_block",
+    "mul_mat_id",
+    "swiglu",
+    "router",
+    "permute",
+    "pack_expert_weights",
+    "quantize_expert_weights",
+    "QuantizedExpertWeights",
+    "PackedExpertWeights",
+    "MoEFFNBlock",
+    "FmoeError",
+    "NoDeviceError",
+]

@@ -1,0 +1,533 @@
+// C ABI of libfmoe.so: argument validation, workspace layout and the launch
+// sequence of each entry point.  Declarations and reference citations are in
+// include/fmoe.h.
+#include "fmoe.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "launch.h"
+
+using namespace fmoe;
+
+namespace {
+
+thread_local char g_err[512] = "";
+thread_local int g_last_path = FMOE_PATH_AUTO;
+std::atomic<int> g_path{FMOE_PATH_AUTO};
+
+constexpr int64_t kMaxExpert = 256;       // router lanes hold 4 experts each
+constexpr int64_t kMaxExpertUsed = 64;    // one slot per lane in top-k
+constexpr int64_t kMaxDim = (1ll << 31) - 1;
+constexpr size_t kAlign = 256;
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return FMOE_OK;
+}
+
+#define FMOE_HIP(call)                                                                     \
+  do {                                                                                     \
+    hipError_t e_ = (call);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      return fail(FMOE_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));            \
+  } while (0)
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool act_dtype_ok(int dt) { return dt == FMOE_F32 || dt == FMOE_BF16; }
+bool w_dtype_ok(int dt) { return dt == FMOE_F32 || dt == FMOE_BF16 || dt == FMOE_F8E4M3FN; }
+
+bool aligned_for(const void* p, int dt) {
+  return reinterpret_cast<uintptr_t>(p) % dtype_bytes(dt) == 0;
+}
+
+// Device check, cached per device ordinal.
+std::mutex g_dev_mu;
+int g_dev_state[64] = {0};  // 0 unknown, 1 gfx950, -1 other
+
+int ensure_device(int* dev_out = nullptr, char* arch = nullptr, size_t arch_len = 0) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0)
+    return fail(FMOE_ERR_NO_DEVICE, "no HIP device available (%s)",
+                e == hipSuccess ? "device count 0" : hipGetErrorString(e));
+  int dev = 0;
+  e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FMOE_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev_out) *dev_out = dev;
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if (dev < 64 && g_dev_state[dev] == 1 && !arch) return FMOE_OK;
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess)
+    return fail(FMOE_ERR_NO_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (arch && arch_len) {
+    strncpy(arch, prop.gcnArchName, arch_len - 1);
+    arch[arch_len - 1] = '\0';
+  }
+  const bool is950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  if (dev < 64) g_dev_state[dev] = is950 ? 1 : -1;
+  if (!is950)
+    return fail(FMOE_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only", dev,
+                prop.gcnArchName);
+  return FMOE_OK;
+}
+
+// Runs one grouped GEMM on the family the process-wide setting asks for,
+// falling back to the automatic choice when that family cannot run it.
+int run_grouped_gemm(const GroupedGemmArgs& g, hipStream_t s) {
+  const int want = g_path.load(std::memory_order_relaxed);
+  const bool can_tile = gemm_tiled_supported(g);
+  const bool can_stream = gemm_stream_supported(g);
+  int path = FMOE_PATH_GENERIC;
+  if (want == FMOE_PATH_TILED && can_tile)
+    path = FMOE_PATH_TILED;
+  else if (want == FMOE_PATH_STREAM && can_stream)
+    path = FMOE_PATH_STREAM;
+  else if (want == FMOE_PATH_GENERIC)
+    path = FMOE_PATH_GENERIC;
+  else {
+    // Few rows per expert: stream the weights once; otherwise tile.
+    const bool small = static_cast<int64_t>(g.n_assign) <= 16ll * g.n_expert;
+    if (small && can_stream)
+      path = FMOE_PATH_STREAM;
+    else if (can_tile)
+      path = FMOE_PATH_TILED;
+    else if (can_stream)
+      path = FMOE_PATH_STREAM;
+  }
+  hipError_t e;
+  if (path == FMOE_PATH_TILED)
+    e = launch_gemm_tiled(g, s);
+  else if (path == FMOE_PATH_STREAM)
+    e = launch_gemm_stream(g, s);
+  else
+    e = launch_gemm_generic(g, s);
+  g_last_path = path;
+  if (e != hipSuccess) return fail(FMOE_ERR_HIP, "grouped GEMM launch: %s", hipGetErrorString(e));
+  return FMOE_OK;
+}
+
+// ------------------------------------------------------------ workspaces
+struct PermuteLayout {
+  size_t order, offsets, err, total;
+};
+
+PermuteLayout permute_layout(int64_t n_assign, int64_t n_expert, size_t base = 0) {
+  PermuteLayout L;
+  size_t off = base;
+  L.err = off;
+  off += align_up(16);
+  L.order = off;
+  off += align_up(static_cast<size_t>(n_assign) * 4);
+  L.offsets = off;
+  off += align_up(static_cast<size_t>(n_expert + 1) * 4);
+  L.total = off;
+  return L;
+}
+
+struct MmidLayout {
+  PermuteLayout perm;
+  size_t x, y, total;
+};
+
+MmidLayout mmid_layout(int64_t n_out, int64_t n_in, int64_t n_expert, int64_t k, int64_t T,
+                       int act) {
+  MmidLayout L;
+  const int64_t n = k * T;
+  L.perm = permute_layout(n, n_expert);
+  size_t off = L.perm.total;
+  L.x = off;
+  off += align_up(static_cast<size_t>(n) * n_in * dtype_bytes(act));
+  L.y = off;
+  off += align_up(static_cast<size_t>(n) * n_out * dtype_bytes(act));
+  L.total = off;
+  return L;
+}
+
+struct BlockLayout {
+  size_t ids, weights;
+  PermuteLayout perm;
+  size_t h, y, total;
+  int h_dtype, y_dtype;
+};
+
+BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act) {
+  BlockLayout L;
+  const int64_t n = k * T;
+  size_t off = 0;
+  L.ids = off;
+  off += align_up(static_cast<size_t>(n) * 4);
+  L.weights = off;
+  off += align_up(static_cast<size_t>(n) * 4);
+  L.perm = permute_layout(n, E, off);
+  off = L.perm.total;
+  L.h_dtype = act;
+  L.h = off;
+  off += align_up(static_cast<size_t>(n) * F * dtype_bytes(L.h_dtype));
+  L.y_dtype = FMOE_F32;
+  L.y = off;
+  off += align_up(static_cast<size_t>(n) * H * dtype_bytes(L.y_dtype));
+  L.total = off;
+  return L;
+}
+
+template <typename T>
+T* at(void* base, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+int check_dims(const char* what, int64_t v, int64_t lo, int64_t hi) {
+  if (v < lo || v > hi)
+    return fail(FMOE_ERR_SHAPE, "%s=%lld outside [%lld, %lld]", what, static_cast<long long>(v),
+                static_cast<long long>(lo), static_cast<long long>(hi));
+  return FMOE_OK;
+}
+
+#define FMOE_TRY(x)            \
+  do {                         \
+    int r_ = (x);              \
+    if (r_ != FMOE_OK) return r_; \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+const char* fmoe_last_error(void) { return g_err; }
+
+int fmoe_abi_version(void) { return FMOE_ABI_VERSION; }
+
+int fmoe_device_check(int* device, char* arch, size_t arch_len) {
+  FMOE_TRY(ensure_device(device, arch, arch_len));
+  return ok();
+}
+
+int fmoe_set_gemm_path(int path) {
+  if (path < FMOE_PATH_AUTO || path > FMOE_PATH_STREAM)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "unknown gemm path %d", path);
+  g_path.store(path);
+  return ok();
+}
+
+int fmoe_get_gemm_path(void) { return g_path.load(); }
+
+int fmoe_last_gemm_path(void) { return g_last_path; }
+
+int fmoe_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  if (!act_dtype_ok(dtype)) return fail(FMOE_ERR_DTYPE, "swiglu dtype %d not F32/BF16", dtype);
+  FMOE_TRY(check_dims("n", n, 0, (1ll << 62)));
+  if (n == 0) return ok();
+  if (!gate || !up || !out) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!aligned_for(gate, dtype) || !aligned_for(up, dtype) || !aligned_for(out, dtype))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+static int validate_router(int64_t T, int64_t H, int64_t E, int64_t k) {
+  FMOE_TRY(check_dims("n_tokens", T, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_embd", H, 1, kMaxDim));
+  FMOE_TRY(check_dims("n_expert", E, 1, kMaxExpert));
+  FMOE_TRY(check_dims("n_expert_used", k, 1, E < kMaxExpertUsed ? E : kMaxExpertUsed));
+  if (k * T > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_expert_used * n_tokens exceeds 2^31-1");
+  return FMOE_OK;
+}
+
+int fmoe_router(const void* input, const void* w_router, int64_t n_tokens, int64_t n_embd,
+                int64_t n_expert, int64_t n_expert_used, int normalize_weights, int dtype,
+                int32_t* ids_out, float* weights_out, void* stream) {
+  if (!act_dtype_ok(dtype)) return fail(FMOE_ERR_DTYPE, "router dtype %d not F32/BF16", dtype);
+  FMOE_TRY(validate_router(n_tokens, n_embd, n_expert, n_expert_used));
+  if (normalize_weights != 0 && normalize_weights != 1)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "normalize_weights must be 0 or 1");
+  if (n_tokens == 0) return ok();
+  if (!input || !w_router || !ids_out || !weights_out)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_router(input, w_router, static_cast<int>(n_tokens), static_cast<int>(n_embd),
+                         static_cast<int>(n_expert), static_cast<int>(n_expert_used),
+                         normalize_weights != 0, dtype, ids_out, weights_out,
+                         static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+size_t fmoe_permute_workspace_bytes(int64_t n_expert_used, int64_t n_tokens, int64_t n_expert) {
+  (void)n_expert_used;
+  (void)n_tokens;
+  (void)n_expert;
+  return align_up(16);
+}
+
+int fmoe_permute(const int32_t* ids, int64_t n_expert_used, int64_t n_tokens, int64_t n_expert,
+                 int32_t* order_out, int32_t* offsets_out, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  FMOE_TRY(check_dims("n_tokens", n_tokens, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_expert", n_expert, 1, 512));
+  FMOE_TRY(check_dims("n_expert_used", n_expert_used, 1, kMaxDim));
+  if (n_expert_used * n_tokens > kMaxDim)
+    return fail(FMOE_ERR_SHAPE, "n_expert_used * n_tokens exceeds 2^31-1");
+  if (!offsets_out || !workspace) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (workspace_bytes < fmoe_permute_workspace_bytes(n_expert_used, n_tokens, n_expert))
+    return fail(FMOE_ERR_WORKSPACE, "workspace too small");
+  if (n_tokens > 0 && (!ids || !order_out)) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_permute(ids, static_cast<int>(n_expert_used * n_tokens),
+                          static_cast<int>(n_expert), order_out, offsets_out,
+                          static_cast<int*>(workspace), static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int fmoe_workspace_error_count(const void* workspace, void* stream, int64_t* count_out) {
+  if (!workspace || !count_out) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  FMOE_TRY(ensure_device());
+  int v = 0;
+  FMOE_HIP(hipMemcpyAsync(&v, workspace, sizeof(int), hipMemcpyDeviceToHost,
+                          static_cast<hipStream_t>(stream)));
+  FMOE_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  *count_out = v;
+  return ok();
+}
+
+size_t fmoe_packed_weight_bytes(int64_t n_out, int64_t n_in, int64_t n_expert, int dtype) {
+  if (n_out < 0 || n_in < 0 || n_expert < 0 || !w_dtype_ok(dtype)) return 0;
+  return static_cast<size_t>(n_out) * n_in * n_expert * dtype_bytes(dtype);
+}
+
+int fmoe_pack_expert_weights(const void* src, int src_dtype, const float* src_scales,
+                             int64_t n_out, int64_t n_in, int64_t n_expert, int dst_dtype,
+                             void* dst, float* dst_scales, void* stream) {
+  if (!w_dtype_ok(src_dtype) || !w_dtype_ok(dst_dtype))
+    return fail(FMOE_ERR_DTYPE, "pack dtypes %d -> %d", src_dtype, dst_dtype);
+  if (src_dtype == FMOE_F8E4M3FN && dst_dtype != FMOE_F8E4M3FN)
+    return fail(FMOE_ERR_DTYPE, "fp8 weights can only be packed as fp8");
+  FMOE_TRY(check_dims("n_out", n_out, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_in", n_in, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_expert", n_expert, 1, 1024));
+  if (n_out == 0 || n_in == 0) return ok();
+  if (!src || !dst) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (src_dtype == FMOE_F8E4M3FN && !src_scales)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 source needs src_scales");
+  if (dst_dtype == FMOE_F8E4M3FN && !dst_scales)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 destination needs dst_scales");
+  if (!aligned_for(src, src_dtype) || !aligned_for(dst, dst_dtype))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_pack(src, src_dtype, src_scales, static_cast<int>(n_out), static_cast<int>(n_in),
+                       static_cast<int>(n_expert), dst_dtype, dst, dst_scales,
+                       static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+size_t fmoe_mul_mat_id_workspace_bytes(int64_t n_out, int64_t n_in, int64_t n_expert,
+                                       int64_t n_expert_used, int64_t n_tokens, int act_dtype) {
+  if (!act_dtype_ok(act_dtype) || n_out < 0 || n_in < 0 || n_expert < 1 || n_expert_used < 0 ||
+      n_tokens < 0)
+    return 0;
+  return mmid_layout(n_out, n_in, n_expert, n_expert_used, n_tokens, act_dtype).total;
+}
+
+int fmoe_mul_mat_id(const void* packed_w, const float* w_scales, int w_dtype, const void* input,
+                    const int32_t* ids, void* out, int64_t n_out, int64_t n_in, int64_t n_expert,
+                    int64_t n_expert_used, int64_t n_tokens, int act_dtype, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (!act_dtype_ok(act_dtype)) return fail(FMOE_ERR_DTYPE, "activation dtype %d", act_dtype);
+  if (!w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", w_dtype);
+  if (act_dtype == FMOE_F32 && w_dtype != FMOE_F32)
+    return fail(FMOE_ERR_DTYPE, "f32 activations need f32 weights");
+  FMOE_TRY(check_dims("n_out", n_out, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_in", n_in, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_expert", n_expert, 1, 512));
+  FMOE_TRY(check_dims("n_expert_used", n_expert_used, 1, kMaxDim));
+  FMOE_TRY(check_dims("n_tokens", n_tokens, 0, kMaxDim));
+  const int64_t n = n_expert_used * n_tokens;
+  if (n > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_expert_used * n_tokens exceeds 2^31-1");
+  if (n == 0 || n_out == 0) return ok();
+  if (!packed_w || !input || !ids || !out || !workspace)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (w_dtype == FMOE_F8E4M3FN && !w_scales)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
+  const MmidLayout L = mmid_layout(n_out, n_in, n_expert, n_expert_used, n_tokens, act_dtype);
+  if (workspace_bytes < L.total)
+    return fail(FMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, L.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
+  if (!aligned_for(input, act_dtype) || !aligned_for(out, act_dtype))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  FMOE_TRY(ensure_device());
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int* err = at<int>(workspace, L.perm.err);
+  int* order = at<int>(workspace, L.perm.order);
+  int* offsets = at<int>(workspace, L.perm.offsets);
+  void* x = at<char>(workspace, L.x);
+  void* y = at<char>(workspace, L.y);
+  // input [n_in, k*T] -> x [k*T, n_in]: row f = s*T + t (mul_mat_id.mlir:63-90)
+  if (n_in > 0) FMOE_HIP(launch_transpose(input, x, n_in, n, act_dtype, s));
+  FMOE_HIP(launch_permute(ids, static_cast<int>(n), static_cast<int>(n_expert), order, offsets, err, s));
+  GroupedGemmArgs g;
+  g.a = x;
+  g.lda = n_in;
+  g.a_mode = A_GATHER_FLAT;
+  g.order = order;
+  g.offsets = offsets;
+  g.n_tokens = static_cast<int>(n_tokens);
+  g.n_assign = static_cast<int>(n);
+  g.n_expert = static_cast<int>(n_expert);
+  g.w0 = packed_w;
+  g.s0 = w_dtype == FMOE_F8E4M3FN ? w_scales : nullptr;
+  g.N = n_out;
+  g.K = n_in;
+  g.out = y;
+  g.ldo = n_out;
+  g.epi = EPI_SCATTER;
+  g.act_dtype = act_dtype;
+  g.w_dtype = w_dtype;
+  g.out_dtype = act_dtype;
+  FMOE_TRY(run_grouped_gemm(g, s));
+  FMOE_HIP(launch_zero_invalid_rows(ids, static_cast<int>(n), static_cast<int>(n_expert), y,
+                                    act_dtype, n_out, s));
+  // y [k*T, n_out] -> out [n_out, k*T] (mul_mat_id.mlir:96-117)
+  FMOE_HIP(launch_transpose(y, out, n, n_out, act_dtype, s));
+  return ok();
+}
+
+size_t fmoe_moe_ffn_block_workspace_bytes(int64_t n_tokens, int64_t n_expert,
+                                          int64_t n_expert_used, int64_t n_embd, int64_t n_ff,
+                                          int act_dtype, int w_dtype) {
+  if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
+      n_expert_used < 1 || n_embd < 1 || n_ff < 0)
+    return 0;
+  return block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype).total;
+}
+
+int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* packed_up,
+                       const void* packed_gate, const void* packed_down, const float* up_scales,
+                       const float* gate_scales, const float* down_scales, int w_dtype, void* out,
+                       int64_t n_tokens, int64_t n_expert, int64_t n_expert_used, int64_t n_embd,
+                       int64_t n_ff, int normalize_weights, int act_dtype, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (!act_dtype_ok(act_dtype)) return fail(FMOE_ERR_DTYPE, "activation dtype %d", act_dtype);
+  if (!w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", w_dtype);
+  if (act_dtype == FMOE_F32 && w_dtype != FMOE_F32)
+    return fail(FMOE_ERR_DTYPE, "f32 activations need f32 weights");
+  FMOE_TRY(validate_router(n_tokens, n_embd, n_expert, n_expert_used));
+  FMOE_TRY(check_dims("n_ff", n_ff, 0, kMaxDim));
+  if (normalize_weights != 0 && normalize_weights != 1)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "normalize_weights must be 0 or 1");
+  if (n_tokens == 0) return ok();
+  if (!input || !w_router || !packed_up || !packed_gate || !packed_down || !out || !workspace)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (w_dtype == FMOE_F8E4M3FN && (!up_scales || !gate_scales || !down_scales))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
+  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype);
+  if (workspace_bytes < L.total)
+    return fail(FMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, L.total);
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
+  if (!aligned_for(input, act_dtype) || !aligned_for(out, act_dtype) ||
+      !aligned_for(w_router, act_dtype))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  FMOE_TRY(ensure_device());
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int T = static_cast<int>(n_tokens);
+  const int n = static_cast<int>(n_tokens * n_expert_used);
+  int* ids = at<int>(workspace, L.ids);
+  float* rw = at<float>(workspace, L.weights);
+  int* err = at<int>(workspace, L.perm.err);
+  int* order = at<int>(workspace, L.perm.order);
+  int* offsets = at<int>(workspace, L.perm.offsets);
+  void* h = at<char>(workspace, L.h);
+  void* y = at<char>(workspace, L.y);
+
+  // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128).
+  FMOE_HIP(launch_router(input, w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
+                         static_cast<int>(n_expert_used), normalize_weights != 0, act_dtype, ids,
+                         rw, s));
+  // Group the slot-major assignments by expert (replaces the gather, mul_mat_id.mlir:50-61).
+  FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err, s));
+
+  // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
+  GroupedGemmArgs g;
+  g.a = input;
+  g.lda = n_embd;
+  g.a_mode = A_GATHER_TOKEN;
+  g.order = order;
+  g.offsets = offsets;
+  g.n_tokens = T;
+  g.n_assign = n;
+  g.n_expert = static_cast<int>(n_expert);
+  g.w0 = packed_gate;
+  g.w1 = packed_up;
+  if (w_dtype == FMOE_F8E4M3FN) {
+    g.s0 = gate_scales;
+    g.s1 = up_scales;
+  }
+  g.N = n_ff;
+  g.K = n_embd;
+  g.out = h;
+  g.ldo = n_ff;
+  g.epi = EPI_SWIGLU;
+  g.act_dtype = act_dtype;
+  g.w_dtype = w_dtype;
+  g.out_dtype = L.h_dtype;
+  FMOE_TRY(run_grouped_gemm(g, s));
+
+  // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
+  GroupedGemmArgs d;
+  d.a = h;
+  d.lda = n_ff;
+  d.a_mode = A_DIRECT;
+  d.order = order;
+  d.offsets = offsets;
+  d.n_tokens = T;
+  d.n_assign = n;
+  d.n_expert = static_cast<int>(n_expert);
+  d.w0 = packed_down;
+  d.s0 = w_dtype == FMOE_F8E4M3FN ? down_scales : nullptr;
+  d.N = n_embd;
+  d.K = n_ff;
+  d.out = y;
+  d.ldo = n_embd;
+  d.epi = EPI_SCATTER_WEIGHTED;
+  d.route_w = rw;
+  d.act_dtype = L.h_dtype;
+  d.w_dtype = w_dtype;
+  d.out_dtype = L.y_dtype;
+  FMOE_TRY(run_grouped_gemm(d, s));
+
+  // Step 11: slot-ordered sum + transpose to [n_tokens, n_embd] (mlir:179-206).
+  FMOE_HIP(launch_combine(y, L.y_dtype, out, act_dtype, T, static_cast<int>(n_expert_used),
+                          static_cast<int>(n_embd), s));
+  return ok();
+}
+
+int fmoe_moe_ffn_block_routing(void* workspace, int64_t n_tokens, int64_t n_expert,
+                               int64_t n_expert_used, int64_t n_embd, int64_t n_ff, int act_dtype,
+                               int w_dtype, int32_t** ids, float** weights, int32_t** order,
+                               int32_t** offsets) {
+  if (!workspace) return fail(FMOE_ERR_INVALID_ARGUMENT, "null workspace");
+  if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "dtype");
+  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype);
+  if (ids) *ids = at<int32_t>(workspace, L.ids);
+  if (weights) *weights = at<float>(workspace, L.weights);
+  if (order) *order = at<int32_t>(workspace, L.perm.order);
+  if (offsets) *offsets = at<int32_t>(workspace, L.perm.offsets);
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+// Device-side helpers shared by the gfx950 kernels of the MoE FFN path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmoe {
+
+typedef uint16_t bf16_t;  // bfloat16 bit pattern in memory
+typedef uint8_t f8_t;     // OCP e4m3fn code in memory
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- numbers
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32), NaN stays NaN.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  __bf16 b = static_cast<__bf16>(f);
+  return __builtin_bit_cast(bf16_t, b);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+  bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// OCP FP8 E4M3 (e4m3fn) code -> float: (8+m) * 2^(e-10) for e>0, m * 2^-9 for
+// e=0, NaN for S.1111.111.
+__device__ __forceinline__ float e4m3fn_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xFu;
+  uint32_t m = c & 7u;
+  float mag;
+  if (e == 0) {
+    mag = static_cast<float>(m) * 0x1p-9f;
+  } else if (e == 15 && m == 7) {
+    mag = __uint_as_float(0x7FC00000u);
+  } else {
+    mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  }
+  return __uint_as_float(__float_as_uint(mag) | s);
+}
+
+// float -> e4m3fn code, round to nearest even, finite overflow saturates to
+// +-448, NaN -> 0x7F.
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  uint32_t bits = __float_as_uint(x);
+  uint32_t sign = (bits >> 24) & 0x80u;
+  float a = fabsf(x);
+  if (a != a) return 0x7Fu;
+  if (a >= 448.0f) return sign | 0x7Eu;
+  uint32_t ab = __float_as_uint(a);
+  int32_t exp = static_cast<int32_t>(ab >> 23) - 127;
+  uint32_t code;
+  if (exp < -6) {
+    // subnormal range: value = m * 2^-9, m in [0, 8]; scale exactly by 2^9.
+    float q = a * 512.0f;  // exact (power of two scaling, no underflow here)
+    float r = rintf(q);    // ties to even
+    code = static_cast<uint32_t>(r);  // 8 becomes the smallest normal 0x08
+  } else {
+    // normal: keep 3 mantissa bits with RNE on the 20 dropped bits.
+    uint32_t mant = ab & 0x7FFFFFu;
+    uint32_t keep = mant >> 20;
+    uint32_t rest = mant & 0xFFFFFu;
+    uint32_t e = static_cast<uint32_t>(exp + 7);
+    uint32_t v = (e << 3) | keep;
+    if (rest > 0x80000u || (rest == 0x80000u && (keep & 1u))) v += 1;
+    code = v > 0x7Eu ? 0x7Eu : v;
+  }
+  return sign | code;
+}
+
+// ---------------------------------------------------------------- waves
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    int u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- tiles
+// A grouped-GEMM row tile: rows [row0, row0+rows) of the expert-sorted
+// assignment list, all routed to `expert`.
+struct TileInfo {
+  int expert;
+  int row0;
+  int rows;
+};
+
+// Maps tile number `tile` to its expert and rows, given the permutation
+// offsets [n_expert+1] and the tile height bm.  Experts contribute
+// ceil(count/bm) tiles each, in expert order.  Every lane of the calling wave
+// must participate; all lanes get the same answer.  Returns false when `tile`
+// is past the last tile.
+__device__ __forceinline__ bool find_tile(const int* __restrict__ offsets, int n_expert,
+                                          int bm, int tile, TileInfo* out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int base = 0;
+  for (int c = 0; c < n_expert; c += kWave) {
+    const int e = c + lane;
+    int cnt = 0;
+    if (e < n_expert) cnt = offsets[e + 1] - offsets[e];
+    const int nt = (cnt + bm - 1) / bm;
+    const int incl = wave_inclusive_scan(nt);
+    const int excl = incl - nt;
+    const bool hit = (tile >= base + excl) && (tile < base + incl);
+    const uint64_t m = __ballot(hit);
+    if (m) {
+      const int src = __builtin_ctzll(m);
+      const int ee = __shfl(e, src, kWave);
+      const int ex = __shfl(excl, src, kWave);
+      const int cn = __shfl(cnt, src, kWave);
+      const int local = tile - base - ex;
+      out->expert = ee;
+      out->row0 = offsets[ee] + local * bm;
+      out->rows = min(bm, cn - local * bm);
+      return true;
+    }
+    base += __shfl(incl, kWave - 1, kWave);
+  }
+  return false;
+}
+
+}  // namespace fmoe

@@ -1,0 +1,92 @@
+// Host-side launchers of the gfx950 kernels (internal to libfmoe.so).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fmoe {
+
+// Element types; values match fmoe_dtype in include/fmoe.h.
+enum DType { DT_F32 = 0, DT_BF16 = 1, DT_F8 = 2 };
+
+inline size_t dtype_bytes(int dt) { return dt == DT_F32 ? 4 : dt == DT_BF16 ? 2 : 1; }
+
+// How a grouped GEMM finds row p's A operand.
+enum AMode {
+  A_GATHER_TOKEN = 0,  // row order[p] % n_tokens of `a` (x rows, per token)
+  A_GATHER_FLAT = 1,   // row order[p] of `a` (flat slot-major assignment rows)
+  A_DIRECT = 2         // row p of `a` (rows already in expert-sorted order)
+};
+
+// What a grouped GEMM does with its fp32 accumulators.
+enum Epilogue {
+  EPI_SWIGLU = 0,            // out[p, n] = g * silu(u) from the two weight sets
+  EPI_SCATTER = 1,           // out[order[p], n] = acc
+  EPI_SCATTER_WEIGHTED = 2   // out[order[p], n] = acc * route_w[order[p]]
+};
+
+struct GroupedGemmArgs {
+  const void* a = nullptr;      // A operand base, act_dtype
+  int64_t lda = 0;              // elements between A rows
+  int a_mode = A_DIRECT;
+  const int* order = nullptr;   // [n_assign] expert-sorted flat assignment ids
+  const int* offsets = nullptr; // [n_expert + 1]
+  int n_tokens = 0;
+  int n_assign = 0;             // k * n_tokens
+  int n_expert = 0;
+  const void* w0 = nullptr;     // packed weights [E][N][K] (gate, or the only set)
+  const void* w1 = nullptr;     // packed up weights for EPI_SWIGLU
+  const float* s0 = nullptr;    // [E][N] scales for fp8 weights
+  const float* s1 = nullptr;
+  int64_t N = 0, K = 0;
+  void* out = nullptr;
+  int64_t ldo = 0;              // elements between output rows
+  int epi = EPI_SCATTER;
+  const float* route_w = nullptr;  // [n_assign] routing weight per flat assignment
+  int act_dtype = DT_F32;       // A operand type
+  int w_dtype = DT_F32;
+  int out_dtype = DT_F32;
+};
+
+// Upper bound on the number of bm-row tiles of a grouping of n_assign rows
+// over n_expert experts.
+inline int max_row_tiles(int n_assign, int n_expert, int bm) {
+  const int e = n_assign < n_expert ? n_assign : n_expert;
+  return n_assign / bm + e;
+}
+
+hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd,
+                         int n_expert, int k, bool normalize, int dtype, int* ids,
+                         float* weights, hipStream_t stream);
+
+hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order,
+                          int* offsets, int* err_count, hipStream_t stream);
+
+hipError_t launch_pack(const void* src, int src_dtype, const float* src_scales,
+                       int n_out, int n_in, int n_expert, int dst_dtype, void* dst,
+                       float* dst_scales, hipStream_t stream);
+
+hipError_t launch_gemm_generic(const GroupedGemmArgs& g, hipStream_t stream);
+// Returns hipErrorNotSupported when the shape or dtype is outside what the
+// MFMA kernels handle; the caller then uses the generic kernel.
+hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t stream);
+hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t stream);
+bool gemm_tiled_supported(const GroupedGemmArgs& g);
+bool gemm_stream_supported(const GroupedGemmArgs& g);
+
+hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
+                         int dtype, hipStream_t stream);
+// out[t, :] = sum over s = 0..k-1 (in order) of y[s*n_tokens + t, :]
+hipError_t launch_combine(const void* y, int y_dtype, void* out, int out_dtype,
+                          int n_tokens, int k, int n_embd, hipStream_t stream);
+// out[c, r] = in[r, c] for an in[rows, cols] matrix (same dtype).
+hipError_t launch_transpose(const void* in, void* out, int64_t rows, int64_t cols,
+                            int dtype, hipStream_t stream);
+// Zero rows f of y[n_assign, width] whose id is outside [0, n_expert).
+hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert,
+                                    void* y, int dtype, int64_t width,
+                                    hipStream_t stream);
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+
+}  // namespace fmoe

@@ -1,0 +1,215 @@
+// Router: logits = W_router @ x^T (fp32 accumulate), softmax over experts in
+// fp32, top-k with exact ties to the lower expert index, optional slot-sum
+// renormalisation.
+//
+// Reference: components/moe/moe_ffn_block.mlir:50-128 (transpose + matmul,
+// linalg.softmax dimension(0), iree_linalg_ext.topk with `ogt`, scf.if
+// renormalisation); oracles/moe.py:86-105.
+//
+// One block handles kTok = 16 tokens.  Logits for those tokens land in LDS,
+// then each wave runs softmax + top-k for 4 of the tokens with the expert
+// axis spread over its 64 lanes.
+#include "common.h"
+#include "launch.h"
+
+namespace fmoe {
+namespace {
+
+constexpr int kTok = 16;
+constexpr int kThreads = 256;
+constexpr int kMaxExpert = 256;    // lanes hold up to 4 experts each
+constexpr int kMfmaMaxExpert = 128;
+
+// Softmax + top-k + optional renormalisation of kTok tokens whose logits
+// are in lds_logits[kTok][ld].
+__device__ void softmax_topk(const float* lds_logits, int ld, int tok0, int n_tokens,
+                             int n_expert, int k, bool normalize, int* ids, float* weights) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  for (int tt = wave; tt < kTok; tt += kThreads / kWave) {
+    const int t = tok0 + tt;
+    if (t >= n_tokens) break;
+    float p[4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + i * kWave;
+      p[i] = e < n_expert ? lds_logits[tt * ld + e] : -INFINITY;
+      m = fmaxf(m, p[i]);
+    }
+    m = wave_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + i * kWave;
+      p[i] = e < n_expert ? expf(p[i] - m) : 0.f;
+      s += p[i];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + i * kWave;
+      p[i] = e < n_expert ? p[i] / s : -1.f;  // -1 marks "not selectable"
+    }
+    // Lane `slot` keeps the slot's expert and probability.
+    float my_w = 0.f;
+    int my_id = 0;
+    for (int slot = 0; slot < k; ++slot) {
+      // lane-local best: larger value, then lower index (i ascending -> e ascending)
+      float bv = -1.f;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (p[i] > bv) {
+          bv = p[i];
+          bi = lane + i * kWave;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, kWave);
+        const int oi = __shfl_xor(bi, o, kWave);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (lane + i * kWave == bi) p[i] = -1.f;
+      if (lane == slot) {
+        my_w = bv;
+        my_id = bi;
+      }
+    }
+    if (normalize) {
+      // Sum in slot order (the linalg reduction of moe_ffn_block.mlir:97-107).
+      float wsum = 0.f;
+      for (int slot = 0; slot < k; ++slot) wsum += __shfl(my_w, slot, kWave);
+      my_w = my_w / wsum;
+    }
+    if (lane < k) {
+      ids[static_cast<int64_t>(lane) * n_tokens + t] = my_id;
+      weights[static_cast<int64_t>(lane) * n_tokens + t] = my_w;
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float ld_f32(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float ld_f32<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float ld_f32<bf16_t>(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+
+// SIMT logits: any n_embd, any dtype.  Thread pairs (token, expert) walk
+// the hidden axis in order.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void router_simt_kernel(
+    const T* __restrict__ x, const T* __restrict__ wr, int n_tokens, int n_embd,
+    int n_expert, int k, int normalize, int* __restrict__ ids, float* __restrict__ weights) {
+  extern __shared__ float lds[];
+  const int ld = n_expert + 1;
+  const int tok0 = blockIdx.x * kTok;
+  for (int idx = threadIdx.x; idx < kTok * n_expert; idx += kThreads) {
+    const int tt = idx / n_expert;
+    const int e = idx - tt * n_expert;
+    const int t = tok0 + tt;
+    float acc = 0.f;
+    if (t < n_tokens) {
+      const T* xr = x + static_cast<int64_t>(t) * n_embd;
+      const T* wrr = wr + static_cast<int64_t>(e) * n_embd;
+      for (int h = 0; h < n_embd; ++h) acc = fmaf(ld_f32(wrr, h), ld_f32(xr, h), acc);
+    }
+    lds[tt * ld + e] = acc;
+  }
+  __syncthreads();
+  softmax_topk(lds, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights);
+}
+
+// MFMA logits for bf16 inputs, n_embd % 128 == 0, n_expert <= 128.
+// v_mfma_f32_16x16x32_bf16 with A = 16 tokens x 32 hidden, B = 32 hidden x
+// 16 experts; the 4 waves split the hidden axis (wave w takes chunks
+// w, w+4, ...) and their partial logits are summed in wave order in LDS.
+__global__ __launch_bounds__(kThreads) void router_mfma_bf16_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, int n_tokens, int n_embd,
+    int n_expert, int k, int normalize, int* __restrict__ ids, float* __restrict__ weights) {
+  __shared__ float part[4][kTok][kMfmaMaxExpert + 4];
+  __shared__ float logits[kTok][kMfmaMaxExpert + 1];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int tok0 = blockIdx.x * kTok;
+  const int n_chunks = (n_expert + 15) / 16;
+
+  f32x4_t acc[kMfmaMaxExpert / 16];
+#pragma unroll
+  for (int c = 0; c < kMfmaMaxExpert / 16; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int row = lane & 15;         // token (A) / expert-in-chunk (B)
+  const int kofs = (lane >> 4) * 8;  // 8 consecutive hidden elements
+  const int t = tok0 + row;
+  const bool t_ok = t < n_tokens;
+  const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t_ok ? t : 0) * n_embd + kofs);
+  for (int h0 = wave * 32; h0 < n_embd; h0 += 4 * 32) {
+    uint4 av = t_ok ? xrow[h0 / 8] : uint4{0, 0, 0, 0};
+    const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+#pragma unroll
+    for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
+      if (c < n_chunks) {
+        const int e = c * 16 + row;
+        uint4 bv = uint4{0, 0, 0, 0};
+        if (e < n_expert)
+          bv = *reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(e) * n_embd + h0 + kofs);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv), acc[c], 0, 0, 0);
+      }
+    }
+  }
+  // D[token][expert]: lane holds expert (lane & 15), tokens 4*(lane>>4)+i.
+#pragma unroll
+  for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
+    if (c < n_chunks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[wave][(lane >> 4) * 4 + i][c * 16 + (lane & 15)] = acc[c][i];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < kTok * n_expert; idx += kThreads) {
+    const int tt = idx / n_expert;
+    const int e = idx - tt * n_expert;
+    logits[tt][e] = ((part[0][tt][e] + part[1][tt][e]) + part[2][tt][e]) + part[3][tt][e];
+  }
+  __syncthreads();
+  softmax_topk(&logits[0][0], kMfmaMaxExpert + 1, tok0, n_tokens, n_expert, k, normalize != 0, ids,
+               weights);
+}
+
+}  // namespace
+
+hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert,
+                         int k, bool normalize, int dtype, int* ids, float* weights,
+                         hipStream_t stream) {
+  if (n_tokens == 0) return hipSuccess;
+  if (n_expert > kMaxExpert) return hipErrorInvalidValue;
+  const dim3 grid((n_tokens + kTok - 1) / kTok);
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(wr) % 16 == 0);
+  if (dtype == DT_BF16 && n_embd % 128 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
+    hipLaunchKernelGGL(router_mfma_bf16_kernel, grid, dim3(kThreads), 0, stream,
+                       static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens,
+                       n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
+  } else {
+    const size_t lds = static_cast<size_t>(kTok) * (n_expert + 1) * sizeof(float);
+    if (dtype == DT_BF16) {
+      hipLaunchKernelGGL(router_simt_kernel<bf16_t>, grid, dim3(kThreads), lds, stream,
+                         static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens,
+                         n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
+    } else {
+      hipLaunchKernelGGL(router_simt_kernel<float>, grid, dim3(kThreads), lds, stream,
+                         static_cast<const float*>(x), static_cast<const float*>(wr), n_tokens,
+                         n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
+    }
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fmoe

@@ -1,0 +1,188 @@
+/*
+ * fmoe.h -- C ABI of the MI355X (gfx950) MoE FFN hot path.
+ *
+ * Drop-in for the reference's MoE FFN functions (stellaraccident/frank-models):
+ *   moe_ffn_block  components/moe/moe_ffn_block.mlir:34-209, oracles/moe.py:51-132
+ *   mul_mat_id     components/moe/mul_mat_id.mlir:22-120,   oracles/moe.py:9-48
+ *   swiglu         components/activation/swiglu.mlir:16-51, oracles/activation.py:11-21
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated otherwise; every call is
+ *     asynchronous on `stream` (a hipStream_t; NULL = the null stream) unless
+ *     stated otherwise.
+ *   - Tensor layouts are the reference's, row-major (C-contiguous):
+ *       input  [n_tokens, n_embd]                 (moe_ffn_block.mlir:35)
+ *       router [n_expert, n_embd]                 (moe_ffn_block.mlir:36)
+ *       up/gate expert weights [n_ff, n_embd, n_expert]  (moe_ffn_block.mlir:37-38)
+ *       down expert weights    [n_embd, n_ff, n_expert]  (moe_ffn_block.mlir:39)
+ *       ids / routing weights  [n_expert_used, n_tokens] (moe_ffn_block.mlir:78-81)
+ *     Expert weights are packed once (fmoe_pack_expert_weights) into the
+ *     per-expert layout the kernels read; the block and mul_mat_id take the
+ *     packed form.
+ *   - The caller owns every buffer, including the workspace; the library
+ *     never allocates or frees device memory.
+ *   - Functions return an fmoe_status; on failure fmoe_last_error() gives a
+ *     thread-local message.  No C++ exception crosses this boundary.
+ */
+#ifndef FMOE_H_
+#define FMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fmoe_status {
+  FMOE_OK = 0,
+  FMOE_ERR_INVALID_ARGUMENT = 1, /* null / misaligned pointer, bad flag */
+  FMOE_ERR_SHAPE = 2,            /* a dimension out of range */
+  FMOE_ERR_DTYPE = 3,            /* unsupported dtype or dtype combination */
+  FMOE_ERR_IDS_RANGE = 4,        /* an expert id outside [0, n_expert) */
+  FMOE_ERR_NO_DEVICE = 5,        /* no usable gfx950 device */
+  FMOE_ERR_HIP = 6,              /* a HIP runtime call or launch failed */
+  FMOE_ERR_WORKSPACE = 7         /* workspace missing or too small */
+} fmoe_status;
+
+typedef enum fmoe_dtype {
+  FMOE_F32 = 0,      /* IEEE binary32 */
+  FMOE_BF16 = 1,     /* bfloat16 */
+  FMOE_F8E4M3FN = 2  /* OCP FP8 E4M3 (finite, NaN = 0x7F/0xFF), weights only,
+                        with float32 per-output-channel scales [n_expert, n_out] */
+} fmoe_dtype;
+
+/* Kernel-path override for tests and tuning (process-wide; default AUTO). */
+typedef enum fmoe_gemm_path {
+  FMOE_PATH_AUTO = 0,
+  FMOE_PATH_GENERIC = 1, /* SIMT grouped GEMM, any shape and dtype */
+  FMOE_PATH_TILED = 2,   /* MFMA tiled grouped GEMM (prefill-sized batches) */
+  FMOE_PATH_STREAM = 3   /* MFMA weight-streaming grouped GEMM (decode) */
+} fmoe_gemm_path;
+
+/* Message describing the last failure on this thread ("" if none). */
+const char *fmoe_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int fmoe_abi_version(void);
+#define FMOE_ABI_VERSION 1
+
+/* Checks that the current HIP device is a gfx950; writes its ordinal and
+ * architecture name (arch may be NULL).  FMOE_ERR_NO_DEVICE otherwise. */
+int fmoe_device_check(int *device, char *arch, size_t arch_len);
+
+/* Selects the grouped-GEMM kernel family (fmoe_gemm_path).  A forced family
+ * that cannot run a given GEMM (dtype, shape, alignment) falls back to the
+ * AUTO choice for that GEMM. */
+int fmoe_set_gemm_path(int path);
+int fmoe_get_gemm_path(void);
+/* The family used by the last grouped GEMM launched on this thread. */
+int fmoe_last_gemm_path(void);
+
+/* ---------------------------------------------------------------------- */
+/* SwiGLU: out[i] = gate[i] * up[i] / (1 + exp(-up[i])), silu on `up`.
+ * Replaces @activation_components.swiglu (components/activation/swiglu.mlir:16-51,
+ * oracles/activation.py:11-21).  dtype FMOE_F32 or FMOE_BF16 for all three. */
+int fmoe_swiglu(const void *gate, const void *up, void *out, int64_t n, int dtype,
+                void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Router: logits = gate_inp_w @ input^T, fp32 softmax over experts, top-k
+ * (descending, exact ties to the lower expert index), optional
+ * renormalisation by the slot sum.  Replaces steps 1-4 of @moe_ffn_block
+ * (moe_ffn_block.mlir:50-128; oracles/moe.py:86-105).
+ *   input [n_tokens, n_embd], w_router [n_expert, n_embd] in `dtype`
+ *   ids_out [k, n_tokens] int32, weights_out [k, n_tokens] float32 */
+int fmoe_router(const void *input, const void *w_router, int64_t n_tokens,
+                int64_t n_embd, int64_t n_expert, int64_t n_expert_used,
+                int normalize_weights, int dtype, int32_t *ids_out,
+                float *weights_out, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Token->expert permutation of the slot-major flat assignment order
+ * f = s*n_tokens + t (the order of `collapse_shape ids [[0,1]]`,
+ * mul_mat_id.mlir:50-61), grouped by expert and stable:
+ *   offsets_out[e] = #assignments to experts < e  (n_expert+1 entries)
+ *   order_out[offsets_out[e] + r] = r-th smallest f with ids_flat[f] == e.
+ * Ids outside [0, n_expert) are left out and counted in the workspace error
+ * word (fmoe_workspace_error_count).  Workspace: fmoe_permute_workspace_bytes. */
+size_t fmoe_permute_workspace_bytes(int64_t n_expert_used, int64_t n_tokens,
+                                    int64_t n_expert);
+int fmoe_permute(const int32_t *ids, int64_t n_expert_used, int64_t n_tokens,
+                 int64_t n_expert, int32_t *order_out, int32_t *offsets_out,
+                 void *workspace, size_t workspace_bytes, void *stream);
+
+/* Number of invalid expert ids seen by the last call that used this
+ * workspace (synchronises `stream`).  Applies to fmoe_permute and
+ * fmoe_mul_mat_id workspaces. */
+int fmoe_workspace_error_count(const void *workspace, void *stream,
+                               int64_t *count_out);
+
+/* ---------------------------------------------------------------------- */
+/* One-time expert-weight packing.  Replaces the per-call transpose
+ * [n_out, n_in, E] -> [E, n_out, n_in] of mul_mat_id.mlir:37-48.
+ *   src [n_out, n_in, n_expert] in src_dtype (F32, BF16, or F8E4M3FN codes)
+ *   src_scales [n_out, n_expert] float32: required iff src_dtype == F8E4M3FN
+ *   dst: fmoe_packed_weight_bytes(n_out, n_in, n_expert, dst_dtype) bytes,
+ *        per-expert [n_out, n_in] rows, n_in contiguous, in dst_dtype
+ *   dst_scales [n_expert, n_out] float32: required iff dst_dtype == F8E4M3FN.
+ * F32/BF16 -> F8E4M3FN quantises each output channel with
+ * scale = absmax/448 (1 for an all-zero channel), code = RNE(w/scale),
+ * saturating at +-448. */
+size_t fmoe_packed_weight_bytes(int64_t n_out, int64_t n_in, int64_t n_expert,
+                                int dtype);
+int fmoe_pack_expert_weights(const void *src, int src_dtype, const float *src_scales,
+                             int64_t n_out, int64_t n_in, int64_t n_expert,
+                             int dst_dtype, void *dst, float *dst_scales,
+                             void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Expert-selected matmul out[:, s, t] = W[:, :, ids[s, t]] @ input[:, s, t].
+ * Replaces @moe_components.mul_mat_id (mul_mat_id.mlir:22-120,
+ * oracles/moe.py:9-48).
+ *   packed_w / w_scales / w_dtype: from fmoe_pack_expert_weights
+ *   input [n_in, k, n_tokens], out [n_out, k, n_tokens] in act_dtype
+ *   ids [k, n_tokens] int32.  Output columns of an invalid id are zero. */
+size_t fmoe_mul_mat_id_workspace_bytes(int64_t n_out, int64_t n_in, int64_t n_expert,
+                                       int64_t n_expert_used, int64_t n_tokens,
+                                       int act_dtype);
+int fmoe_mul_mat_id(const void *packed_w, const float *w_scales, int w_dtype,
+                    const void *input, const int32_t *ids, void *out, int64_t n_out,
+                    int64_t n_in, int64_t n_expert, int64_t n_expert_used,
+                    int64_t n_tokens, int act_dtype, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Full MoE FFN block.  Replaces @moe_ffn_components.moe_ffn_block
+ * (moe_ffn_block.mlir:34-209, oracles/moe.py:51-132), same argument meaning:
+ *   input [n_tokens, n_embd], w_router [n_expert, n_embd], out [n_tokens, n_embd]
+ *   all in act_dtype (F32 or BF16);
+ *   packed_up / packed_gate ([n_ff, n_embd] per expert) and packed_down
+ *   ([n_embd, n_ff] per expert) in w_dtype, with scales when w_dtype is
+ *   F8E4M3FN.  SwiGLU is gate * silu(up).  Weighted expert outputs are summed
+ *   in slot order.  Workspace: fmoe_moe_ffn_block_workspace_bytes. */
+size_t fmoe_moe_ffn_block_workspace_bytes(int64_t n_tokens, int64_t n_expert,
+                                          int64_t n_expert_used, int64_t n_embd,
+                                          int64_t n_ff, int act_dtype, int w_dtype);
+int fmoe_moe_ffn_block(const void *input, const void *w_router, const void *packed_up,
+                       const void *packed_gate, const void *packed_down,
+                       const float *up_scales, const float *gate_scales,
+                       const float *down_scales, int w_dtype, void *out,
+                       int64_t n_tokens, int64_t n_expert, int64_t n_expert_used,
+                       int64_t n_embd, int64_t n_ff, int normalize_weights,
+                       int act_dtype, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
+/* Views into a block workspace after fmoe_moe_ffn_block on it: the routing it
+ * computed (ids/weights [k, n_tokens]), the permutation (order [k*n_tokens],
+ * offsets [n_expert+1]).  Pointers are device pointers inside `workspace`. */
+int fmoe_moe_ffn_block_routing(void *workspace, int64_t n_tokens, int64_t n_expert,
+                               int64_t n_expert_used, int64_t n_embd, int64_t n_ff,
+                               int act_dtype, int w_dtype, int32_t **ids,
+                               float **weights, int32_t **order, int32_t **offsets);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FMOE_H_ */

@@ -1,0 +1,143 @@
+"""The C ABI boundary, checked without a GPU: the library loads, exports
+every symbol include/fmoe.h declares, and turns bad arguments into status
+codes (never a crash) before it touches a device."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fmoe.h"
+
+NO_GPU = not torch.cuda.is_available()
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(fmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_drop_in_entry_points():
+    names = declared_functions()
+    for required in ("fmoe_moe_ffn_block", "fmoe_mul_mat_id", "fmoe_swiglu", "fmoe_router",
+                     "fmoe_permute", "fmoe_pack_expert_weights"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(fm):
+    lib = fm.lowlevel.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding types every one of them
+    assert set(declared_functions()) == set(fm.lowlevel.SIGNATURES)
+
+
+def test_abi_version(fm):
+    assert fm.lowlevel.lib().fmoe_abi_version() == 1
+
+
+def test_single_hip_runtime(fm):
+    # libfmoe binds to the runtime torch loaded (one libamdhip64 mapping)
+    assert len(fm.hip_runtimes_loaded()) == 1, fm.hip_runtimes_loaded()
+
+
+def st(fm, name, *args):
+    return getattr(fm.lowlevel.lib(), name)(*args)
+
+
+def test_argument_errors_before_device(fm):
+    ll = fm.lowlevel
+    # bad dtype
+    assert st(fm, "fmoe_swiglu", None, None, None, 4, 9, None) == ll.ERR_DTYPE
+    # bad shapes: n_expert 0, k > E, too many experts
+    assert st(fm, "fmoe_router", None, None, 4, 8, 0, 1, 0, ll.F32, None, None, None) == ll.ERR_SHAPE
+    assert st(fm, "fmoe_router", None, None, 4, 8, 4, 5, 0, ll.F32, None, None, None) == ll.ERR_SHAPE
+    assert st(fm, "fmoe_router", None, None, 4, 8, 300, 2, 0, ll.F32, None, None, None) == ll.ERR_SHAPE
+    assert "n_expert" in ll.last_error()
+    # bad flag
+    assert st(fm, "fmoe_router", None, None, 4, 8, 4, 2, 2, ll.F32, None, None, None) == ll.ERR_INVALID_ARGUMENT
+    # null pointers with valid shapes
+    assert st(fm, "fmoe_router", None, None, 4, 8, 4, 2, 0, ll.F32, None, None, None) == ll.ERR_INVALID_ARGUMENT
+    # fp8 activations are not a thing
+    assert st(fm, "fmoe_moe_ffn_block", None, None, None, None, None, None, None, None, ll.F8E4M3FN,
+              None, 4, 4, 2, 8, 16, 0, ll.F8E4M3FN, None, 0, None) == ll.ERR_DTYPE
+    # f32 activations with bf16 weights
+    assert st(fm, "fmoe_moe_ffn_block", None, None, None, None, None, None, None, None, ll.BF16,
+              None, 4, 4, 2, 8, 16, 0, ll.F32, None, 0, None) == ll.ERR_DTYPE
+    # packing fp8 into bf16
+    assert st(fm, "fmoe_pack_expert_weights", None, ll.F8E4M3FN, None, 4, 4, 2, ll.BF16, None, None,
+              None) == ll.ERR_DTYPE
+    # unknown GEMM path
+    assert st(fm, "fmoe_set_gemm_path", 17) == ll.ERR_INVALID_ARGUMENT
+    assert st(fm, "fmoe_get_gemm_path") == ll.PATH_AUTO
+
+
+def test_workspace_too_small_is_reported(fm):
+    ll = fm.lowlevel
+    need = ll.lib().fmoe_moe_ffn_block_workspace_bytes(16, 8, 2, 64, 128, ll.BF16, ll.BF16)
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    r = st(fm, "fmoe_moe_ffn_block", fake, fake, fake, fake, fake, None, None, None, ll.BF16, fake,
+           16, 8, 2, 64, 128, 0, ll.BF16, fake, need - 1, None)
+    assert r == ll.ERR_WORKSPACE
+
+
+def test_empty_batch_is_a_no_op(fm):
+    ll = fm.lowlevel
+    # n_tokens = 0 returns OK without touching pointers or the device
+    assert st(fm, "fmoe_moe_ffn_block", None, None, None, None, None, None, None, None, ll.F32,
+              None, 0, 4, 2, 8, 16, 0, ll.F32, None, 0, None) == ll.OK
+    assert st(fm, "fmoe_router", None, None, 0, 8, 4, 2, 0, ll.F32, None, None, None) == ll.OK
+
+
+def test_workspace_sizes(fm):
+    lib = fm.lowlevel.lib()
+    ll = fm.lowlevel
+    a = lib.fmoe_moe_ffn_block_workspace_bytes(16, 8, 2, 4096, 14336, ll.BF16, ll.BF16)
+    b = lib.fmoe_moe_ffn_block_workspace_bytes(4096, 8, 2, 4096, 14336, ll.BF16, ll.BF16)
+    assert 0 < a < b
+    assert b % 256 == 0
+    assert lib.fmoe_moe_ffn_block_workspace_bytes(16, 8, 2, 4096, 14336, 9, ll.BF16) == 0
+    assert lib.fmoe_packed_weight_bytes(14336, 4096, 8, ll.BF16) == 14336 * 4096 * 8 * 2
+    assert lib.fmoe_packed_weight_bytes(14336, 4096, 8, ll.F8E4M3FN) == 14336 * 4096 * 8
+    assert lib.fmoe_mul_mat_id_workspace_bytes(64, 32, 8, 2, 16, ll.F32) > 0
+
+
+@pytest.mark.skipif(not NO_GPU, reason="checks the no-device path")
+def test_no_device_is_an_error_not_a_crash(fm):
+    ll = fm.lowlevel
+    fake = ctypes.c_void_p(0x1000)  # validation passes; the device check must fail before any launch
+    r = st(fm, "fmoe_router", fake, fake, 4, 8, 4, 2, 0, ll.F32, fake, fake, None)
+    assert r == ll.ERR_NO_DEVICE
+    d = ctypes.c_int(-1)
+    assert st(fm, "fmoe_device_check", ctypes.byref(d), None, 0) == ll.ERR_NO_DEVICE
+
+
+def test_python_api_errors_without_device(fm):
+    x = np.zeros((4, 8), np.float32)
+    w3 = np.zeros((16, 8, 4), np.float32)
+    wd = np.zeros((8, 16, 4), np.float32)
+    wr = np.zeros((4, 8), np.float32)
+    with pytest.raises(TypeError):
+        fm.moe_ffn_block(x.astype(np.float64), wr, w3, w3, wd, 4, 2, 8, 16, False)
+    with pytest.raises(ValueError):
+        fm.moe_ffn_block(x, wr, w3, w3, wd, 4, 2, 9, 16, False)  # n_embd mismatch
+    with pytest.raises(ValueError):
+        fm.moe_ffn_block(x, wr, w3, w3, wd, 4, 5, 8, 16, False)  # k > E
+    with pytest.raises(IndexError):
+        fm.mul_mat_id(np.zeros((4, 3, 8), np.float32), np.zeros((3, 1, 2), np.float32),
+                      np.array([[0, 8]], np.int32))
+    with pytest.raises(IndexError):
+        fm.mul_mat_id(np.zeros((4, 3, 8), np.float32), np.zeros((3, 1, 2), np.float32),
+                      np.array([[-1, 0]], np.int32))
+    with pytest.raises(ValueError):
+        fm.mul_mat_id(np.zeros((4, 3, 8), np.float32), np.zeros((3, 2, 2), np.float32),
+                      np.array([[0, 1]], np.int32))
+    with pytest.raises(TypeError):
+        fm.mul_mat_id(np.zeros((4, 3, 8), np.float32), np.zeros((3, 1, 2), np.float32),
+                      np.array([[0.0, 1.0]]))
+    with pytest.raises(ValueError):
+        fm.swiglu(np.zeros((2, 3), np.float32), np.zeros((3, 2), np.float32))

@@ -1,0 +1,186 @@
+"""moe_ffn_block on the GPU vs the oracle on the configurations C1-C5.
+
+* Routing ids and permutation offsets/order computed inside the block are
+  compared bit-exactly with the oracle's.
+* Outputs: fp32 rtol 1e-4; bf16 rtol 2e-2; fp8 5e-2 against the oracle on
+  the dequantised weights; atol = rtol * RMS(reference) (helpers.assert_close_rms).
+* At full Mixtral size (T=4096) the oracle runs on a seeded sample of
+  tokens: tokens route and mix independently (moe_ffn_block.mlir:21), so the
+  sampled rows of the full-batch output must equal the oracle on those rows.
+* Every kernel family (generic SIMT, MFMA tiled, MFMA streaming) that can run
+  a case is checked on it.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from oracle import numerics as nm
+from helpers import assert_close_rms
+
+pytestmark = pytest.mark.gpu
+
+PATHS = ["auto", "generic", "tiled", "stream"]
+
+
+def _set_path(ll, name):
+    code = {"auto": ll.PATH_AUTO, "generic": ll.PATH_GENERIC, "tiled": ll.PATH_TILED, "stream": ll.PATH_STREAM}[name]
+    ll.check(ll.lib().fmoe_set_gemm_path(code))
+
+
+class Case:
+    """Inputs of one configuration at one token count, on device and host."""
+
+    def __init__(self, fm, wl, cfg, T, seed=None):
+        self.cfg, self.T = cfg, T
+        x, wr, _ = wl.router_inputs(cfg, T, seed=seed)
+        act = torch.bfloat16 if cfg.act == "bf16" else torch.float32
+        self.x_np, self.wr_np = x, wr
+        self.x = torch.from_numpy(x).to("cuda", act)
+        self.wr = torch.from_numpy(wr).to("cuda", act)
+        up, gate, down = wl.expert_weights(cfg, "cuda", dtype=torch.float32 if cfg.act == "f32" else torch.bfloat16)
+        self.dev_w = (up, gate, down)
+        if cfg.weights == "fp8":
+            self.packed = [fm.quantize_expert_weights(w) for w in (up, gate, down)]
+            host = []
+            for w in (up, gate, down):
+                q, s = nm.quantize_per_channel_e4m3fn(w.float().cpu().numpy())
+                host.append(nm.dequantize_e4m3fn(q, s))
+            self.host_w = host
+        else:
+            self.packed = [fm.pack_expert_weights(w) for w in (up, gate, down)]
+            self.host_w = [w.float().cpu().numpy() for w in (up, gate, down)]
+        self.block = fm.MoEFFNBlock(self.wr, *self.packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd,
+                                    cfg.n_ff, cfg.normalize, act_dtype=act)
+
+    def run(self):
+        out = self.block(self.x)
+        torch.cuda.synchronize()
+        return out.float().cpu().numpy()
+
+    def oracle(self, tokens=None, dtype=np.float64):
+        c = self.cfg
+        x = self.x_np if tokens is None else self.x_np[tokens]
+        return om.moe_ffn_block(x, self.wr_np, *self.host_w, c.n_expert, c.n_expert_used, c.n_embd, c.n_ff,
+                                c.normalize, dtype=dtype, return_routing=True)
+
+
+def _check_routing(case, ref_ids):
+    ids, w, order, offsets = case.block.routing(case.T)
+    ids = ids.cpu().numpy()
+    np.testing.assert_array_equal(ids, ref_ids)
+    ro, roff = om.permute(ref_ids, case.cfg.n_expert)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), roff)
+    np.testing.assert_array_equal(order.cpu().numpy(), ro)
+
+
+def _scaled(wl, name, H, F, **kw):
+    return wl.scaled(wl.CONFIGS[name], H, F, **kw)
+
+
+# ------------------------------------------------------------------ C1 (fp32, full size)
+def test_c1_toy_fp32(fm, wl, gemm_path):
+    case = Case(fm, wl, wl.CONFIGS["C1"], 32)
+    ref, ids, _ = case.oracle()
+    for p in PATHS:
+        _set_path(gemm_path, p)
+        out = case.run()
+        _check_routing(case, ids)
+        np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-4 * np.sqrt(np.mean(ref**2)), err_msg=p)
+
+
+# ------------------------------------------------------------------ scaled-down bf16 shapes, all paths
+SMALL = [
+    ("C2", 256, 512, 16), ("C2", 256, 512, 300), ("C3", 128, 256, 64), ("C3", 128, 192, 700),
+    ("C4", 256, 384, 1), ("C4", 256, 384, 64), ("C5", 256, 512, 16), ("C5", 256, 512, 300),
+]
+
+
+@pytest.mark.parametrize("name,H,F,T", SMALL)
+def test_scaled_configs_all_paths(fm, wl, gemm_path, name, H, F, T):
+    cfg = _scaled(wl, name, H, F)
+    case = Case(fm, wl, cfg, T)
+    ref, ids, _ = case.oracle()
+    outs = {}
+    for p in PATHS:
+        _set_path(gemm_path, p)
+        outs[p] = case.run()
+        _check_routing(case, ids)
+        assert_close_rms(outs[p], ref, cfg.rtol, what=f"{name} T={T} path={p}")
+
+
+@pytest.mark.parametrize("H,F,T", [(72, 40, 9), (200, 136, 33)])
+def test_unaligned_shapes_bf16(fm, wl, gemm_path, H, F, T):
+    """Hidden/ffn sizes no MFMA tile divides fall back to the generic kernel."""
+    cfg = _scaled(wl, "C4", H, F)
+    case = Case(fm, wl, cfg, T)
+    ref, ids, _ = case.oracle()
+    for p in PATHS:
+        _set_path(gemm_path, p)
+        out = case.run()
+        _check_routing(case, ids)
+        assert_close_rms(out, ref, cfg.rtol, what=f"path={p}")
+
+
+# ------------------------------------------------------------------ full-size configurations
+@pytest.mark.parametrize("name,T", [("C2", 16), ("C4", 1), ("C4", 4), ("C4", 16), ("C4", 64), ("C3", 64),
+                                    ("C5", 16)])
+def test_full_size_decode(fm, wl, name, T):
+    cfg = wl.CONFIGS[name]
+    case = Case(fm, wl, cfg, T)
+    out = case.run()
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} T={T}")
+
+
+@pytest.mark.parametrize("name,T,sample", [("C2", 512, None), ("C2", 4096, 256), ("C3", 2048, 256),
+                                           ("C3", 8192, 256), ("C5", 4096, 256)])
+def test_full_size_prefill(fm, wl, name, T, sample):
+    cfg = wl.CONFIGS[name]
+    case = Case(fm, wl, cfg, T)
+    out = case.run()
+    ids_dev, *_ = case.block.routing(T)
+    if sample is None:
+        ref, ids, _ = case.oracle(dtype=np.float32)
+        _check_routing(case, ids)
+        assert_close_rms(out, ref, cfg.rtol, what=f"{name} T={T}")
+    else:
+        tok = np.sort(np.random.default_rng(T).choice(T, size=sample, replace=False))
+        ref, ids, _ = case.oracle(tokens=tok, dtype=np.float32)
+        np.testing.assert_array_equal(ids_dev.cpu().numpy()[:, tok], ids)
+        assert_close_rms(out[tok], ref, cfg.rtol, what=f"{name} T={T} sampled")
+
+
+# ------------------------------------------------------------------ properties
+def test_deterministic_and_token_order_equivariant(fm, wl, gemm_path):
+    cfg = _scaled(wl, "C3", 256, 256)
+    case = Case(fm, wl, cfg, 500)
+    for p in PATHS:
+        _set_path(gemm_path, p)
+        a = case.run()
+        b = case.run()
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+        # Permuting the tokens permutes the output rows bit-exactly: a row's
+        # arithmetic does not depend on which other rows share its tile.
+        perm = np.random.default_rng(0).permutation(case.T)
+        x0 = case.x
+        case.x = x0[torch.from_numpy(perm).cuda()].contiguous()
+        c = case.run()
+        case.x = x0
+        np.testing.assert_array_equal(c.view(np.uint32), a[perm].view(np.uint32), err_msg=p)
+
+
+def test_numpy_drop_in_signature(fm, wl):
+    """The NumPy-in / NumPy-out call of oracles/moe.py:51-62 at C1."""
+    cfg = wl.CONFIGS["C1"]
+    x, wr, _ = wl.router_inputs(cfg, 32)
+    rng = np.random.default_rng(0)
+    up = (rng.standard_normal((128, 64, 8)) * 0.02).astype(np.float32)
+    gate = (rng.standard_normal((128, 64, 8)) * 0.02).astype(np.float32)
+    down = (rng.standard_normal((64, 128, 8)) * 0.02).astype(np.float32)
+    out = fm.moe_ffn_block(x, wr, up, gate, down, 8, 2, 64, 128, True)
+    ref = om.moe_ffn_block_literal(x, wr, up, gate, down, 8, 2, 64, 128, True)
+    assert isinstance(out, np.ndarray) and out.dtype == np.float32 and out.shape == (32, 64)
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-5)

@@ -1,0 +1,206 @@
+"""GPU parity of the path's components against the oracle: router (ids
+bit-exact), permutation (bit-exact), SwiGLU, packing (bf16 / fp8 bits),
+and the reference's own mul_mat_id / moe_ffn_block test cases at the
+reference's tolerance (rtol 1e-4, atol 1e-5)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import moe as om
+from oracle import numerics as nm
+from helpers import assert_close
+from test_oracle import BLOCK_REFERENCE_CASES, MMID_REFERENCE_CASES, REFERENCE_IDS, _mmid_case, block_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_is_gfx950(fm):
+    import ctypes
+
+    d = ctypes.c_int(-1)
+    buf = ctypes.create_string_buffer(64)
+    fm.lowlevel.check(fm.lowlevel.lib().fmoe_device_check(ctypes.byref(d), buf, 64))
+    assert buf.value.decode().startswith("gfx950")
+    assert len(fm.hip_runtimes_loaded()) == 1, fm.hip_runtimes_loaded()
+
+
+# ------------------------------------------------------------------ swiglu
+@pytest.mark.parametrize("seed,scale,kind", [(42, 1, "rand"), (0, 0, "zeros"), (123, 1, "pos"), (456, 10, "rand")])
+def test_swiglu_reference_cases(fm, seed, scale, kind):
+    """tests/components/test_swiglu.py:15-59."""
+    if kind == "zeros":
+        g = np.zeros((2, 4, 8), np.float32)
+        u = np.zeros((2, 4, 8), np.float32)
+    else:
+        np.random.seed(seed)
+        g = np.random.randn(2, 4, 8).astype(np.float32) * scale
+        u = np.random.randn(2, 4, 8).astype(np.float32) * scale
+        if kind == "pos":
+            g, u = np.abs(g) + 0.1, np.abs(u) + 0.1
+    out = fm.swiglu(g, u)
+    tol = dict(rtol=1e-4, atol=1e-5) if scale == 10 else dict(rtol=1e-5, atol=1e-6)
+    assert_close(out, oracle.swiglu(g.astype(np.float64), u.astype(np.float64)), **tol)
+
+
+def test_swiglu_bf16(fm):
+    rng = np.random.default_rng(1)
+    g = torch.from_numpy(rng.standard_normal(10000).astype(np.float32)).to("cuda", torch.bfloat16)
+    u = torch.from_numpy(rng.standard_normal(10000).astype(np.float32) * 3).to("cuda", torch.bfloat16)
+    out = fm.swiglu(g, u).float().cpu().numpy()
+    ref = oracle.swiglu(g.float().cpu().numpy().astype(np.float64), u.float().cpu().numpy().astype(np.float64))
+    np.testing.assert_allclose(out, ref, rtol=2**-8, atol=1e-6)
+
+
+# ------------------------------------------------------------------ router
+def _router_check(fm, x, wr, k, norm, rtol_w=1e-5):
+    ids, w = fm.router(x, wr, k, norm)
+    rids, rw = om.router(x, wr, k, norm)
+    np.testing.assert_array_equal(ids, rids)
+    np.testing.assert_allclose(w, rw, rtol=rtol_w, atol=1e-7)
+
+
+@pytest.mark.parametrize("case", range(len(BLOCK_REFERENCE_CASES)))
+def test_router_reference_cases(fm, case):
+    seed, T, H, F, E, k, norm = BLOCK_REFERENCE_CASES[case]
+    x, wr, *_ = block_inputs(seed, T, H, F, E)
+    _router_check(fm, x, wr, k, norm)
+
+
+@pytest.mark.parametrize("cfg_name,T", [("C1", 32), ("C2", 16), ("C2", 512), ("C3", 64), ("C3", 2048),
+                                        ("C4", 1), ("C4", 64)])
+def test_router_configs(fm, wl, cfg_name, T):
+    cfg = wl.CONFIGS[cfg_name]
+    x, wr, _ = wl.router_inputs(cfg, T)
+    if cfg.act == "bf16":
+        xt = torch.from_numpy(x).to("cuda", torch.bfloat16)
+        wt = torch.from_numpy(wr).to("cuda", torch.bfloat16)
+        ids, w = fm.router(xt, wt, cfg.n_expert_used, cfg.normalize)
+        ids, w = ids.cpu().numpy(), w.cpu().numpy()
+        rids, rw = om.router(x, wr, cfg.n_expert_used, cfg.normalize)
+        np.testing.assert_array_equal(ids, rids)
+        np.testing.assert_allclose(w, rw, rtol=1e-5, atol=1e-7)
+    else:
+        _router_check(fm, x, wr, cfg.n_expert_used, cfg.normalize)
+
+
+def test_router_ties_lower_index(fm):
+    # identity inputs make the logits equal to the router columns exactly
+    logits = np.array([[1.0, 0.0, 5.0], [2.0, 0.0, 5.0], [2.0, 0.0, 5.0], [0.0, 0.0, 5.0]], np.float32)
+    x = np.eye(3, dtype=np.float32)
+    for dt in (torch.float32, torch.bfloat16):
+        # H = 3 (SIMT path) and a padded H = 128 (MFMA path for bf16)
+        for H in (3, 128):
+            xx = np.zeros((3, H), np.float32)
+            xx[:, :3] = x
+            wr = np.zeros((4, H), np.float32)
+            wr[:, :3] = logits
+            ids, w = fm.router(torch.from_numpy(xx).to("cuda", dt), torch.from_numpy(wr).to("cuda", dt), 2, False)
+            np.testing.assert_array_equal(ids.cpu().numpy(), [[1, 0, 0], [2, 1, 1]])
+
+
+def test_router_many_experts_and_k(fm):
+    # N(0,1) router weights give logits of std ~sqrt(H); their fp32
+    # accumulation error (~1e-5 absolute) is a relative error of the
+    # probabilities, so the weights are held to the reference's fp32 rtol 1e-4.
+    rng = np.random.default_rng(11)
+    for E, k, H in [(256, 8, 64), (128, 64, 128), (3, 3, 5)]:
+        x = rng.standard_normal((37, H)).astype(np.float32)
+        wr = rng.standard_normal((E, H)).astype(np.float32)
+        _router_check(fm, x, wr, k, True, rtol_w=1e-4)
+
+
+# ------------------------------------------------------------------ permutation
+@pytest.mark.parametrize("case", range(len(REFERENCE_IDS)))
+def test_permute_reference_ids(fm, case):
+    ids, E = REFERENCE_IDS[case]
+    order, offsets = fm.permute(ids, E)
+    ro, roff = om.permute(ids, E)
+    np.testing.assert_array_equal(order, ro)
+    np.testing.assert_array_equal(offsets, roff)
+
+
+@pytest.mark.parametrize("E,k,T,skew", [(8, 2, 4096, 0), (128, 8, 8192, 1.1), (64, 6, 64, 0),
+                                        (8, 2, 1, 0), (512, 1, 3000, 0), (4, 4, 1500, 0), (2, 1, 70000, 0)])
+def test_permute_random(fm, E, k, T, skew):
+    rng = np.random.default_rng(E * 7 + k + T)
+    if skew:
+        p = 1.0 / np.arange(1, E + 1) ** skew
+        p /= p.sum()
+        ids = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)], axis=1)
+    elif k <= E:
+        ids = np.argsort(rng.random((E, T)), axis=0)[:k]
+    ids = ids.astype(np.int32)
+    order, offsets = fm.permute(ids, E)
+    ro, roff = om.permute(ids, E)
+    np.testing.assert_array_equal(offsets, roff)
+    np.testing.assert_array_equal(order, ro)
+
+
+def test_permute_all_one_expert_and_empty(fm):
+    ids = np.full((2, 3000), 5, np.int32)
+    order, offsets = fm.permute(ids, 8)
+    ro, roff = om.permute(ids, 8)
+    np.testing.assert_array_equal(order, ro)
+    np.testing.assert_array_equal(offsets, roff)
+    order, offsets = fm.permute(np.zeros((2, 0), np.int32), 8)
+    assert order.size == 0 and np.all(offsets == 0)
+
+
+def test_permute_device_ids_out_of_range(fm):
+    ids = torch.tensor([[0, 9, 1], [2, -1, 3]], dtype=torch.int32, device="cuda")
+    with pytest.raises(IndexError):
+        fm.permute(ids, 8)
+
+
+# ------------------------------------------------------------------ packing
+def test_pack_bf16_bits(fm):
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((24, 40, 5)) * 0.02).astype(np.float32)
+    p = fm.pack_expert_weights(w, "bf16")
+    got = p.data.view(torch.int16).view(5, 24, 40).cpu().numpy().view(np.uint16)
+    ref = nm.bf16_bits(w).transpose(2, 0, 1)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_pack_fp8_codes_and_scales(fm):
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((24, 40, 5)) * 0.02).astype(np.float32)
+    w[3, :, 2] = 0.0
+    w[4, 7, 1] = 1e-9  # subnormal after scaling
+    p = fm.quantize_expert_weights(w)
+    q, s = nm.quantize_per_channel_e4m3fn(w)
+    got_q = p.data.view(5, 24, 40).cpu().numpy()
+    np.testing.assert_array_equal(got_q, q.transpose(2, 0, 1))
+    np.testing.assert_array_equal(p.scales.cpu().numpy(), s.T)
+
+
+def test_pack_prequantized(fm):
+    rng = np.random.default_rng(14)
+    w = (rng.standard_normal((8, 16, 3)) * 0.02).astype(np.float32)
+    q, s = nm.quantize_per_channel_e4m3fn(w)
+    p = fm.pack_expert_weights(fm.QuantizedExpertWeights(q, s))
+    np.testing.assert_array_equal(p.data.view(3, 8, 16).cpu().numpy(), q.transpose(2, 0, 1))
+    np.testing.assert_array_equal(p.scales.cpu().numpy(), s.T)
+
+
+# ------------------------------------------------------------------ reference cases, fp32
+@pytest.mark.parametrize("case", range(len(MMID_REFERENCE_CASES)))
+def test_mul_mat_id_reference_cases(fm, case):
+    """tests/components/test_mul_mat_id.py, same seeds/shapes/tolerance."""
+    w, x, ids = _mmid_case(*MMID_REFERENCE_CASES[case])
+    out = fm.mul_mat_id(w, x, ids)
+    assert out.shape == (w.shape[0], *ids.shape) and out.dtype == np.float32
+    assert_close(out, om.mul_mat_id_literal(w, x, ids), rtol=1e-4, atol=1e-5)
+    assert_close(out, om.mul_mat_id(w, x, ids), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("case", range(len(BLOCK_REFERENCE_CASES)))
+def test_moe_ffn_block_reference_cases(fm, case):
+    """tests/components/test_moe_ffn_block.py, same seeds/shapes/tolerance."""
+    seed, T, H, F, E, k, norm = BLOCK_REFERENCE_CASES[case]
+    x, wr, up, gate, down = block_inputs(seed, T, H, F, E)
+    out = fm.moe_ffn_block(x, wr, up, gate, down, E, k, H, F, norm)
+    assert out.shape == (T, H) and out.dtype == np.float32
+    assert_close(out, om.moe_ffn_block_literal(x, wr, up, gate, down, E, k, H, F, norm), rtol=1e-4, atol=1e-5)

@@ -1,0 +1,358 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Every oracle function is checked against something other than a retyped copy
+of its own formula: brute-force loops, closed forms in another form,
+invariants, special cases that reduce to textbook routines, torch's casts,
+and the reference's hand-written id arrays.  Each group also plants a
+plausible mistake in a copy of the oracle and shows the pin catches it.
+"""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import moe as om
+from oracle import numerics as nm
+
+
+# ------------------------------------------------------------------ swiglu
+def test_swiglu_known_answers():
+    g = np.array([0.0, 1.0, 1.0, 1.0, 2.0, -3.0], np.float64)
+    u = np.array([0.0, 0.0, 30.0, -30.0, 1.0, 2.0], np.float64)
+    out = oracle.swiglu(g, u)
+    assert out[0] == 0.0 and out[1] == 0.0  # u = 0 -> silu 0
+    assert abs(out[2] - 30.0) < 1e-9  # silu(30) ~ 30
+    assert abs(out[3]) < 1e-10  # silu(-30) ~ -30 e^-30
+    assert out[4] == pytest.approx(2.0 / (1.0 + math.exp(-1.0)))  # g * sigmoid(1) * 1
+    assert out[5] == pytest.approx(-3.0 * 2.0 / (1.0 + math.exp(-2.0)))
+
+
+def test_swiglu_matches_torch_silu():
+    rng = np.random.default_rng(0)
+    g = rng.standard_normal((3, 5, 7)) * 4
+    u = rng.standard_normal((3, 5, 7)) * 4
+    ref = (torch.nn.functional.silu(torch.from_numpy(u)) * torch.from_numpy(g)).numpy()
+    np.testing.assert_allclose(oracle.swiglu(g, u), ref, rtol=1e-12, atol=1e-14)
+
+
+def test_swiglu_operand_swap_is_caught():
+    """silu acts on `up` (swiglu.mlir:37-47): the HF/llama.cpp order would
+    fail the known-answer test."""
+    swapped = lambda g, u: u * om.silu(g)  # noqa: E731  (planted mistake)
+    g, u = np.array([1.0]), np.array([-30.0])
+    assert abs(oracle.swiglu(g, u)[0]) < 1e-10
+    assert abs(swapped(g, u)[0]) > 1.0
+
+
+# ------------------------------------------------------------------ router
+def _one_hot_router(logits_et):
+    """Input/router pair whose logits are exactly `logits_et` [E, T]:
+    x = identity rows (T = H), W_router = logits."""
+    E, T = logits_et.shape
+    return np.eye(T), np.asarray(logits_et, np.float64)
+
+
+def test_router_softmax_closed_form_and_invariants():
+    rng = np.random.default_rng(1)
+    logits = rng.standard_normal((8, 16)) * 3
+    x, wr = _one_hot_router(logits)
+    p = om.router_probs(x, wr)
+    # scipy's softmax is an independent restatement
+    from scipy.special import softmax
+
+    np.testing.assert_allclose(p, softmax(logits, axis=0), rtol=1e-13)
+    np.testing.assert_allclose(p.sum(axis=0), 1.0, rtol=1e-14)
+    # shift invariance: adding c to every logit of a token changes nothing
+    p2 = om.router_probs(x, wr + 5.0)
+    np.testing.assert_allclose(p, p2, rtol=1e-12)
+    # equal logits -> 1/E
+    x, wr = _one_hot_router(np.zeros((8, 3)))
+    np.testing.assert_allclose(om.router_probs(x, wr), 1.0 / 8)
+
+
+def _topk_brute(probs, k):
+    E, T = probs.shape
+    ids = np.zeros((k, T), np.int32)
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-probs[e, t], e))
+        ids[:, t] = order[:k]
+    return ids
+
+
+@pytest.mark.parametrize("E,k,T", [(4, 2, 5), (8, 2, 16), (8, 8, 3), (16, 6, 9), (5, 1, 7)])
+def test_router_topk_brute_force(E, k, T):
+    rng = np.random.default_rng(E * 100 + k)
+    x = rng.standard_normal((T, 12))
+    wr = rng.standard_normal((E, 12))
+    ids, w = om.router(x, wr, k, False)
+    p = om.router_probs(x, wr)
+    np.testing.assert_array_equal(ids, _topk_brute(p, k))
+    np.testing.assert_array_equal(w, np.take_along_axis(p, ids.astype(np.int64), axis=0))
+    assert np.all(np.diff(w, axis=0) <= 0)  # descending slots
+
+
+def test_router_ties_go_to_lower_index():
+    logits = np.array([[1.0, 0.0, 5.0], [2.0, 0.0, 5.0], [2.0, 0.0, 5.0], [0.0, 0.0, 5.0]])  # [E=4, T=3]
+    x, wr = _one_hot_router(logits)
+    ids, _ = om.router(x, wr, 2, False)
+    np.testing.assert_array_equal(ids[:, 0], [1, 2])  # 2.0 tie between experts 1, 2
+    np.testing.assert_array_equal(ids[:, 1], [0, 1])  # all equal
+    np.testing.assert_array_equal(ids[:, 2], [0, 1])
+    # planted mistake: ties to the higher index
+    p = om.router_probs(x, wr)
+    bad = (p.shape[0] - 1 - np.argsort(-p[::-1], axis=0, kind="stable"))[:2]
+    assert not np.array_equal(bad, ids)
+
+
+def test_router_renormalisation():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((20, 16))
+    wr = rng.standard_normal((8, 16))
+    ids, w = om.router(x, wr, 3, True)
+    np.testing.assert_allclose(w.sum(axis=0), 1.0, rtol=1e-14)
+    ids1, w1 = om.router(x, wr, 1, True)
+    assert np.all(w1 == 1.0)
+    ids0, w0 = om.router(x, wr, 3, False)
+    np.testing.assert_array_equal(ids, ids0)
+    np.testing.assert_allclose(w, w0 / w0.sum(axis=0), rtol=1e-15)
+
+
+# ------------------------------------------------------------------ permutation
+def _permute_brute(ids, E):
+    flat = [int(v) for v in np.asarray(ids).reshape(-1)]
+    order, offsets = [], [0]
+    for e in range(E):
+        order += [f for f, v in enumerate(flat) if v == e]
+        offsets.append(len(order))
+    return np.array(order, np.int32), np.array(offsets, np.int32)
+
+
+REFERENCE_IDS = [  # tests/components/test_mul_mat_id.py:23-25, :42-48, :64
+    (np.array([[0, 3]], np.int32), 8),
+    (np.array([[0, 1, 2, 3], [4, 5, 6, 7]], np.int32), 8),
+    (np.array([[2, 2, 2]], np.int32), 4),
+]
+
+
+@pytest.mark.parametrize("case", range(len(REFERENCE_IDS)))
+def test_permute_reference_ids(case):
+    ids, E = REFERENCE_IDS[case]
+    order, offsets = om.permute(ids, E)
+    bo, boff = _permute_brute(ids, E)
+    np.testing.assert_array_equal(order, bo)
+    np.testing.assert_array_equal(offsets, boff)
+
+
+def test_permute_known_answer():
+    ids = np.array([[0, 1, 2, 3], [4, 5, 6, 7]], np.int32)
+    order, offsets = om.permute(ids, 8)
+    np.testing.assert_array_equal(order, [0, 1, 2, 3, 4, 5, 6, 7])
+    ids = np.array([[2, 0, 2], [0, 1, 1]], np.int32)  # flat [2,0,2,0,1,1]
+    order, offsets = om.permute(ids, 3)
+    np.testing.assert_array_equal(order, [1, 3, 4, 5, 0, 2])
+    np.testing.assert_array_equal(offsets, [0, 2, 4, 6])
+
+
+@pytest.mark.parametrize("E,k,T", [(8, 2, 50), (64, 6, 33), (128, 8, 17), (3, 3, 1)])
+def test_permute_random_vs_brute(E, k, T):
+    rng = np.random.default_rng(E + k + T)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)], axis=1).astype(np.int32)
+    order, offsets = om.permute(ids, E)
+    bo, boff = _permute_brute(ids, E)
+    np.testing.assert_array_equal(order, bo)
+    np.testing.assert_array_equal(offsets, boff)
+    # planted mistake: an unstable sort is not the stable grouping
+    rng2 = np.random.default_rng(0)
+    shuffled = np.concatenate([rng2.permutation(bo[offsets[e]:offsets[e + 1]]) for e in range(E)])
+    if not np.array_equal(shuffled, bo):
+        assert not np.array_equal(shuffled, order)
+
+
+def test_permute_rejects_bad_ids():
+    with pytest.raises(ValueError):
+        om.permute(np.array([[0, 8]], np.int32), 8)
+    with pytest.raises(ValueError):
+        om.permute(np.array([[-1, 0]], np.int32), 8)
+
+
+# ------------------------------------------------------------------ mul_mat_id
+def _mmid_case(seed, n_out, n_in, E, k, T, ids=None):
+    np.random.seed(seed)
+    w = np.random.randn(n_out, n_in, E).astype(np.float32) * 0.1
+    x = np.random.randn(n_in, k, T).astype(np.float32) * 0.1
+    if ids is None:
+        ids = np.random.randint(0, E, size=(k, T), dtype=np.int32)
+    return w, x, ids
+
+
+# The reference's four mul_mat_id cases (tests/components/test_mul_mat_id.py).
+MMID_REFERENCE_CASES = [
+    (42, 4, 3, 8, 1, 2, np.array([[0, 3]], np.int32)),
+    (123, 8, 4, 8, 2, 4, np.array([[0, 1, 2, 3], [4, 5, 6, 7]], np.int32)),
+    (456, 6, 4, 4, 1, 3, np.array([[2, 2, 2]], np.int32)),
+    (789, 64, 32, 8, 2, 16, None),
+]
+
+
+@pytest.mark.parametrize("case", range(len(MMID_REFERENCE_CASES)))
+def test_mul_mat_id_three_forms_agree(case):
+    w, x, ids = _mmid_case(*MMID_REFERENCE_CASES[case])
+    loops = om.mul_mat_id_loops(w, x, ids)
+    lit = om.mul_mat_id_literal(w, x, ids)
+    grp = om.mul_mat_id(w, x, ids)
+    np.testing.assert_allclose(lit, loops, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(grp, loops, rtol=1e-12, atol=1e-14)
+    # planted mistake: the transposed weight operand is caught by the loops
+    if w.shape[0] == w.shape[1]:
+        bad = om.mul_mat_id(w.transpose(1, 0, 2), x, ids)
+        assert not np.allclose(bad, loops)
+
+
+def test_mul_mat_id_special_cases():
+    rng = np.random.default_rng(3)
+    E, k, T, n = 4, 2, 5, 6
+    # identity weights -> output equals input
+    w = np.repeat(np.eye(n)[:, :, None], E, axis=2)
+    x = rng.standard_normal((n, k, T))
+    ids = rng.integers(0, E, (k, T)).astype(np.int32)
+    np.testing.assert_allclose(om.mul_mat_id(w, x, ids), x, rtol=1e-15)
+    # all ids equal e -> dense GEMM with W[:, :, e]
+    w = rng.standard_normal((7, n, E))
+    ids = np.full((k, T), 2, np.int32)
+    dense = np.einsum("oi,ist->ost", w[:, :, 2], x)
+    np.testing.assert_allclose(om.mul_mat_id(w, x, ids), dense, rtol=1e-12)
+    # one-hot input e_j selects column j of the routed expert
+    x1 = np.zeros((n, 1, 1))
+    x1[3, 0, 0] = 1.0
+    out = om.mul_mat_id(w, x1, np.array([[1]], np.int32))
+    np.testing.assert_array_equal(out[:, 0, 0], w[:, 3, 1])
+
+
+# ------------------------------------------------------------------ moe_ffn_block
+# The reference's four block cases (tests/components/test_moe_ffn_block.py).
+BLOCK_REFERENCE_CASES = [
+    # seed, T, H, F, E, k, normalize
+    (42, 4, 8, 16, 4, 2, False),
+    (123, 3, 8, 12, 4, 2, True),
+    (456, 4, 8, 16, 8, 1, False),
+    (789, 8, 32, 64, 8, 2, False),
+]
+
+
+def block_inputs(seed, T, H, F, E):
+    np.random.seed(seed)
+    x = np.random.randn(T, H).astype(np.float32) * 0.1
+    wr = np.random.randn(E, H).astype(np.float32) * 0.1
+    up = np.random.randn(F, H, E).astype(np.float32) * 0.1
+    gate = np.random.randn(F, H, E).astype(np.float32) * 0.1
+    down = np.random.randn(H, F, E).astype(np.float32) * 0.1
+    return x, wr, up, gate, down
+
+
+@pytest.mark.parametrize("case", range(len(BLOCK_REFERENCE_CASES)))
+def test_block_grouped_equals_literal(case):
+    seed, T, H, F, E, k, norm = BLOCK_REFERENCE_CASES[case]
+    x, wr, up, gate, down = block_inputs(seed, T, H, F, E)
+    lit = om.moe_ffn_block_literal(x, wr, up, gate, down, E, k, H, F, norm)
+    lit64 = om.moe_ffn_block_literal(x, wr, up, gate, down, E, k, H, F, norm, dtype=np.float64)
+    grp = om.moe_ffn_block(x, wr, up, gate, down, E, k, H, F, norm)
+    np.testing.assert_allclose(lit64, grp, rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(lit, grp, rtol=1e-4, atol=1e-6)
+
+
+def test_block_single_expert_is_dense_swiglu_ffn():
+    rng = np.random.default_rng(5)
+    T, H, F = 6, 10, 14
+    x = rng.standard_normal((T, H))
+    up, gate, down = rng.standard_normal((F, H, 1)), rng.standard_normal((F, H, 1)), rng.standard_normal((H, F, 1))
+    wr = rng.standard_normal((1, H))
+    out = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False)
+    u = x @ up[:, :, 0].T
+    g = x @ gate[:, :, 0].T
+    h = g * (u * (1.0 / (1.0 + np.exp(-u))))  # sigmoid form of swiglu.mlir:40-45
+    np.testing.assert_allclose(out, h @ down[:, :, 0].T, rtol=1e-12)
+
+
+def test_block_identical_experts_normalized_is_dense():
+    rng = np.random.default_rng(6)
+    T, H, F, E, k = 9, 8, 12, 6, 3
+    x = rng.standard_normal((T, H))
+    wr = rng.standard_normal((E, H))
+    one_up, one_gate, one_down = rng.standard_normal((F, H)), rng.standard_normal((F, H)), rng.standard_normal((H, F))
+    up = np.repeat(one_up[:, :, None], E, axis=2)
+    gate = np.repeat(one_gate[:, :, None], E, axis=2)
+    down = np.repeat(one_down[:, :, None], E, axis=2)
+    dense = (x @ one_gate.T) * om.silu(x @ one_up.T) @ one_down.T
+    out = om.moe_ffn_block(x, wr, up, gate, down, E, k, H, F, True)
+    np.testing.assert_allclose(out, dense, rtol=1e-12, atol=1e-13)
+    # planted mistake: dropping the renormalisation scales the output by sum(w) < 1
+    unnorm = om.moe_ffn_block(x, wr, up, gate, down, E, k, H, F, False)
+    assert not np.allclose(unnorm, dense, rtol=1e-3)
+
+
+def test_block_token_independence():
+    rng = np.random.default_rng(7)
+    T, H, F, E, k = 12, 8, 16, 5, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    wr = rng.standard_normal((E, H)).astype(np.float32)
+    up, gate, down = (rng.standard_normal(s).astype(np.float32) for s in ((F, H, E), (F, H, E), (H, F, E)))
+    full = om.moe_ffn_block(x, wr, up, gate, down, E, k, H, F, False)
+    idx = np.array([11, 0, 5])
+    part = om.moe_ffn_block_tokens(idx, x, wr, up, gate, down, E, k, H, F, False)
+    np.testing.assert_allclose(part, full[idx], rtol=1e-12)
+
+
+# ------------------------------------------------------------------ numerics
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(8)
+    x = np.concatenate([
+        rng.standard_normal(50000).astype(np.float32) * 100,
+        np.array([0.0, -0.0, 1.0 + 2**-8, 1.0 + 3 * 2**-8, 3.3895314e38, np.inf, -np.inf], np.float32),
+    ])
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(nm.bf16_round(x).view(np.uint32), ref.view(np.uint32))
+    # ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> 1
+    assert nm.bf16_round(np.float32(1.0 + 2**-8)) == 1.0
+    assert nm.bf16_round(np.float32(1.0 + 3 * 2**-8)) == np.float32(1.0 + 2**-6)
+
+
+def test_e4m3fn_decode_table():
+    v = nm.E4M3FN_VALUES
+    assert v[0x7E] == 448.0 and v[0xFE] == -448.0
+    assert np.isnan(v[0x7F]) and np.isnan(v[0xFF])
+    assert v[0x01] == 2.0**-9 and v[0x08] == 2.0**-6 and v[0x38] == 1.0
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(nm.e4m3fn_decode(codes), ref)
+
+
+def test_e4m3fn_encode_matches_torch_and_saturates():
+    rng = np.random.default_rng(9)
+    mids = ((nm.E4M3FN_VALUES[:126] + nm.E4M3FN_VALUES[1:127]) / 2).astype(np.float32)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 50, mids, -mids,
+                        nm.E4M3FN_VALUES[:127].astype(np.float32)])
+    x = x[np.abs(x) <= 448]
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(nm.e4m3fn_encode(x), ref)
+    sat = nm.e4m3fn_encode(np.array([449.0, 1e6, -500.0, np.nan], np.float32))
+    np.testing.assert_array_equal(sat, [0x7E, 0x7E, 0xFE, 0x7F])
+
+
+def test_per_channel_quantisation():
+    rng = np.random.default_rng(10)
+    w = (rng.standard_normal((16, 64, 3)) * 0.02).astype(np.float32)
+    w[5, :, 1] = 0.0
+    q, s = nm.quantize_per_channel_e4m3fn(w)
+    assert q.shape == w.shape and s.shape == (16, 3)
+    assert s[5, 1] == 1.0 and np.all(q[5, :, 1] == 0)
+    # the absmax element of every non-zero channel encodes to +-448
+    mags = nm.e4m3fn_decode(q & 0x7F)
+    assert np.all(mags.max(axis=1)[s != 1.0] == 448.0)
+    deq = nm.dequantize_e4m3fn(q, s)
+    # e4m3 has 3 mantissa bits: relative error <= 2^-4 for normals
+    big = np.abs(w) > s[:, None, :] * 2.0**-6
+    assert np.all(np.abs(deq - w)[big] <= np.abs(w)[big] * 2.0**-4 + 1e-12)
