@@ -1,0 +1,232 @@
+"""Benchmark of the MoE FFN block on one MI355X.
+
+Workload ("C2"): Mixtral-8x7B-shaped moe_ffn_block,
+bf16 activations and weights, fp32 accumulation, hidden 4096, ffn 14336,
+8 experts, top-2, no renormalisation.  A step is one moe_ffn_block call on
+4096 tokens already resident in HBM (prefill); the 16-token decode call is
+measured the same way and reported under "decode".  Inputs are synthetic and
+seeded (frank-models_amd/workloads.py): activations N(0,1), weights
+N(0,0.02^2), router rows redrawn until the top-3 probabilities are >= 1e-3
+apart.
+
+The JSON line carries:
+  value / ms_per_step   whole-block throughput (tokens/s) over --steps calls,
+                        bracketed by torch.cuda.synchronize()
+  roofline              the dominant kernel (grouped gate+up GEMM), its
+                        average duration from HIP events recorded by the
+                        library on the launch stream, algorithmic FLOPs per
+                        launch (useful work only) against the dense bf16 MFMA
+                        peak (2.5 PFLOP/s); traffic from rocprofv3 PMC
+                        counters when a summary is committed, else null
+  block_mfma_frac       block FLOPs (2*T*H*E + 6*T*k*H*F) / step time / peak
+  decode                T=16: tokens/s and block HBM fraction (bytes of the
+                        touched experts' weights + activations / time / 8 TB/s)
+  cpu_baseline          the oracle's expert-grouped NumPy restatement (oracle/)
+                        timed on this host on a bounded token sample
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_FLOPS = 2.5e15
+PEAK_HBM_BYTES = 8.0e12
+METRIC = "MoE FFN tokens/s + % MFMA peak (prefill) / % HBM BW (decode), Mixtral-shape"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def block_flops(T, H, F, E, k):
+    return 2.0 * T * H * E + 6.0 * T * k * H * F
+
+
+def block_bytes(T, H, F, E, k, touched, wbytes=2, abytes=2):
+    return touched * 3.0 * H * F * wbytes + E * H * abytes + 2.0 * T * H * abytes + 2.0 * T * k * 4
+
+
+def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None):
+    """Times `steps` block calls at T tokens; returns a dict of measurements."""
+    x_np, wr_np, gen = wl.router_inputs(cfg, T)
+    x = torch.from_numpy(x_np).to("cuda", torch.bfloat16)
+    wr = torch.from_numpy(wr_np).to("cuda", torch.bfloat16)
+    if weights is None:
+        t0 = time.perf_counter()
+        dev_w = wl.expert_weights(cfg, "cuda", dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        log(f"weights drawn in {time.perf_counter() - t0:.1f}s")
+        t0 = time.perf_counter()
+        packed = [fm.pack_expert_weights(w) for w in dev_w]
+        torch.cuda.synchronize()
+        pack_s = time.perf_counter() - t0
+        weights = (dev_w, packed, pack_s)
+    dev_w, packed, pack_s = weights
+    block = fm.MoEFFNBlock(wr, *packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                           cfg.normalize, act_dtype=torch.bfloat16)
+    out = torch.empty((T, cfg.n_embd), dtype=torch.bfloat16, device="cuda")
+    for _ in range(warmup):
+        block(x, out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        block(x, out=out)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # Per-kernel durations: HIP events recorded by the library on the launch stream.
+    ll = fm.lowlevel
+    ll.timing_read()
+    ll.timing_enable(True)
+    for _ in range(steps):
+        block(x, out=out)
+    torch.cuda.synchronize()
+    kernels = ll.timing_read()
+    ll.timing_enable(False)
+    ids = block.routing(T)[0]
+    touched = int(torch.unique(ids).numel())
+    return dict(T=T, elapsed=elapsed, ms=elapsed / steps * 1e3, tok_s=steps * T / elapsed,
+                kernels={k: (v[0] / v[1] if v[1] else 0.0) for k, v in kernels.items() if v[1]},
+                touched=touched, pack_s=pack_s, gen=gen, x_np=x_np, wr_np=wr_np, weights=weights)
+
+
+def cpu_baseline(torch, cfg, res, sample):
+    """Expert-grouped NumPy restatement (oracle/) on `sample` tokens of the
+    same batch, fp32, on this host's cores."""
+    import numpy as np
+    from oracle import moe as om
+
+    dev_w = res["weights"][0]
+    host_w = [w.float().cpu().numpy() for w in dev_w]
+    xs = res["x_np"][:sample]
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # pragma: no cover - reporting only
+        threads = len(os.sched_getaffinity(0))
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        om.moe_ffn_block(xs, res["wr_np"], *host_w, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                         cfg.normalize, dtype=np.float32)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    return {
+        "value": sample / best,
+        "unit": "tokens/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"{sample} of the {res['T']} tokens, fp32 expert-grouped NumPy/OpenBLAS restatement of "
+                   f"oracles/moe.py (oracle/moe.py), best of {len(times)} runs ({best:.2f}s each)"),
+    }
+
+
+def read_traffic(kernel_name):
+    """HBM bytes per launch of `kernel_name` from a committed rocprofv3 PMC
+    summary (profiles/pmc_<name>.json), or None."""
+    p = ROOT / "profiles" / f"pmc_{kernel_name}.json"
+    if not p.exists():
+        return None
+    try:
+        return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--decode-tokens", type=int, default=16)
+    ap.add_argument("--cpu-sample", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the MoE FFN path here is built and timed on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured configuration); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    fm = importlib.import_module("frank-models_amd")
+    wl = importlib.import_module("frank-models_amd.workloads")
+    cfg = wl.CONFIGS["C2"]
+    H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
+
+    log(f"prefill T={args.tokens}: {args.warmup} warmup + {args.steps} timed steps")
+    pre = run_config(fm, wl, torch, cfg, args.tokens, args.steps, args.warmup)
+    log(f"prefill {pre['ms']:.3f} ms/step, {pre['tok_s']:.0f} tok/s, kernels(ms) {pre['kernels']}")
+
+    T = args.tokens
+    n_assign = T * k
+    gu_ms = pre["kernels"].get("gate_up", 0.0)
+    gu_flops = 2.0 * n_assign * H * (2 * F)
+    achieved = gu_flops / (gu_ms * 1e-3) / 1e12 if gu_ms else 0.0
+    roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
+                "frac": achieved * 1e12 / PEAK_BF16_FLOPS, "traffic": read_traffic("gate_up_prefill"),
+                "kernel": "gemm_tiled_kernel<SWIGLU> (gate+up grouped GEMM, SwiGLU epilogue)",
+                "kernel_ms": gu_ms, "flops_per_launch": gu_flops}
+    flops = block_flops(T, H, F, E, k)
+    result = {
+        "metric": METRIC,
+        "value": pre["tok_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": pre["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02^2) random-init weights of the Mixtral-8x7B MoE layer)",
+        "config": {"workload": "C2 Mixtral-8x7B moe_ffn_block prefill", "tokens": T, "n_embd": H, "n_ff": F,
+                   "n_expert": E, "n_expert_used": k, "normalize_weights": cfg.normalize,
+                   "weights": "bf16", "accumulate": "fp32"},
+        "roofline": roofline,
+        "block_mfma_frac": flops / (pre["ms"] * 1e-3) / PEAK_BF16_FLOPS,
+        "block_tflops": flops / (pre["ms"] * 1e-3) / 1e12,
+        "kernels_ms": pre["kernels"],
+        "pack_s": pre["pack_s"],
+    }
+
+    if not args.no_decode:
+        Td = args.decode_tokens
+        log(f"decode T={Td}")
+        dec = run_config(fm, wl, torch, cfg, Td, max(args.steps, 20), args.warmup, weights=pre["weights"])
+        nbytes = block_bytes(Td, H, F, E, k, dec["touched"])
+        result["decode"] = {
+            "tokens": Td, "tokens_per_s": dec["tok_s"], "ms_per_step": dec["ms"],
+            "experts_touched": dec["touched"], "algorithmic_bytes": nbytes,
+            "hbm_frac": nbytes / (dec["ms"] * 1e-3) / PEAK_HBM_BYTES,
+            "achieved_GBps": nbytes / (dec["ms"] * 1e-3) / 1e9,
+            "kernels_ms": dec["kernels"],
+        }
+        log(f"decode {dec['ms']:.3f} ms/step, {result['decode']['hbm_frac']:.3f} of HBM peak")
+
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline on {args.cpu_sample} tokens")
+        result["cpu_baseline"] = cpu_baseline(torch, cfg, pre, min(args.cpu_sample, T))
+        log(f"cpu baseline {result['cpu_baseline']['value']:.1f} tok/s")
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -40,6 +40,10 @@ PATH_TILED = 2
 PATH_STREAM = 3
 
 
+# fmoe_timer
+TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id")
+
+
 class FmoeError(RuntimeError):
     """A HIP-level failure reported by libfmoe (status FMOE_ERR_HIP)."""
 
@@ -71,6 +75,8 @@ SIGNATURES = {
     "fmoe_set_gemm_path": (_c_int, [_c_int]),
     "fmoe_get_gemm_path": (_c_int, []),
     "fmoe_last_gemm_path": (_c_int, []),
+    "fmoe_timing_enable": (_c_int, [_c_int]),
+    "fmoe_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64), _c_int]),
     "fmoe_swiglu": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _vp]),
     "fmoe_router": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),
     "fmoe_permute_workspace_bytes": (_sz, [_c_i64, _c_i64, _c_i64]),
@@ -145,3 +151,17 @@ def hip_runtimes_loaded():
             if len(parts) >= 6 and "libamdhip64" in parts[5]:
                 paths.add(os.path.realpath(parts[5]))
     return sorted(paths)
+
+
+def timing_enable(on: bool = True) -> None:
+    check(lib().fmoe_timing_enable(int(bool(on))), "fmoe_timing_enable")
+
+
+def timing_read():
+    """{kernel family: (total ms, launches)} since the last read (waits for
+    the recorded HIP events)."""
+    n = len(TIMERS)
+    ms = (ctypes.c_double * n)()
+    cnt = (_c_i64 * n)()
+    check(lib().fmoe_timing_read(ms, cnt, n), "fmoe_timing_read")
+    return {name: (ms[i], cnt[i]) for i, name in enumerate(TIMERS)}

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "launch.h"
 
@@ -86,6 +87,54 @@ int ensure_device(int* dev_out = nullptr, char* arch = nullptr, size_t arch_len 
                 prop.gcnArchName);
   return FMOE_OK;
 }
+
+// ------------------------------------------------------------ kernel timing
+// Event pairs recorded around launches while timing is enabled; read back
+// (and recycled) by fmoe_timing_read.
+struct PendingTiming {
+  int timer;
+  hipEvent_t start, stop;
+};
+
+std::mutex g_t_mu;
+std::atomic<bool> g_timing{false};
+std::vector<PendingTiming> g_pending;
+std::vector<hipEvent_t> g_event_pool;
+double g_t_ms[FMOE_TIMER_COUNT] = {0};
+int64_t g_t_calls[FMOE_TIMER_COUNT] = {0};
+
+hipEvent_t take_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+class ScopedTimer {
+ public:
+  ScopedTimer(int timer, hipStream_t s) : timer_(timer), s_(s) {
+    if (!g_timing.load(std::memory_order_relaxed)) return;
+    std::lock_guard<std::mutex> lk(g_t_mu);
+    start_ = take_event();
+    stop_ = take_event();
+    if (start_ && stop_) hipEventRecord(start_, s_);
+  }
+  ~ScopedTimer() {
+    if (!start_ || !stop_) return;
+    hipEventRecord(stop_, s_);
+    std::lock_guard<std::mutex> lk(g_t_mu);
+    g_pending.push_back({timer_, start_, stop_});
+  }
+
+ private:
+  int timer_;
+  hipStream_t s_;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+};
 
 // Runs one grouped GEMM on the family the process-wide setting asks for,
 // falling back to the automatic choice when that family cannot run it.
@@ -227,6 +276,34 @@ int fmoe_set_gemm_path(int path) {
 int fmoe_get_gemm_path(void) { return g_path.load(); }
 
 int fmoe_last_gemm_path(void) { return g_last_path; }
+
+int fmoe_timing_enable(int on) {
+  g_timing.store(on != 0);
+  return ok();
+}
+
+int fmoe_timing_read(double* ms_out, int64_t* launches_out, int n) {
+  std::lock_guard<std::mutex> lk(g_t_mu);
+  for (const PendingTiming& p : g_pending) {
+    float ms = 0.f;
+    if (hipEventSynchronize(p.stop) == hipSuccess && hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+      g_t_ms[p.timer] += ms;
+      g_t_calls[p.timer] += 1;
+    }
+    g_event_pool.push_back(p.start);
+    g_event_pool.push_back(p.stop);
+  }
+  g_pending.clear();
+  for (int i = 0; i < n && i < FMOE_TIMER_COUNT; ++i) {
+    if (ms_out) ms_out[i] = g_t_ms[i];
+    if (launches_out) launches_out[i] = g_t_calls[i];
+  }
+  for (int i = 0; i < FMOE_TIMER_COUNT; ++i) {
+    g_t_ms[i] = 0;
+    g_t_calls[i] = 0;
+  }
+  return ok();
+}
 
 int fmoe_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
   if (!act_dtype_ok(dtype)) return fail(FMOE_ERR_DTYPE, "swiglu dtype %d not F32/BF16", dtype);
@@ -397,8 +474,12 @@ int fmoe_mul_mat_id(const void* packed_w, const float* w_scales, int w_dtype, co
   g.epi = EPI_SCATTER;
   g.act_dtype = act_dtype;
   g.w_dtype = w_dtype;
+  g.w_format = packed_format(n_out, n_in, w_dtype);
   g.out_dtype = act_dtype;
-  FMOE_TRY(run_grouped_gemm(g, s));
+  {
+    ScopedTimer t(FMOE_TIMER_MUL_MAT_ID, s);
+    FMOE_TRY(run_grouped_gemm(g, s));
+  }
   FMOE_HIP(launch_zero_invalid_rows(ids, static_cast<int>(n), static_cast<int>(n_expert), y,
                                     act_dtype, n_out, s));
   // y [k*T, n_out] -> out [n_out, k*T] (mul_mat_id.mlir:96-117)
@@ -455,11 +536,17 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
   void* y = at<char>(workspace, L.y);
 
   // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128).
-  FMOE_HIP(launch_router(input, w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
+  {
+    ScopedTimer t(FMOE_TIMER_ROUTER, s);
+    FMOE_HIP(launch_router(input, w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
                          static_cast<int>(n_expert_used), normalize_weights != 0, act_dtype, ids,
-                         rw, s));
+                           rw, s));
+  }
   // Group the slot-major assignments by expert (replaces the gather, mul_mat_id.mlir:50-61).
-  FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err, s));
+  {
+    ScopedTimer t(FMOE_TIMER_PERMUTE, s);
+    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err, s));
+  }
 
   // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
   GroupedGemmArgs g;
@@ -484,8 +571,12 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
   g.epi = EPI_SWIGLU;
   g.act_dtype = act_dtype;
   g.w_dtype = w_dtype;
+  g.w_format = packed_format(n_ff, n_embd, w_dtype);
   g.out_dtype = L.h_dtype;
-  FMOE_TRY(run_grouped_gemm(g, s));
+  {
+    ScopedTimer t(FMOE_TIMER_GATE_UP, s);
+    FMOE_TRY(run_grouped_gemm(g, s));
+  }
 
   // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
   GroupedGemmArgs d;
@@ -507,12 +598,19 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
   d.route_w = rw;
   d.act_dtype = L.h_dtype;
   d.w_dtype = w_dtype;
+  d.w_format = packed_format(n_embd, n_ff, w_dtype);
   d.out_dtype = L.y_dtype;
-  FMOE_TRY(run_grouped_gemm(d, s));
+  {
+    ScopedTimer t(FMOE_TIMER_DOWN, s);
+    FMOE_TRY(run_grouped_gemm(d, s));
+  }
 
   // Step 11: slot-ordered sum + transpose to [n_tokens, n_embd] (mlir:179-206).
-  FMOE_HIP(launch_combine(y, L.y_dtype, out, act_dtype, T, static_cast<int>(n_expert_used),
-                          static_cast<int>(n_embd), s));
+  {
+    ScopedTimer t(FMOE_TIMER_COMBINE, s);
+    FMOE_HIP(launch_combine(y, L.y_dtype, out, act_dtype, T, static_cast<int>(n_expert_used),
+                            static_cast<int>(n_embd), s));
+  }
   return ok();
 }
 

@@ -12,6 +12,10 @@ typedef uint8_t f8_t;     // OCP e4m3fn code in memory
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+// Native 16-byte vector for all data movement (HIP's uint4 is a struct whose
+// copies lower to memcpy, which keeps arrays of it out of registers).
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
 constexpr int kWave = 64;
 

@@ -64,11 +64,11 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(GroupedGemmArgs 
       r = g.order[p];
     a_row = static_cast<const TA*>(g.a) + r * g.lda;
   }
-  const int64_t wofs = static_cast<int64_t>(ti.expert) * N * K;
-  const TW* w_row[NB];
+  const TW* w_base[NB];
   const int bn = n0 + lr;
-  w_row[0] = bn < N ? static_cast<const TW*>(g.w0) + wofs + bn * K : nullptr;
-  if (NB == 2) w_row[NB - 1] = bn < N ? static_cast<const TW*>(g.w1) + wofs + bn * K : nullptr;
+  w_base[0] = static_cast<const TW*>(g.w0);
+  if (NB == 2) w_base[NB - 1] = static_cast<const TW*>(g.w1);
+  const bool bn_ok = bn < N;
 
   float acc[NB][4][4];
 #pragma unroll
@@ -84,7 +84,9 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(GroupedGemmArgs 
       const int64_t k = k0 + lk + j;
       As[lk + j][lr] = (a_row && k < K) ? to_f32(a_row, k) : 0.f;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) Bs[b][lk + j][lr] = (w_row[b] && k < K) ? to_f32(w_row[b], k) : 0.f;
+      for (int b = 0; b < NB; ++b)
+        Bs[b][lk + j][lr] =
+            (bn_ok && k < K) ? to_f32(w_base[b], packed_offset(g.w_format, g.w_dtype, ti.expert, bn, k, N, K)) : 0.f;
     }
     __syncthreads();
 #pragma unroll

@@ -1,12 +1,487 @@
-// MFMA grouped GEMMs for gfx950 (placeholder: not yet enabled).
+// MFMA grouped GEMMs for gfx950: bf16 activations x (bf16 | fp8-e4m3)
+// expert weights in the WF_MFMA16 packed layout, fp32 accumulation.
+//
+// These are mul_mat_id's per-assignment mat-vecs (components/moe/
+// mul_mat_id.mlir:55-94, oracles/moe.py:37-45) with the assignments of one
+// expert batched into a GEMM over the expert-sorted rows of the permutation.
+// The gate and up projections share one kernel (two weight sets, the SwiGLU
+// of components/activation/swiglu.mlir:37-47 in the epilogue); the down
+// projection's epilogue applies the routing weight
+// (moe_ffn_block.mlir:162-177) and writes each assignment's row.
+//
+// Operand roles are swapped with respect to "rows x columns": the MFMA's A
+// operand is a 16-row weight block (16 outputs x 32 inputs), its B operand
+// is 16 assignment rows x 32 inputs.  The accumulator then gives each lane 4
+// consecutive output columns of one assignment row, so epilogue stores are
+// 8-byte (bf16) or 16-byte (fp32) vectors.
+//
+// Two kernels:
+//   tiled   128 rows x 256 weight rows per 256-thread block (2x2 waves, each
+//           64 rows x 128 weight rows), 64 inputs per stage, LDS double
+//           buffer (96 KiB), global loads of stage k+1 in flight while stage
+//           k computes.  Block order is XCD-aware: consecutive tiles that
+//           share weight rows run on the same XCD (same L2).
+//   stream  decode-sized batches: every weight block is read exactly once
+//           straight into MFMA registers (no LDS), 16 assignment rows per
+//           pass, 4 input steps of loads in flight per wave.
 #include "common.h"
 #include "launch.h"
 
 namespace fmoe {
+namespace {
 
-bool gemm_tiled_supported(const GroupedGemmArgs&) { return false; }
-bool gemm_stream_supported(const GroupedGemmArgs&) { return false; }
-hipError_t launch_gemm_tiled(const GroupedGemmArgs&, hipStream_t) { return hipErrorNotSupported; }
-hipError_t launch_gemm_stream(const GroupedGemmArgs&, hipStream_t) { return hipErrorNotSupported; }
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// Two e4m3fn codes (bytes 0-1, or 2-3 when HI) -> two bf16, exact (scale 1).
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+
+// 16 e4m3fn codes (two 32-input steps of one lane) -> two bf16x8 fragments.
+__device__ __forceinline__ void f8x16_to_bf16(const u32x4_t q, u32x4_t& s0, u32x4_t& s1) {
+  s0 = u32x4_t{cvt2<false>(q.x), cvt2<true>(q.x), cvt2<false>(q.y), cvt2<true>(q.y)};
+  s1 = u32x4_t{cvt2<false>(q.z), cvt2<true>(q.z), cvt2<false>(q.w), cvt2<true>(q.w)};
+}
+
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // gate * silu(up) = g * u / (1 + exp(-u))
+  return g * (u / (1.f + __expf(-u)));
+}
+
+// Source row of assignment p (see AMode).
+__device__ __forceinline__ int64_t a_source_row(const GroupedGemmArgs& g, int p) {
+  if (g.a_mode == A_GATHER_TOKEN) return g.order[p] % g.n_tokens;
+  if (g.a_mode == A_GATHER_FLAT) return g.order[p];
+  return p;
+}
+
+// Writes 4 consecutive columns [n, n+4) of row p's result.
+template <int EPI>
+__device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t n, float v0, float v1,
+                                       float v2, float v3) {
+  if (EPI == EPI_SWIGLU || g.out_dtype == DT_BF16) {
+    int64_t row = p;
+    if (EPI != EPI_SWIGLU) row = g.order[p];
+    if (EPI == EPI_SCATTER_WEIGHTED) {
+      const float w = g.route_w[row];
+      v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+    }
+    u32x2_t pk{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+    *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(g.out) + row * g.ldo + n) = pk;
+  } else {
+    const int64_t row = g.order[p];
+    if (EPI == EPI_SCATTER_WEIGHTED) {
+      const float w = g.route_w[row];
+      v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+    }
+    *reinterpret_cast<float4*>(static_cast<float*>(g.out) + row * g.ldo + n) = float4{v0, v1, v2, v3};
+  }
+}
+
+// ======================================================================= tiled
+constexpr int kThreads = 256;
+constexpr int kBM = 128;  // assignment rows per tile
+constexpr int kBK = 64;   // inputs per stage
+constexpr int kGroupN = 4;  // column tiles swept together per row-tile sweep
+
+template <int NSETS>
+struct Tiled {
+  static constexpr int kBNSet = NSETS == 2 ? 128 : 256;  // weight rows per set per tile
+  static constexpr int kWaveN = kBNSet / 2;              // per wave per set
+  static constexpr int kNSub = kWaveN / 16;              // 16-row weight blocks per wave per set
+  static constexpr int kMSub = 4;                        // 64 rows per wave
+  static constexpr int kNBStage = NSETS * kBNSet / 16;   // weight row blocks per stage (16)
+  static constexpr int kABytes = kBM * kBK * 2;          // 16 KiB
+  static constexpr int kBBytes = kNBStage * 2 * 1024;    // 32 KiB (two 32-input blocks per row block)
+};
+
+// Logical tile of a hardware block id: hardware dispatches block b to XCD
+// b % 8; logical ids are handed out so that each XCD gets a contiguous range,
+// and within it kGroupN column tiles are swept across all row tiles
+// (weight rows of a column tile are then re-read from the XCD's L2 by the
+// row tiles of the same expert running beside each other).
+__device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, int* row_tile, int* col_tile) {
+  const int total = n_row_tiles * n_col_tiles;
+  const int per_xcd = (total + 7) / 8;
+  const int b = blockIdx.x;
+  const int logical = (b % 8) * per_xcd + b / 8;
+  if (logical >= total) return false;
+  const int group_span = kGroupN * n_row_tiles;
+  const int group = logical / group_span;
+  const int within = logical - group * group_span;
+  const int cols_in_group = min(kGroupN, n_col_tiles - group * kGroupN);
+  *row_tile = within / cols_in_group;
+  *col_tile = group * kGroupN + within % cols_in_group;
+  return true;
+}
+
+template <int EPI, int NSETS, bool F8>
+__global__ __launch_bounds__(kThreads, 1) void gemm_tiled_kernel(GroupedGemmArgs g, int n_row_tiles,
+                                                                  int n_col_tiles) {
+  using C = Tiled<NSETS>;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  unsigned char* a_s = lds;                   // [2][kBM][kBK] bf16, 16-byte chunks XOR-swizzled
+  unsigned char* b_s = lds + 2 * C::kABytes;  // [2][kNBStage][2][64 lanes][16 B]
+
+  int row_tile, col_tile;
+  if (!logical_tile(n_row_tiles, n_col_tiles, &row_tile, &col_tile)) return;
+  TileInfo ti;
+  if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;  // rows wm*64 .. +64
+  const int wn = wave & 1;   // weight rows wn*kWaveN .. per set
+  const int64_t N = g.N, K = g.K;
+  const int64_t n0 = static_cast<int64_t>(col_tile) * C::kBNSet;
+  const int64_t nblocks = N / 16;  // row blocks per expert
+  const int KT = static_cast<int>(K / kBK);
+
+  // ---- A rows this thread stages: rows (tid >> 3) + 32 j, 16-byte chunk tid & 7.
+  const int a_chunk = tid & 7;
+  const bf16_t* a_src[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = (tid >> 3) + 32 * j;
+    const int p = ti.row0 + (r < ti.rows ? r : 0);
+    a_src[j] = static_cast<const bf16_t*>(g.a) + a_source_row(g, p) * g.lda + a_chunk * 8;
+  }
+
+  // ---- weight blocks this thread stages, per weight set.
+  // bf16: 2 input blocks per row block per stage; chunk c = tid + 256 j covers
+  //   stage block c >> 6 = 2 * (row block) + input block, lane c & 63, so
+  //   thread tid stages row blocks (tid >> 7) + 2 jj of each set (jj < kRB / 2)
+  //   at input block (tid >> 6) & 1.
+  // fp8: 1 packed block (64 inputs) per row block per stage; thread tid stages
+  //   row blocks (tid >> 6) + 4 jj of each set (jj < kRB / 4).
+  constexpr int kRB = C::kBNSet / 16;               // row blocks per set per stage
+  constexpr int kJ = F8 ? kRB / 4 : kRB / 2;        // loads per set per stage
+  const int64_t kblocks = F8 ? K / 64 : K / 32;     // packed blocks per row block
+  const int rb_first = F8 ? (tid >> 6) : (tid >> 7);
+  const int rb_step = F8 ? 4 : 2;
+  const int kb_sel = F8 ? 0 : ((tid >> 6) & 1);
+  const int64_t b_stride = static_cast<int64_t>(rb_step) * kblocks * 1024;  // bytes between jj
+  const unsigned char* b_base[NSETS];
+#pragma unroll
+  for (int set = 0; set < NSETS; ++set) {
+    const unsigned char* w = static_cast<const unsigned char*>(set == 0 ? g.w0 : g.w1);
+    b_base[set] = w + ((static_cast<int64_t>(ti.expert) * nblocks + n0 / 16 + rb_first) * kblocks + kb_sel) * 1024 +
+                  lane * 16;
+  }
+  // Row blocks past N (partial last column tile) are staged as zeros.
+  const int64_t rb_limit = nblocks - n0 / 16 - rb_first;  // jj*rb_step < rb_limit is in range
+
+  u32x4_t a_reg[4];
+  u32x4_t b_reg[NSETS * kJ];
+
+  auto load_stage = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a_reg[j] = *reinterpret_cast<const u32x4_t*>(a_src[j] + kt * kBK);
+    const int64_t adv = static_cast<int64_t>(kt) * (F8 ? 1024 : 2048);
+#pragma unroll
+    for (int set = 0; set < NSETS; ++set)
+#pragma unroll
+      for (int jj = 0; jj < kJ; ++jj)
+        b_reg[set * kJ + jj] = (jj * rb_step < rb_limit)
+                                   ? *reinterpret_cast<const u32x4_t*>(b_base[set] + jj * b_stride + adv)
+                                   : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  auto store_stage = [&](int st) __attribute__((always_inline)) {
+    unsigned char* as = a_s + st * C::kABytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = (tid >> 3) + 32 * j;
+      *reinterpret_cast<u32x4_t*>(as + r * 128 + ((a_chunk ^ (r & 7)) << 4)) = a_reg[j];
+    }
+    unsigned char* bs = b_s + st * C::kBBytes;
+#pragma unroll
+    for (int set = 0; set < NSETS; ++set) {
+#pragma unroll
+      for (int jj = 0; jj < kJ; ++jj) {
+        const int rb = set * kRB + rb_first + jj * rb_step;  // stage row block
+        if (F8) {
+          u32x4_t s0, s1;
+          f8x16_to_bf16(b_reg[set * kJ + jj], s0, s1);
+          *reinterpret_cast<u32x4_t*>(bs + (rb * 2 + 0) * 1024 + lane * 16) = s0;
+          *reinterpret_cast<u32x4_t*>(bs + (rb * 2 + 1) * 1024 + lane * 16) = s1;
+        } else {
+          *reinterpret_cast<u32x4_t*>(bs + (rb * 2 + kb_sel) * 1024 + lane * 16) = b_reg[set * kJ + jj];
+        }
+      }
+    }
+  };
+
+  f32x4_t acc[NSETS][C::kNSub][C::kMSub];
+#pragma unroll
+  for (int s = 0; s < NSETS; ++s)
+#pragma unroll
+    for (int i = 0; i < C::kNSub; ++i)
+#pragma unroll
+      for (int m = 0; m < C::kMSub; ++m) acc[s][i][m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    // Prefetch the next stage (the last iteration re-reads the final stage
+    // into the idle buffer: branch-free, so the staging registers stay in
+    // registers).
+    load_stage(kt + 1 < KT ? kt + 1 : kt);
+    const unsigned char* as = a_s + cur * C::kABytes;
+    const unsigned char* bs = b_s + cur * C::kBBytes;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {  // two 32-input steps per stage
+      u32x4_t tok[C::kMSub];
+#pragma unroll
+      for (int m = 0; m < C::kMSub; ++m) {
+        const int r = wm * 64 + m * 16 + (lane & 15);
+        const int ch = s * 4 + (lane >> 4);
+        tok[m] = *reinterpret_cast<const u32x4_t*>(as + r * 128 + ((ch ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int set = 0; set < NSETS; ++set) {
+#pragma unroll
+        for (int i = 0; i < C::kNSub; ++i) {
+          const int rb = set * (C::kBNSet / 16) + wn * C::kNSub + i;
+          const u32x4_t w = *reinterpret_cast<const u32x4_t*>(bs + (rb * 2 + s) * 1024 + lane * 16);
+#pragma unroll
+          for (int m = 0; m < C::kMSub; ++m) acc[set][i][m] = mfma16(w, tok[m], acc[set][i][m]);
+        }
+      }
+    }
+    store_stage(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds row (lane & 15) of each 16-row group, columns 4*(lane>>4) .. +4.
+  const int64_t e = ti.expert;
+#pragma unroll
+  for (int i = 0; i < C::kNSub; ++i) {
+    const int64_t n = n0 + wn * C::kWaveN + i * 16 + 4 * (lane >> 4);
+    if (n >= N) continue;
+    float4 sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
+    if (F8) {
+      sc0 = *reinterpret_cast<const float4*>(g.s0 + e * N + n);
+      if (NSETS == 2) sc1 = *reinterpret_cast<const float4*>(g.s1 + e * N + n);
+    }
+#pragma unroll
+    for (int m = 0; m < C::kMSub; ++m) {
+      const int r = wm * 64 + m * 16 + (lane & 15);
+      if (r >= ti.rows) continue;
+      const int p = ti.row0 + r;
+      const f32x4_t a0 = acc[0][i][m];
+      if (EPI == EPI_SWIGLU) {
+        const f32x4_t a1 = acc[NSETS - 1][i][m];
+        store4<EPI>(g, p, n, silu_mul(a0[0] * sc0.x, a1[0] * sc1.x), silu_mul(a0[1] * sc0.y, a1[1] * sc1.y),
+                    silu_mul(a0[2] * sc0.z, a1[2] * sc1.z), silu_mul(a0[3] * sc0.w, a1[3] * sc1.w));
+      } else {
+        store4<EPI>(g, p, n, a0[0] * sc0.x, a0[1] * sc0.y, a0[2] * sc0.z, a0[3] * sc0.w);
+      }
+    }
+  }
+}
+
+// ======================================================================= stream
+constexpr int kStreamRowsPerWave = 16;
+constexpr int kStreamRows = 4 * kStreamRowsPerWave;  // weight rows per set per block
+constexpr int kStreamUnroll = 4;                     // 32-input steps per iteration
+
+template <int EPI, int NSETS, bool F8>
+__global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
+  const int e = blockIdx.x / col_tiles;
+  const int ct = blockIdx.x - e * col_tiles;
+  const int row_begin = g.offsets[e];
+  const int count = g.offsets[e + 1] - row_begin;
+  if (count == 0) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t N = g.N, K = g.K;
+  const int64_t n_base = static_cast<int64_t>(ct) * kStreamRows + wave * kStreamRowsPerWave;
+  if (n_base >= N) return;
+  const int64_t nblocks = N / 16;
+  const int64_t nb = n_base / 16;
+  const int64_t kblocks = F8 ? K / 64 : K / 32;
+  const unsigned char* wsrc[NSETS];
+#pragma unroll
+  for (int s = 0; s < NSETS; ++s) {
+    const unsigned char* base = static_cast<const unsigned char*>(s == 0 ? g.w0 : g.w1);
+    wsrc[s] = base + ((static_cast<int64_t>(e) * nblocks + nb) * kblocks) * 1024 + lane * 16;
+  }
+  const int ksteps = static_cast<int>(K / 32);
+  const int kq = (lane >> 4) * 8;  // this lane's 8 inputs within a 32-input step
+
+  for (int m0 = 0; m0 < count; m0 += 16) {
+    const int r = m0 + (lane & 15);
+    const bool r_ok = r < count;
+    const bf16_t* arow = static_cast<const bf16_t*>(g.a) +
+                         a_source_row(g, row_begin + (r_ok ? r : 0)) * g.lda + kq;
+    f32x4_t acc[NSETS];
+#pragma unroll
+    for (int s = 0; s < NSETS; ++s) acc[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    int ks = 0;
+    for (; ks + kStreamUnroll <= ksteps; ks += kStreamUnroll) {
+      u32x4_t tok[kStreamUnroll];
+      u32x4_t wv[NSETS][kStreamUnroll];
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u)
+        tok[u] = r_ok ? *reinterpret_cast<const u32x4_t*>(arow + (ks + u) * 32) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int s = 0; s < NSETS; ++s) {
+        if (F8) {
+#pragma unroll
+          for (int u = 0; u < kStreamUnroll; u += 2) {
+            const u32x4_t q = *reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>((ks + u) / 2) * 1024);
+            f8x16_to_bf16(q, wv[s][u], wv[s][u + 1]);
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < kStreamUnroll; ++u)
+            wv[s][u] = *reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks + u) * 1024);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u)
+#pragma unroll
+        for (int s = 0; s < NSETS; ++s) acc[s] = mfma16(wv[s][u], tok[u], acc[s]);
+    }
+    for (; ks < ksteps; ks += F8 ? 2 : 1) {  // tail (K % 128 != 0)
+      const u32x4_t t0 = r_ok ? *reinterpret_cast<const u32x4_t*>(arow + ks * 32) : u32x4_t{0u, 0u, 0u, 0u};
+      if (F8) {
+        const u32x4_t t1 = r_ok ? *reinterpret_cast<const u32x4_t*>(arow + (ks + 1) * 32) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int s = 0; s < NSETS; ++s) {
+          u32x4_t w0, w1;
+          f8x16_to_bf16(*reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks / 2) * 1024), w0, w1);
+          acc[s] = mfma16(w0, t0, acc[s]);
+          acc[s] = mfma16(w1, t1, acc[s]);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < NSETS; ++s)
+          acc[s] = mfma16(*reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks) * 1024), t0, acc[s]);
+      }
+    }
+
+    if (r_ok) {
+      const int64_t n = n_base + 4 * (lane >> 4);
+      float4 sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
+      if (F8) {
+        sc0 = *reinterpret_cast<const float4*>(g.s0 + static_cast<int64_t>(e) * N + n);
+        if (NSETS == 2) sc1 = *reinterpret_cast<const float4*>(g.s1 + static_cast<int64_t>(e) * N + n);
+      }
+      const int p = row_begin + r;
+      const f32x4_t a0 = acc[0];
+      if (EPI == EPI_SWIGLU) {
+        const f32x4_t a1 = acc[NSETS - 1];
+        store4<EPI>(g, p, n, silu_mul(a0[0] * sc0.x, a1[0] * sc1.x), silu_mul(a0[1] * sc0.y, a1[1] * sc1.y),
+                    silu_mul(a0[2] * sc0.z, a1[2] * sc1.z), silu_mul(a0[3] * sc0.w, a1[3] * sc1.w));
+      } else {
+        store4<EPI>(g, p, n, a0[0] * sc0.x, a0[1] * sc0.y, a0[2] * sc0.z, a0[3] * sc0.w);
+      }
+    }
+  }
+}
+
+bool mfma_common_ok(const GroupedGemmArgs& g) {
+  if (g.act_dtype != DT_BF16) return false;
+  if (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) return false;
+  if (g.w_format != WF_MFMA16) return false;
+  if (g.epi == EPI_SWIGLU && g.out_dtype != DT_BF16) return false;
+  if (g.epi == EPI_SWIGLU && !g.w1) return false;
+  if (g.N % 16 || g.lda % 8 || g.ldo % 4) return false;
+  if (reinterpret_cast<uintptr_t>(g.a) % 16 || reinterpret_cast<uintptr_t>(g.out) % 16) return false;
+  if (g.w_dtype == DT_F8 && (!g.s0 || (g.epi == EPI_SWIGLU && !g.s1))) return false;
+  return true;
+}
+
+template <bool F8>
+hipError_t launch_tiled_t(const GroupedGemmArgs& g, hipStream_t s) {
+  const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
+  if (g.epi == EPI_SWIGLU) {
+    using C = Tiled<2>;
+    const int col_tiles = static_cast<int>((g.N + C::kBNSet - 1) / C::kBNSet);
+    const size_t lds = 2 * (C::kABytes + C::kBBytes);
+    const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles;
+    const unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
+    hipLaunchKernelGGL((gemm_tiled_kernel<EPI_SWIGLU, 2, F8>), dim3(blocks), dim3(kThreads), lds, s, g,
+                       row_tiles, col_tiles);
+  } else {
+    using C = Tiled<1>;
+    const int col_tiles = static_cast<int>((g.N + C::kBNSet - 1) / C::kBNSet);
+    const size_t lds = 2 * (C::kABytes + C::kBBytes);
+    const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles;
+    const unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
+    if (g.epi == EPI_SCATTER_WEIGHTED)
+      hipLaunchKernelGGL((gemm_tiled_kernel<EPI_SCATTER_WEIGHTED, 1, F8>), dim3(blocks), dim3(kThreads), lds,
+                         s, g, row_tiles, col_tiles);
+    else
+      hipLaunchKernelGGL((gemm_tiled_kernel<EPI_SCATTER, 1, F8>), dim3(blocks), dim3(kThreads), lds, s, g,
+                         row_tiles, col_tiles);
+  }
+  return hipGetLastError();
+}
+
+template <bool F8>
+hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
+  const int col_tiles = static_cast<int>((g.N + kStreamRows - 1) / kStreamRows);
+  const dim3 grid(static_cast<unsigned>(col_tiles * g.n_expert));
+  if (g.epi == EPI_SWIGLU)
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8>), grid, dim3(kThreads), 0, s, g, col_tiles);
+  else if (g.epi == EPI_SCATTER_WEIGHTED)
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER_WEIGHTED, 1, F8>), grid, dim3(kThreads), 0, s, g,
+                       col_tiles);
+  else
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER, 1, F8>), grid, dim3(kThreads), 0, s, g, col_tiles);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_tiled_supported(const GroupedGemmArgs& g) {
+  return mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0;
+}
+
+bool gemm_stream_supported(const GroupedGemmArgs& g) {
+  return mfma_common_ok(g) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0;
+}
+
+hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t s) {
+  if (!gemm_tiled_supported(g)) return hipErrorNotSupported;
+  if (g.n_assign == 0 || g.N == 0) return hipSuccess;
+  // 96 KiB of dynamic LDS per block (gfx950 has 160 KiB per CU); set once per process.
+  static const bool configured = [] {
+    const int b2 = 2 * (Tiled<2>::kABytes + Tiled<2>::kBBytes);
+    const int b1 = 2 * (Tiled<1>::kABytes + Tiled<1>::kBBytes);
+    const void* k2[] = {reinterpret_cast<const void*>(gemm_tiled_kernel<EPI_SWIGLU, 2, false>),
+                        reinterpret_cast<const void*>(gemm_tiled_kernel<EPI_SWIGLU, 2, true>)};
+    const void* k1[] = {reinterpret_cast<const void*>(gemm_tiled_kernel<EPI_SCATTER_WEIGHTED, 1, false>),
+                        reinterpret_cast<const void*>(gemm_tiled_kernel<EPI_SCATTER_WEIGHTED, 1, true>),
+                        reinterpret_cast<const void*>(gemm_tiled_kernel<EPI_SCATTER, 1, false>),
+                        reinterpret_cast<const void*>(gemm_tiled_kernel<EPI_SCATTER, 1, true>)};
+    for (const void* k : k2) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, b2);
+    for (const void* k : k1) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, b1);
+    (void)hipGetLastError();
+    return true;
+  }();
+  (void)configured;
+  return g.w_dtype == DT_F8 ? launch_tiled_t<true>(g, s) : launch_tiled_t<false>(g, s);
+}
+
+hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t s) {
+  if (!gemm_stream_supported(g)) return hipErrorNotSupported;
+  if (g.n_assign == 0 || g.N == 0) return hipSuccess;
+  return g.w_dtype == DT_F8 ? launch_stream_t<true>(g, s) : launch_stream_t<false>(g, s);
+}
 
 }  // namespace fmoe

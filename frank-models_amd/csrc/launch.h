@@ -12,6 +12,41 @@ enum DType { DT_F32 = 0, DT_BF16 = 1, DT_F8 = 2 };
 
 inline size_t dtype_bytes(int dt) { return dt == DT_F32 ? 4 : dt == DT_BF16 ? 2 : 1; }
 
+// Packed expert-weight layouts.  The layout is a function of (n_out, n_in,
+// dtype) only, so producer and consumers agree without carrying a tag.
+//
+// WF_ROWMAJOR: per expert [n_out][n_in], n_in contiguous.
+// WF_MFMA16:   per expert, blocks of 16 output rows x KB inputs (KB = 32 for
+//   bf16, 64 for fp8), blocks ordered [row block][input block], each block
+//   1 KiB = 64 lanes x 16 bytes in the operand order of
+//   v_mfma_f32_16x16x32_bf16: lane l holds rows (l % 16) and inputs
+//   8*(l / 16) .. +8 of a 32-input step.  fp8 lanes hold two such steps
+//   (inputs q and 32+q at bytes q%8 and 8+q%8).  A wave loads one block with
+//   one fully coalesced 16-byte-per-lane load, ready for the MFMA.
+enum WFormat { WF_ROWMAJOR = 0, WF_MFMA16 = 1 };
+
+__host__ __device__ inline int packed_format(int64_t n_out, int64_t n_in, int dtype) {
+  if (dtype == DT_BF16 && n_out % 16 == 0 && n_in % 32 == 0) return WF_MFMA16;
+  if (dtype == DT_F8 && n_out % 16 == 0 && n_in % 64 == 0) return WF_MFMA16;
+  return WF_ROWMAJOR;
+}
+
+// Element offset of weight (e, n, k) in a packed buffer of n_out = N, n_in = K.
+__host__ __device__ inline int64_t packed_offset(int fmt, int dtype, int64_t e, int64_t n, int64_t k,
+                                                 int64_t N, int64_t K) {
+  if (fmt == WF_ROWMAJOR) return (e * N + n) * K + k;
+  if (dtype == DT_BF16) {
+    const int64_t blk = (e * (N / 16) + n / 16) * (K / 32) + k / 32;
+    const int64_t lane = (n % 16) + 16 * ((k % 32) / 8);
+    return blk * 512 + lane * 8 + k % 8;
+  }
+  const int64_t blk = (e * (N / 16) + n / 16) * (K / 64) + k / 64;
+  const int64_t kk = k % 64;
+  const int64_t q = kk % 32;
+  const int64_t lane = (n % 16) + 16 * (q / 8);
+  return blk * 1024 + lane * 16 + (kk / 32) * 8 + q % 8;
+}
+
 // How a grouped GEMM finds row p's A operand.
 enum AMode {
   A_GATHER_TOKEN = 0,  // row order[p] % n_tokens of `a` (x rows, per token)
@@ -46,6 +81,7 @@ struct GroupedGemmArgs {
   const float* route_w = nullptr;  // [n_assign] routing weight per flat assignment
   int act_dtype = DT_F32;       // A operand type
   int w_dtype = DT_F32;
+  int w_format = WF_ROWMAJOR;   // packed_format(N, K, w_dtype)
   int out_dtype = DT_F32;
 };
 

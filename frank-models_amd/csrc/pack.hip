@@ -1,7 +1,7 @@
 // One-time expert-weight packing: reference layout [n_out, n_in, E] (expert
-// innermost, components/moe/moe_ffn_block.mlir:37-39) -> per-expert
-// [E][n_out][n_in] with n_in contiguous, the K-contiguous operand layout the
-// grouped GEMMs stream.  The reference instead transposes every weight on
+// innermost, components/moe/moe_ffn_block.mlir:37-39) -> per-expert operand
+// layout (packed_format / packed_offset in launch.h: MFMA-ready 1 KiB blocks
+// when the shape allows, else [E][n_out][n_in] row-major).  The reference instead transposes every weight on
 // every call (components/moe/mul_mat_id.mlir:37-48).
 //
 // fp8 (OCP e4m3fn) packing quantises each output channel (o, e):
@@ -33,6 +33,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__
   __shared__ uint32_t amax_bits[kMaxExpert];
   __shared__ float scale[kMaxExpert];
   const int o = blockIdx.x;
+  const int fmt = packed_format(n_out, n_in, dst_dt);
   const int64_t slab = static_cast<int64_t>(n_in) * n_expert;
   const int64_t src0 = static_cast<int64_t>(o) * slab;
 
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__
   for (int64_t idx = threadIdx.x; idx < slab; idx += kThreads) {
     const int e = static_cast<int>(idx % n_expert);
     const int64_t i = idx / n_expert;
-    const int64_t d = (static_cast<int64_t>(e) * n_out + o) * n_in + i;
+    const int64_t d = packed_offset(fmt, dst_dt, e, o, i, n_out, n_in);
     if (dst_dt == DT_F8) {
       if (src_dt == DT_F8) {
         static_cast<f8_t*>(dst)[d] = static_cast<const f8_t*>(src)[src0 + idx];

@@ -79,6 +79,24 @@ int fmoe_get_gemm_path(void);
 /* The family used by the last grouped GEMM launched on this thread. */
 int fmoe_last_gemm_path(void);
 
+/* Kernel timing (no counterpart in the reference, which has no profiling
+ * beyond dumping linked IR, tests/conftest.py:24-30).  While enabled, each
+ * kernel that fmoe_moe_ffn_block / fmoe_mul_mat_id launch is bracketed by
+ * HIP events recorded on the caller's stream.  fmoe_timing_read waits for
+ * the recorded events, writes the summed milliseconds and launch counts per
+ * kernel family (index fmoe_timer, up to n entries) and clears them. */
+typedef enum fmoe_timer {
+  FMOE_TIMER_ROUTER = 0,
+  FMOE_TIMER_PERMUTE = 1,
+  FMOE_TIMER_GATE_UP = 2, /* grouped GEMM: gate + up projections + SwiGLU */
+  FMOE_TIMER_DOWN = 3,    /* grouped GEMM: down projection + routing weight */
+  FMOE_TIMER_COMBINE = 4,
+  FMOE_TIMER_MUL_MAT_ID = 5,
+  FMOE_TIMER_COUNT = 6
+} fmoe_timer;
+int fmoe_timing_enable(int on);
+int fmoe_timing_read(double *ms_out, int64_t *launches_out, int n);
+
 /* ---------------------------------------------------------------------- */
 /* SwiGLU: out[i] = gate[i] * up[i] / (1 + exp(-up[i])), silu on `up`.
  * Replaces @activation_components.swiglu (components/activation/swiglu.mlir:16-51,

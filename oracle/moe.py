@@ -136,7 +136,7 @@ def mul_mat_id(weights: np.ndarray, input: np.ndarray, ids: np.ndarray, dtype=np
     out = np.zeros((k * T, n_out), dtype=dtype)
     for e in np.unique(flat):
         rows = np.nonzero(flat == e)[0]
-        w = np.asarray(weights[:, :, int(e)], dtype=dtype)  # [n_out, n_in]
+        w = np.ascontiguousarray(weights[:, :, int(e)], dtype=dtype)  # [n_out, n_in]
         out[rows] = x[rows] @ w.T
     return np.ascontiguousarray(out.T).reshape(n_out, k, T)
 
@@ -197,10 +197,12 @@ def moe_ffn_block(
     for e in np.unique(ids):
         s_idx, t_idx = np.nonzero(ids == e)
         xe = x[t_idx]
-        up = xe @ np.asarray(up_exps_w[:, :, int(e)], dtype=dtype).T
-        gate = xe @ np.asarray(gate_exps_w[:, :, int(e)], dtype=dtype).T
+        # Contiguous per-expert copies keep the products on BLAS (a strided
+        # expert slice would send NumPy down its element-wise matmul loop).
+        up = xe @ np.ascontiguousarray(up_exps_w[:, :, int(e)], dtype=dtype).T
+        gate = xe @ np.ascontiguousarray(gate_exps_w[:, :, int(e)], dtype=dtype).T
         h = swiglu(gate, up)
-        d = h @ np.asarray(down_exps_w[:, :, int(e)], dtype=dtype).T
+        d = h @ np.ascontiguousarray(down_exps_w[:, :, int(e)], dtype=dtype).T
         y[s_idx, t_idx] = d * w[s_idx, t_idx][:, None]
     out = y[0].copy()
     for s in range(1, k):

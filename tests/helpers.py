@@ -25,3 +25,23 @@ def assert_close_rms(actual, expected, rtol, what=""):
 def assert_close(actual, expected, rtol=1e-5, atol=1e-6):
     """The reference's comparison (tests/utils.py:244-251)."""
     np.testing.assert_allclose(np.asarray(actual), np.asarray(expected), rtol=rtol, atol=atol)
+
+
+def packed_index(n_out, n_in, n_expert, dtype):
+    """Flat element offset of every weight (e, n, k) in the packed buffer,
+    shape [E, n_out, n_in]: the WF_MFMA16 block layout (16 rows x 32 inputs
+    per 1 KiB block for bf16, 16 x 64 for fp8, 64 lanes x 16 bytes, lane l =
+    row l%16, inputs 8*(l//16)..+8 of each 32-input step) when the shape
+    allows it, else row-major [E][n_out][n_in]."""
+    e, n, k = np.meshgrid(np.arange(n_expert), np.arange(n_out), np.arange(n_in), indexing="ij")
+    if dtype == "bf16" and n_out % 16 == 0 and n_in % 32 == 0:
+        blk = (e * (n_out // 16) + n // 16) * (n_in // 32) + k // 32
+        lane = n % 16 + 16 * ((k % 32) // 8)
+        return blk * 512 + lane * 8 + k % 8
+    if dtype == "fp8" and n_out % 16 == 0 and n_in % 64 == 0:
+        blk = (e * (n_out // 16) + n // 16) * (n_in // 64) + k // 64
+        kk = k % 64
+        q = kk % 32
+        lane = n % 16 + 16 * (q // 8)
+        return blk * 1024 + lane * 16 + (kk // 32) * 8 + q % 8
+    return (e * n_out + n) * n_in + k

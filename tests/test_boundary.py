@@ -141,3 +141,12 @@ def test_python_api_errors_without_device(fm):
                       np.array([[0.0, 1.0]]))
     with pytest.raises(ValueError):
         fm.swiglu(np.zeros((2, 3), np.float32), np.zeros((3, 2), np.float32))
+
+
+@pytest.mark.parametrize("shape,dt", [((32, 64, 3), "bf16"), ((32, 128, 2), "fp8"), ((24, 40, 5), "bf16"),
+                                      ((16, 96, 2), "fp8")])
+def test_packed_layout_is_a_bijection(shape, dt):
+    from helpers import packed_index
+
+    idx = packed_index(*shape, dt).reshape(-1)
+    assert np.array_equal(np.sort(idx), np.arange(idx.size))

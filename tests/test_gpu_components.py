@@ -10,7 +10,7 @@ import torch
 import oracle
 from oracle import moe as om
 from oracle import numerics as nm
-from helpers import assert_close
+from helpers import assert_close, packed_index
 from test_oracle import BLOCK_REFERENCE_CASES, MMID_REFERENCE_CASES, REFERENCE_IDS, _mmid_case, block_inputs
 
 pytestmark = pytest.mark.gpu
@@ -155,33 +155,41 @@ def test_permute_device_ids_out_of_range(fm):
 
 
 # ------------------------------------------------------------------ packing
-def test_pack_bf16_bits(fm):
+def _unpack(buf, shape, dt):
+    """Packed buffer -> [E, n_out, n_in] through the documented layout."""
+    n_out, n_in, E = shape
+    idx = packed_index(n_out, n_in, E, dt)
+    return buf[idx]
+
+
+@pytest.mark.parametrize("shape", [(24, 40, 5), (32, 64, 3), (48, 96, 2)])
+def test_pack_bf16_bits(fm, shape):
     rng = np.random.default_rng(12)
-    w = (rng.standard_normal((24, 40, 5)) * 0.02).astype(np.float32)
+    w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
     p = fm.pack_expert_weights(w, "bf16")
-    got = p.data.view(torch.int16).view(5, 24, 40).cpu().numpy().view(np.uint16)
-    ref = nm.bf16_bits(w).transpose(2, 0, 1)
-    np.testing.assert_array_equal(got, ref)
+    buf = p.data.view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(_unpack(buf, shape, "bf16"), nm.bf16_bits(w).transpose(2, 0, 1))
 
 
-def test_pack_fp8_codes_and_scales(fm):
+@pytest.mark.parametrize("shape", [(24, 40, 5), (32, 128, 3), (16, 64, 2)])
+def test_pack_fp8_codes_and_scales(fm, shape):
     rng = np.random.default_rng(13)
-    w = (rng.standard_normal((24, 40, 5)) * 0.02).astype(np.float32)
-    w[3, :, 2] = 0.0
+    w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    w[3, :, 1] = 0.0
     w[4, 7, 1] = 1e-9  # subnormal after scaling
     p = fm.quantize_expert_weights(w)
     q, s = nm.quantize_per_channel_e4m3fn(w)
-    got_q = p.data.view(5, 24, 40).cpu().numpy()
-    np.testing.assert_array_equal(got_q, q.transpose(2, 0, 1))
+    np.testing.assert_array_equal(_unpack(p.data.cpu().numpy(), shape, "fp8"), q.transpose(2, 0, 1))
     np.testing.assert_array_equal(p.scales.cpu().numpy(), s.T)
 
 
 def test_pack_prequantized(fm):
     rng = np.random.default_rng(14)
-    w = (rng.standard_normal((8, 16, 3)) * 0.02).astype(np.float32)
+    shape = (32, 64, 3)
+    w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
     q, s = nm.quantize_per_channel_e4m3fn(w)
     p = fm.pack_expert_weights(fm.QuantizedExpertWeights(q, s))
-    np.testing.assert_array_equal(p.data.view(3, 8, 16).cpu().numpy(), q.transpose(2, 0, 1))
+    np.testing.assert_array_equal(_unpack(p.data.cpu().numpy(), shape, "fp8"), q.transpose(2, 0, 1))
     np.testing.assert_array_equal(p.scales.cpu().numpy(), s.T)
 
 
