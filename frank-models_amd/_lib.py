@@ -38,6 +38,7 @@ PATH_AUTO = 0
 PATH_GENERIC = 1
 PATH_TILED = 2
 PATH_STREAM = 3
+PATH_TILED_LARGE = 4
 
 
 # fmoe_timer

@@ -143,7 +143,14 @@ int run_grouped_gemm(const GroupedGemmArgs& g, hipStream_t s) {
   const bool can_tile = gemm_tiled_supported(g);
   const bool can_stream = gemm_stream_supported(g);
   int path = FMOE_PATH_GENERIC;
-  if (want == FMOE_PATH_TILED && can_tile)
+  int variant = TILED_AUTO;
+  if (want == FMOE_PATH_TILED_LARGE && gemm_tiled256_supported(g)) {
+    path = FMOE_PATH_TILED_LARGE;
+    variant = TILED_256;
+  } else if (want == FMOE_PATH_TILED && can_tile) {
+    path = FMOE_PATH_TILED;
+    variant = TILED_128;
+  } else if (want == FMOE_PATH_TILED_LARGE && can_tile)
     path = FMOE_PATH_TILED;
   else if (want == FMOE_PATH_STREAM && can_stream)
     path = FMOE_PATH_STREAM;
@@ -160,8 +167,8 @@ int run_grouped_gemm(const GroupedGemmArgs& g, hipStream_t s) {
       path = FMOE_PATH_STREAM;
   }
   hipError_t e;
-  if (path == FMOE_PATH_TILED)
-    e = launch_gemm_tiled(g, s);
+  if (path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE)
+    e = launch_gemm_tiled(g, s, variant);
   else if (path == FMOE_PATH_STREAM)
     e = launch_gemm_stream(g, s);
   else
@@ -267,7 +274,7 @@ int fmoe_device_check(int* device, char* arch, size_t arch_len) {
 }
 
 int fmoe_set_gemm_path(int path) {
-  if (path < FMOE_PATH_AUTO || path > FMOE_PATH_STREAM)
+  if (path < FMOE_PATH_AUTO || path > FMOE_PATH_TILED_LARGE)
     return fail(FMOE_ERR_INVALID_ARGUMENT, "unknown gemm path %d", path);
   g_path.store(path);
   return ok();
@@ -383,7 +390,9 @@ int fmoe_workspace_error_count(const void* workspace, void* stream, int64_t* cou
 
 size_t fmoe_packed_weight_bytes(int64_t n_out, int64_t n_in, int64_t n_expert, int dtype) {
   if (n_out < 0 || n_in < 0 || n_expert < 0 || !w_dtype_ok(dtype)) return 0;
-  return static_cast<size_t>(n_out) * n_in * n_expert * dtype_bytes(dtype);
+  // + a tail the tiled kernels may read (never use) past the last expert
+  return static_cast<size_t>(n_out) * n_in * n_expert * dtype_bytes(dtype) +
+         static_cast<size_t>(kPackedTailRows) * n_in * 2;
 }
 
 int fmoe_pack_expert_weights(const void* src, int src_dtype, const float* src_scales,

@@ -449,15 +449,20 @@ hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
 }  // namespace
 
 bool gemm_tiled_supported(const GroupedGemmArgs& g) {
-  return mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0;
+  return gemm_tiled256_supported(g) || (mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0);
 }
 
 bool gemm_stream_supported(const GroupedGemmArgs& g) {
   return mfma_common_ok(g) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0;
 }
 
-hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t s) {
-  if (!gemm_tiled_supported(g)) return hipErrorNotSupported;
+hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t s, int variant) {
+  const bool large_ok = gemm_tiled256_supported(g);
+  const bool small_ok = mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0;
+  if (variant == TILED_AUTO)
+    variant = (large_ok && static_cast<int64_t>(g.n_assign) >= 512ll * g.n_expert) ? TILED_256 : TILED_128;
+  if (variant == TILED_256 && large_ok) return launch_gemm_tiled256(g, s);
+  if (!small_ok) return large_ok ? launch_gemm_tiled256(g, s) : hipErrorNotSupported;
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
   // 96 KiB of dynamic LDS per block (gfx950 has 160 KiB per CU); set once per process.
   static const bool configured = [] {

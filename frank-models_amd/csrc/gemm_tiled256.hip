@@ -1,0 +1,274 @@
+// Large-tile MFMA grouped GEMM for gfx950 (bf16 activations x bf16 expert
+// weights in the WF_MFMA16 packed layout, fp32 accumulation).  This is the
+// prefill kernel of the MoE FFN block: mul_mat_id's per-assignment mat-vecs
+// (components/moe/mul_mat_id.mlir:55-94) batched per expert, the gate/up pair
+// fused with SwiGLU (components/activation/swiglu.mlir:37-47), the down
+// projection with the routing weight (moe_ffn_block.mlir:162-177).
+//
+// Tile: 256 assignment rows x 256 weight rows (gate/up: 128 + 128) per
+// 512-thread block; 4x2 waves, each 64 x 128 = 4 x 8 v_mfma_f32_16x16x32_bf16
+// tiles, 128 fp32 accumulators per lane (AGPRs).  Two waves per SIMD, so one
+// wave's LDS reads overlap the other's MFMAs.  Per 32-input stage a wave reads
+// 12 fragments (12 KiB) from LDS for 32 MFMAs.
+//
+// Pipeline: a 4-deep LDS ring of 32-input stages (32 KiB each: 256 token rows
+// x 64 B + 16 weight blocks x 1 KiB).  Global data goes straight to LDS
+// (global_load_lds_dwordx4, no staging registers), three stages ahead of the
+// stage being multiplied, so HBM latency hides behind ~3000 cycles of MFMA.
+// Fragments of stage k+1 are read from LDS while stage k's MFMAs run.  One
+// barrier per stage.
+//
+// LDS layouts: weight blocks are copied as packed (lane-ordered 1 KiB blocks,
+// conflict-free 16-byte reads); token rows are 64 B with the 16-byte chunk
+// index XORed by ((row >> 1) & 3) so the 8 lanes of an LDS read phase hit 8
+// distinct bank groups.
+#include "common.h"
+#include "launch.h"
+
+namespace fmoe {
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kBM = 256;
+constexpr int kBN = 256;   // weight rows per tile over all sets
+constexpr int kBK = 32;    // inputs per stage
+constexpr int kStages = 4;
+constexpr int kAStage = kBM * kBK * 2;       // 16 KiB
+constexpr int kBStage = (kBN / 16) * 1024;   // 16 KiB
+constexpr int kStage = kAStage + kBStage;    // 32 KiB
+constexpr int kLds = kStages * kStage;       // 128 KiB
+constexpr int kGroupN = 4;                   // column tiles swept together
+
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g * (u / (1.f + __expf(-u))); }
+
+__device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
+  if (g.a_mode == A_GATHER_TOKEN) return g.order[p] % g.n_tokens;
+  if (g.a_mode == A_GATHER_FLAT) return g.order[p];
+  return p;
+}
+
+// Hardware block b runs on XCD b % 8.  Logical tiles are dealt so that each
+// XCD owns a contiguous range, swept kGroupN column tiles at a time over all
+// row tiles: the row tiles of one expert that share a column tile's weights
+// run side by side on one XCD and share its L2.
+__device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, int* row_tile, int* col_tile) {
+  const int total = n_row_tiles * n_col_tiles;
+  const int per_xcd = (total + 7) / 8;
+  const int b = blockIdx.x;
+  const int logical = (b % 8) * per_xcd + b / 8;
+  if (logical >= total) return false;
+  const int group_span = kGroupN * n_row_tiles;
+  const int group = logical / group_span;
+  const int within = logical - group * group_span;
+  const int cols_in_group = min(kGroupN, n_col_tiles - group * kGroupN);
+  *row_tile = within / cols_in_group;
+  *col_tile = group * kGroupN + within % cols_in_group;
+  return true;
+}
+
+template <int EPI>
+__device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t n, float v0, float v1, float v2,
+                                       float v3) {
+  if (EPI == EPI_SWIGLU || g.out_dtype == DT_BF16) {
+    int64_t row = p;
+    if (EPI != EPI_SWIGLU) row = g.order[p];
+    if (EPI == EPI_SCATTER_WEIGHTED) {
+      const float w = g.route_w[row];
+      v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+    }
+    const u32x2_t pk{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+    *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(g.out) + row * g.ldo + n) = pk;
+  } else {
+    const int64_t row = g.order[p];
+    if (EPI == EPI_SCATTER_WEIGHTED) {
+      const float w = g.route_w[row];
+      v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+    }
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(g.out) + row * g.ldo + n) = f32x4_t{v0, v1, v2, v3};
+  }
+}
+
+template <int EPI, int NSETS>
+__global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmArgs g, int n_row_tiles,
+                                                                     int n_col_tiles) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+
+  int row_tile, col_tile;
+  if (!logical_tile(n_row_tiles, n_col_tiles, &row_tile, &col_tile)) return;
+  TileInfo ti;
+  if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1;  // rows wm*64 .. +64
+  const int wn = wave & 1;   // weight rows of each set: wn half
+  const int64_t N = g.N, K = g.K;
+  const int64_t n0 = static_cast<int64_t>(col_tile) * (kBN / NSETS);
+  const int64_t nblocks = N / 16;
+  const int64_t kblocks = K / 32;
+  const int KT = static_cast<int>(kblocks);
+
+  // ---- global -> LDS sources.  Token rows: this wave stages rows
+  // (wave*2 + j)*16 + (lane >> 2), 16-byte physical chunk (lane & 3), which
+  // holds logical chunk (lane & 3) ^ ((lane >> 3) & 3).  Byte offsets from
+  // the A base fit 32 bits (checked on the host).
+  const unsigned char* a_base = static_cast<const unsigned char*>(g.a);
+  uint32_t a_off[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = (wave * 2 + j) * 16 + (lane >> 2);
+    const int p = ti.row0 + (r < ti.rows ? r : 0);
+    const int c = (lane & 3) ^ ((lane >> 3) & 3);
+    a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + c * 16);
+  }
+  // Weight blocks: this wave stages row blocks wave*2 + j of the stage (wave
+  // uniform addresses).  The packed buffer has a 256-row tail, so row blocks
+  // past N stay in bounds (their columns are never stored).
+  const unsigned char* b_base[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int rb = wave * 2 + j;
+    const int set = NSETS == 2 ? rb >> 3 : 0;
+    const int64_t nb = n0 / 16 + (NSETS == 2 ? (rb & 7) : rb);
+    const unsigned char* w = static_cast<const unsigned char*>(set == 0 ? g.w0 : g.w1);
+    b_base[j] = w + (static_cast<int64_t>(ti.expert) * nblocks + nb) * kblocks * 1024;
+  }
+  const uint32_t b_lane = lane * 16;
+
+  auto issue_stage = [&](int kt, int buf) __attribute__((always_inline)) {
+    unsigned char* st = lds + buf * kStage;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds(a_base + (a_off[j] + kt * 64), st + (wave * 2 + j) * 1024, 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds(b_base[j] + (static_cast<uint32_t>(kt) * 1024 + b_lane),
+                                       st + kAStage + (wave * 2 + j) * 1024, 16, 0, 0);
+  };
+
+  // ---- fragment reads
+  const int a_lane = (lane & 15) * 64 + ((((lane >> 4) ^ (((lane & 15) >> 1) & 3))) << 4);
+  auto read_frags = [&](int buf, u32x4_t* fa, u32x4_t* fb) __attribute__((always_inline)) {
+    const unsigned char* st = lds + buf * kStage;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      fa[m] = *reinterpret_cast<const u32x4_t*>(st + (wm * 64 + m * 16) * 64 + a_lane);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int rb = NSETS == 2 ? ((n >> 2) * 8 + wn * 4 + (n & 3)) : (wn * 8 + n);
+      fb[n] = *reinterpret_cast<const u32x4_t*>(st + kAStage + rb * 1024 + lane * 16);
+    }
+  };
+
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[n][m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: stages 0..3 in flight (4 loads per wave each); wait for 0 and 1.
+#pragma unroll
+  for (int s = 0; s < kStages; ++s) issue_stage(s < KT ? s : KT - 1, s);
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+  u32x4_t fa0[4], fb0[8], fa1[4], fb1[8];
+  read_frags(0, fa0, fb0);
+
+  // One iteration = two stages (KT is even), so the two fragment sets swap
+  // roles without register copies.  Per stage kt:
+  //   read stage kt+1's fragments (it became visible at the last barrier),
+  //   refill the buffer stage kt came from with stage kt+4 (clamped: the
+  //   tail re-reads the last stage into idle buffers, keeping the wait
+  //   count constant), multiply stage kt, wait until only the 8 loads of
+  //   stages kt+3 and kt+4 are outstanding (stage kt+2 has landed), barrier.
+  for (int kt = 0; kt < KT; kt += 2) {
+    read_frags((kt + 1) & 3, fa1, fb1);
+    issue_stage(kt + 4 < KT ? kt + 4 : KT - 1, kt & 3);
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[n][m] = mfma16(fb0[n], fa0[m], acc[n][m]);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+
+    read_frags((kt + 2) & 3, fa0, fb0);
+    issue_stage(kt + 5 < KT ? kt + 5 : KT - 1, (kt + 1) & 3);
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[n][m] = mfma16(fb1[n], fa1[m], acc[n][m]);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue: lane holds assignment row (lane & 15) of each 16-row
+  // group and 4 consecutive weight rows 4*(lane >> 4) .. +4.
+  const int64_t e = ti.expert;
+  (void)e;
+#pragma unroll
+  for (int n = 0; n < (NSETS == 2 ? 4 : 8); ++n) {
+    const int64_t col = n0 + (NSETS == 2 ? wn * 64 : wn * 128) + n * 16 + 4 * (lane >> 4);
+    if (col >= N) continue;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int r = wm * 64 + m * 16 + (lane & 15);
+      if (r >= ti.rows) continue;
+      const int p = ti.row0 + r;
+      const f32x4_t a0 = acc[n][m];
+      if (EPI == EPI_SWIGLU) {
+        const f32x4_t a1 = acc[n + 4][m];
+        store4<EPI>(g, p, col, silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]),
+                    silu_mul(a0[3], a1[3]));
+      } else {
+        store4<EPI>(g, p, col, a0[0], a0[1], a0[2], a0[3]);
+      }
+    }
+  }
+}
+
+template <int EPI, int NSETS>
+hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
+  static const bool configured = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    (void)hipGetLastError();
+    return true;
+  }();
+  (void)configured;
+  const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
+  const int col_tiles = static_cast<int>((g.N + kBN / NSETS - 1) / (kBN / NSETS));
+  const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles;
+  const unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
+  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS>), dim3(blocks), dim3(kThreads), kLds, s, g, row_tiles,
+                     col_tiles);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
+  if (g.act_dtype != DT_BF16 || g.w_dtype != DT_BF16 || g.w_format != WF_MFMA16) return false;
+  if (g.K <= 0 || g.K % (2 * kBK) || g.N % 16 || g.lda % 8 || g.ldo % 4) return false;
+  // 32-bit byte offsets of A rows
+  const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;
+  if (a_rows * g.lda * 2 >= (int64_t(1) << 32)) return false;
+  if (g.epi == EPI_SWIGLU && (g.out_dtype != DT_BF16 || !g.w1)) return false;
+  if (reinterpret_cast<uintptr_t>(g.a) % 16 || reinterpret_cast<uintptr_t>(g.out) % 16) return false;
+  return true;
+}
+
+hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t s) {
+  if (!gemm_tiled256_supported(g)) return hipErrorNotSupported;
+  if (g.n_assign == 0 || g.N == 0) return hipSuccess;
+  if (g.epi == EPI_SWIGLU) return launch_t<EPI_SWIGLU, 2>(g, s);
+  if (g.epi == EPI_SCATTER_WEIGHTED) return launch_t<EPI_SCATTER_WEIGHTED, 1>(g, s);
+  return launch_t<EPI_SCATTER, 1>(g, s);
+}
+
+}  // namespace fmoe

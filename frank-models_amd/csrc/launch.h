@@ -31,6 +31,11 @@ __host__ __device__ inline int packed_format(int64_t n_out, int64_t n_in, int dt
   return WF_ROWMAJOR;
 }
 
+// Packed buffers end with a tail of kPackedTailRows rows x n_in inputs (at
+// the widest element size) that tiled kernels may read past the last expert
+// instead of guarding partial column tiles; its contents are never used.
+constexpr int64_t kPackedTailRows = 256;
+
 // Element offset of weight (e, n, k) in a packed buffer of n_out = N, n_in = K.
 __host__ __device__ inline int64_t packed_offset(int fmt, int dtype, int64_t e, int64_t n, int64_t k,
                                                  int64_t N, int64_t K) {
@@ -106,10 +111,16 @@ hipError_t launch_pack(const void* src, int src_dtype, const float* src_scales,
 hipError_t launch_gemm_generic(const GroupedGemmArgs& g, hipStream_t stream);
 // Returns hipErrorNotSupported when the shape or dtype is outside what the
 // MFMA kernels handle; the caller then uses the generic kernel.
-hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t stream);
+enum TiledVariant { TILED_AUTO = 0, TILED_128 = 1, TILED_256 = 2 };
+// TILED_AUTO picks 256x256 tiles when experts average >= 512 rows.
+hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t stream, int variant);
 hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t stream);
 bool gemm_tiled_supported(const GroupedGemmArgs& g);
 bool gemm_stream_supported(const GroupedGemmArgs& g);
+// 256x256-tile bf16 kernel (gemm_tiled256.hip); launch_gemm_tiled uses it
+// when it applies.
+bool gemm_tiled256_supported(const GroupedGemmArgs& g);
+hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t stream);
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
                          int dtype, hipStream_t stream);

@@ -56,8 +56,9 @@ typedef enum fmoe_dtype {
 typedef enum fmoe_gemm_path {
   FMOE_PATH_AUTO = 0,
   FMOE_PATH_GENERIC = 1, /* SIMT grouped GEMM, any shape and dtype */
-  FMOE_PATH_TILED = 2,   /* MFMA tiled grouped GEMM (prefill-sized batches) */
-  FMOE_PATH_STREAM = 3   /* MFMA weight-streaming grouped GEMM (decode) */
+  FMOE_PATH_TILED = 2,   /* MFMA tiled grouped GEMM, 128-row tiles */
+  FMOE_PATH_STREAM = 3,  /* MFMA weight-streaming grouped GEMM (decode) */
+  FMOE_PATH_TILED_LARGE = 4 /* MFMA tiled grouped GEMM, 256x256 tiles (prefill) */
 } fmoe_gemm_path;
 
 /* Message describing the last failure on this thread ("" if none). */
@@ -141,8 +142,10 @@ int fmoe_workspace_error_count(const void *workspace, void *stream,
  * [n_out, n_in, E] -> [E, n_out, n_in] of mul_mat_id.mlir:37-48.
  *   src [n_out, n_in, n_expert] in src_dtype (F32, BF16, or F8E4M3FN codes)
  *   src_scales [n_out, n_expert] float32: required iff src_dtype == F8E4M3FN
- *   dst: fmoe_packed_weight_bytes(n_out, n_in, n_expert, dst_dtype) bytes,
- *        per-expert [n_out, n_in] rows, n_in contiguous, in dst_dtype
+ *   dst: fmoe_packed_weight_bytes(n_out, n_in, n_expert, dst_dtype) bytes:
+ *        per-expert [n_out, n_in] weights in dst_dtype, in an internal
+ *        layout that depends only on (n_out, n_in, dtype), followed by a
+ *        tail the kernels may read but never use
  *   dst_scales [n_expert, n_out] float32: required iff dst_dtype == F8E4M3FN.
  * F32/BF16 -> F8E4M3FN quantises each output channel with
  * scale = absmax/448 (1 for an all-zero channel), code = RNE(w/scale),

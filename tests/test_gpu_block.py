@@ -21,11 +21,12 @@ from helpers import assert_close_rms
 
 pytestmark = pytest.mark.gpu
 
-PATHS = ["auto", "generic", "tiled", "stream"]
+PATHS = ["auto", "generic", "tiled", "stream", "tiled_large"]
 
 
 def _set_path(ll, name):
-    code = {"auto": ll.PATH_AUTO, "generic": ll.PATH_GENERIC, "tiled": ll.PATH_TILED, "stream": ll.PATH_STREAM}[name]
+    code = {"auto": ll.PATH_AUTO, "generic": ll.PATH_GENERIC, "tiled": ll.PATH_TILED, "stream": ll.PATH_STREAM,
+            "tiled_large": ll.PATH_TILED_LARGE}[name]
     ll.check(ll.lib().fmoe_set_gemm_path(code))
 
 
