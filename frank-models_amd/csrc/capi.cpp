@@ -121,11 +121,11 @@ class ScopedTimer {
     std::lock_guard<std::mutex> lk(g_t_mu);
     start_ = take_event();
     stop_ = take_event();
-    if (start_ && stop_) hipEventRecord(start_, s_);
+    if (start_ && stop_) (void)hipEventRecord(start_, s_);
   }
   ~ScopedTimer() {
     if (!start_ || !stop_) return;
-    hipEventRecord(stop_, s_);
+    (void)hipEventRecord(stop_, s_);
     std::lock_guard<std::mutex> lk(g_t_mu);
     g_pending.push_back({timer_, start_, stop_});
   }
@@ -138,25 +138,27 @@ class ScopedTimer {
 
 // Runs one grouped GEMM on the family the process-wide setting asks for,
 // falling back to the automatic choice when that family cannot run it.
-int run_grouped_gemm(const GroupedGemmArgs& g, hipStream_t s) {
+// `g.split_stride` > 0 offers room for a K split into fp32 partials; the
+// split used is returned in *ksplit_used (1 if none).
+int run_grouped_gemm(GroupedGemmArgs g, hipStream_t s, int* ksplit_used = nullptr) {
   const int want = g_path.load(std::memory_order_relaxed);
-  const bool can_tile = gemm_tiled_supported(g);
-  const bool can_stream = gemm_stream_supported(g);
+  GroupedGemmArgs probe = g;
+  probe.ksplit = 1;
+  const bool can_tile = resolve_tiled_variant(probe, TILED_AUTO) >= 0;
+  const bool can_stream = gemm_stream_supported(probe);
   int path = FMOE_PATH_GENERIC;
   int variant = TILED_AUTO;
-  if (want == FMOE_PATH_TILED_LARGE && gemm_tiled256_supported(g)) {
+  if (want == FMOE_PATH_TILED_LARGE && gemm_tiled256_supported(probe)) {
     path = FMOE_PATH_TILED_LARGE;
     variant = TILED_256;
-  } else if (want == FMOE_PATH_TILED && can_tile) {
+  } else if ((want == FMOE_PATH_TILED || want == FMOE_PATH_TILED_LARGE) && can_tile) {
     path = FMOE_PATH_TILED;
-    variant = TILED_128;
-  } else if (want == FMOE_PATH_TILED_LARGE && can_tile)
-    path = FMOE_PATH_TILED;
-  else if (want == FMOE_PATH_STREAM && can_stream)
+    variant = want == FMOE_PATH_TILED ? TILED_128 : TILED_AUTO;
+  } else if (want == FMOE_PATH_STREAM && can_stream) {
     path = FMOE_PATH_STREAM;
-  else if (want == FMOE_PATH_GENERIC)
+  } else if (want == FMOE_PATH_GENERIC) {
     path = FMOE_PATH_GENERIC;
-  else {
+  } else {
     // Few rows per expert: stream the weights once; otherwise tile.
     const bool small = static_cast<int64_t>(g.n_assign) <= 16ll * g.n_expert;
     if (small && can_stream)
@@ -166,6 +168,11 @@ int run_grouped_gemm(const GroupedGemmArgs& g, hipStream_t s) {
     else if (can_stream)
       path = FMOE_PATH_STREAM;
   }
+  g.ksplit = 1;
+  if (path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE) {
+    variant = resolve_tiled_variant(probe, variant);
+    if (variant == TILED_256 && g.split_stride > 0) g.ksplit = gemm_tiled256_ksplit(g);
+  }
   hipError_t e;
   if (path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE)
     e = launch_gemm_tiled(g, s, variant);
@@ -174,6 +181,7 @@ int run_grouped_gemm(const GroupedGemmArgs& g, hipStream_t s) {
   else
     e = launch_gemm_generic(g, s);
   g_last_path = path;
+  if (ksplit_used) *ksplit_used = g.ksplit;
   if (e != hipSuccess) return fail(FMOE_ERR_HIP, "grouped GEMM launch: %s", hipGetErrorString(e));
   return FMOE_OK;
 }
@@ -220,9 +228,32 @@ struct BlockLayout {
   PermuteLayout perm;
   size_t h, y, total;
   int h_dtype, y_dtype;
+  int y_parts;           // fp32 partial buffers reserved for a K-split down GEMM
+  int64_t y_part_elems;  // elements per partial
 };
 
-BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act) {
+// Shape-only part of the down projection's GEMM arguments (the split
+// decision depends on nothing else).
+GroupedGemmArgs down_shape(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act, int wdt) {
+  GroupedGemmArgs d;
+  d.a_mode = A_DIRECT;
+  d.lda = F;
+  d.n_tokens = static_cast<int>(T);
+  d.n_assign = static_cast<int>(T * k);
+  d.n_expert = static_cast<int>(E);
+  d.N = H;
+  d.K = F;
+  d.ldo = H;
+  d.epi = EPI_SCATTER_WEIGHTED;
+  d.act_dtype = act;
+  d.w_dtype = wdt;
+  d.w_format = packed_format(H, F, wdt);
+  d.out_dtype = FMOE_F32;
+  d.split_stride = 1;
+  return d;
+}
+
+BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act, int wdt) {
   BlockLayout L;
   const int64_t n = k * T;
   size_t off = 0;
@@ -236,8 +267,10 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   L.h = off;
   off += align_up(static_cast<size_t>(n) * F * dtype_bytes(L.h_dtype));
   L.y_dtype = FMOE_F32;
+  L.y_part_elems = n * H;
+  L.y_parts = (n > 0 && H > 0 && F > 0) ? gemm_tiled256_ksplit(down_shape(T, E, k, H, F, act, wdt)) : 1;
   L.y = off;
-  off += align_up(static_cast<size_t>(n) * H * dtype_bytes(L.y_dtype));
+  off += align_up(static_cast<size_t>(n) * H * dtype_bytes(L.y_dtype) * L.y_parts);
   L.total = off;
   return L;
 }
@@ -502,7 +535,7 @@ size_t fmoe_moe_ffn_block_workspace_bytes(int64_t n_tokens, int64_t n_expert,
   if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
       n_expert_used < 1 || n_embd < 1 || n_ff < 0)
     return 0;
-  return block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype).total;
+  return block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype).total;
 }
 
 int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* packed_up,
@@ -524,7 +557,7 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
     return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
   if (w_dtype == FMOE_F8E4M3FN && (!up_scales || !gate_scales || !down_scales))
     return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
-  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype);
+  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
   if (workspace_bytes < L.total)
     return fail(FMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, L.total);
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
@@ -609,16 +642,18 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
   d.w_dtype = w_dtype;
   d.w_format = packed_format(n_embd, n_ff, w_dtype);
   d.out_dtype = L.y_dtype;
+  d.split_stride = L.y_parts > 1 ? L.y_part_elems : 0;
+  int down_split = 1;
   {
     ScopedTimer t(FMOE_TIMER_DOWN, s);
-    FMOE_TRY(run_grouped_gemm(d, s));
+    FMOE_TRY(run_grouped_gemm(d, s, &down_split));
   }
 
   // Step 11: slot-ordered sum + transpose to [n_tokens, n_embd] (mlir:179-206).
   {
     ScopedTimer t(FMOE_TIMER_COMBINE, s);
     FMOE_HIP(launch_combine(y, L.y_dtype, out, act_dtype, T, static_cast<int>(n_expert_used),
-                            static_cast<int>(n_embd), s));
+                            static_cast<int>(n_embd), down_split, L.y_part_elems, s));
   }
   return ok();
 }
@@ -629,7 +664,7 @@ int fmoe_moe_ffn_block_routing(void* workspace, int64_t n_tokens, int64_t n_expe
                                int32_t** offsets) {
   if (!workspace) return fail(FMOE_ERR_INVALID_ARGUMENT, "null workspace");
   if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "dtype");
-  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype);
+  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
   if (ids) *ids = at<int32_t>(workspace, L.ids);
   if (weights) *weights = at<float>(workspace, L.weights);
   if (order) *order = at<int32_t>(workspace, L.perm.order);

@@ -43,17 +43,23 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const T* __restrict__ 
   }
 }
 
-// One thread per 4 consecutive columns when aligned, else per column.
+// out[t, c] = sum_s (y_0 + y_1 + ...)[s*T + t, c]: slots in order, K-split
+// partials summed first in split order.
 template <typename TY, typename TO>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const TY* __restrict__ y,
                                                            TO* __restrict__ out, int n_tokens,
-                                                           int k, int n_embd) {
+                                                           int k, int n_embd, int nsplit,
+                                                           int64_t split_stride) {
   const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
   const int64_t slot_stride = total;  // y rows s*T + t -> element offset s*T*H + t*H
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * kThreads) {
-    float acc = ldf(y, i);
-    for (int s = 1; s < k; ++s) acc += ldf(y, i + s * slot_stride);
+    float acc = 0.f;
+    for (int s = 0; s < k; ++s) {
+      float v = ldf(y, i + s * slot_stride);
+      for (int p = 1; p < nsplit; ++p) v += ldf(y, i + s * slot_stride + p * split_stride);
+      acc = s == 0 ? v : acc + v;
+    }
     stf(out, i, acc);
   }
 }
@@ -120,22 +126,26 @@ hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
 }
 
 hipError_t launch_combine(const void* y, int y_dtype, void* out, int out_dtype, int n_tokens,
-                          int k, int n_embd, hipStream_t stream) {
+                          int k, int n_embd, int nsplit, int64_t split_stride, hipStream_t stream) {
   const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
   if (total == 0) return hipSuccess;
   const dim3 grid(grid_for(total));
   if (y_dtype == DT_F32 && out_dtype == DT_F32)
     hipLaunchKernelGGL((combine_kernel<float, float>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const float*>(y), static_cast<float*>(out), n_tokens, k, n_embd);
+                       static_cast<const float*>(y), static_cast<float*>(out), n_tokens, k, n_embd, nsplit,
+                       split_stride);
   else if (y_dtype == DT_F32)
     hipLaunchKernelGGL((combine_kernel<float, bf16_t>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const float*>(y), static_cast<bf16_t*>(out), n_tokens, k, n_embd);
+                       static_cast<const float*>(y), static_cast<bf16_t*>(out), n_tokens, k, n_embd, nsplit,
+                       split_stride);
   else if (out_dtype == DT_F32)
     hipLaunchKernelGGL((combine_kernel<bf16_t, float>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const bf16_t*>(y), static_cast<float*>(out), n_tokens, k, n_embd);
+                       static_cast<const bf16_t*>(y), static_cast<float*>(out), n_tokens, k, n_embd, nsplit,
+                       split_stride);
   else
     hipLaunchKernelGGL((combine_kernel<bf16_t, bf16_t>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const bf16_t*>(y), static_cast<bf16_t*>(out), n_tokens, k, n_embd);
+                       static_cast<const bf16_t*>(y), static_cast<bf16_t*>(out), n_tokens, k, n_embd, nsplit,
+                       split_stride);
   return hipGetLastError();
 }
 

@@ -23,7 +23,7 @@
 //           share weight rows run on the same XCD (same L2).
 //   stream  decode-sized batches: every weight block is read exactly once
 //           straight into MFMA registers (no LDS), 16 assignment rows per
-//           pass, 4 input steps of loads in flight per wave.
+//           pass, 8 input steps of loads in flight per wave.
 #include "common.h"
 #include "launch.h"
 
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled_kernel(GroupedGemmArgs
 // ======================================================================= stream
 constexpr int kStreamRowsPerWave = 16;
 constexpr int kStreamRows = 4 * kStreamRowsPerWave;  // weight rows per set per block
-constexpr int kStreamUnroll = 4;                     // 32-input steps per iteration
+constexpr int kStreamUnroll = 8;                     // 32-input steps per iteration
 
 template <int EPI, int NSETS, bool F8>
 __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
@@ -456,13 +456,20 @@ bool gemm_stream_supported(const GroupedGemmArgs& g) {
   return mfma_common_ok(g) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0;
 }
 
-hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t s, int variant) {
+int resolve_tiled_variant(const GroupedGemmArgs& g, int variant) {
   const bool large_ok = gemm_tiled256_supported(g);
-  const bool small_ok = mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0;
+  const bool small_ok = mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0 && g.ksplit == 1;
   if (variant == TILED_AUTO)
     variant = (large_ok && static_cast<int64_t>(g.n_assign) >= 512ll * g.n_expert) ? TILED_256 : TILED_128;
-  if (variant == TILED_256 && large_ok) return launch_gemm_tiled256(g, s);
-  if (!small_ok) return large_ok ? launch_gemm_tiled256(g, s) : hipErrorNotSupported;
+  if (variant == TILED_256 && large_ok) return TILED_256;
+  if (small_ok) return TILED_128;
+  return large_ok ? TILED_256 : -1;
+}
+
+hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t s, int variant) {
+  const int v = resolve_tiled_variant(g, variant);
+  if (v == TILED_256) return launch_gemm_tiled256(g, s);
+  if (v != TILED_128) return hipErrorNotSupported;
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
   // 96 KiB of dynamic LDS per block (gfx950 has 160 KiB per CU); set once per process.
   static const bool configured = [] {

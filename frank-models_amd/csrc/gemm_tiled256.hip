@@ -46,6 +46,13 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g * (u / (1.f + __expf(-u))); }
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8; a field at its maximum does not wait).  Issued through the
+// builtin so the compiler's own wait insertion accounts for them.
+constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
+constexpr int kWaitVm8 = 0x0F70 | 8;                // vmcnt(8)
+constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
+
 __device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
   if (g.a_mode == A_GATHER_TOKEN) return g.order[p] % g.n_tokens;
   if (g.a_mode == A_GATHER_FLAT) return g.order[p];
@@ -56,12 +63,18 @@ __device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
 // XCD owns a contiguous range, swept kGroupN column tiles at a time over all
 // row tiles: the row tiles of one expert that share a column tile's weights
 // run side by side on one XCD and share its L2.
-__device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, int* row_tile, int* col_tile) {
-  const int total = n_row_tiles * n_col_tiles;
+// With a K split, the split index is the slowest-varying part of the
+// logical id.
+__device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, int ksplit, int* row_tile,
+                                             int* col_tile, int* split) {
+  const int per_split = n_row_tiles * n_col_tiles;
+  const int total = per_split * ksplit;
   const int per_xcd = (total + 7) / 8;
   const int b = blockIdx.x;
-  const int logical = (b % 8) * per_xcd + b / 8;
+  int logical = (b % 8) * per_xcd + b / 8;
   if (logical >= total) return false;
+  *split = logical / per_split;
+  logical -= *split * per_split;
   const int group_span = kGroupN * n_row_tiles;
   const int group = logical / group_span;
   const int within = logical - group * group_span;
@@ -72,8 +85,8 @@ __device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, i
 }
 
 template <int EPI>
-__device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t n, float v0, float v1, float v2,
-                                       float v3) {
+__device__ __forceinline__ void store4(const GroupedGemmArgs& g, int split, int p, int64_t n, float v0, float v1,
+                                       float v2, float v3) {
   if (EPI == EPI_SWIGLU || g.out_dtype == DT_BF16) {
     int64_t row = p;
     if (EPI != EPI_SWIGLU) row = g.order[p];
@@ -89,7 +102,26 @@ __device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t 
       const float w = g.route_w[row];
       v0 *= w, v1 *= w, v2 *= w, v3 *= w;
     }
-    *reinterpret_cast<f32x4_t*>(static_cast<float*>(g.out) + row * g.ldo + n) = f32x4_t{v0, v1, v2, v3};
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(g.out) + split * g.split_stride + row * g.ldo + n) =
+        f32x4_t{v0, v1, v2, v3};
+  }
+}
+
+// Instruction order within one stage: the 12 fragment reads of the next
+// stage and the 4 global->LDS loads of a later stage are spread between this
+// stage's 32 MFMAs (1 read, 2 MFMAs; then 1 load, 2 MFMAs), so the LDS and
+// memory pipes work while the matrix cores do.  Masks: 0x100 DS read,
+// 0x010 VMEM, 0x008 MFMA.
+__device__ __forceinline__ void stage_schedule() {
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   }
 }
 
@@ -98,8 +130,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
                                                                      int n_col_tiles) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
 
-  int row_tile, col_tile;
-  if (!logical_tile(n_row_tiles, n_col_tiles, &row_tile, &col_tile)) return;
+  int row_tile, col_tile, split;
+  if (!logical_tile(n_row_tiles, n_col_tiles, g.ksplit, &row_tile, &col_tile, &split)) return;
   TileInfo ti;
   if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
 
@@ -111,7 +143,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   const int64_t n0 = static_cast<int64_t>(col_tile) * (kBN / NSETS);
   const int64_t nblocks = N / 16;
   const int64_t kblocks = K / 32;
-  const int KT = static_cast<int>(kblocks);
+  // This block's share of K: stages [k_first, k_first + KT) of 32 inputs.
+  const int KT = static_cast<int>(kblocks / g.ksplit);
+  const int k_first = split * KT;
 
   // ---- global -> LDS sources.  Token rows: this wave stages rows
   // (wave*2 + j)*16 + (lane >> 2), 16-byte physical chunk (lane & 3), which
@@ -124,7 +158,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     const int r = (wave * 2 + j) * 16 + (lane >> 2);
     const int p = ti.row0 + (r < ti.rows ? r : 0);
     const int c = (lane & 3) ^ ((lane >> 3) & 3);
-    a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + c * 16);
+    a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + c * 16 + k_first * 64);
   }
   // Weight blocks: this wave stages row blocks wave*2 + j of the stage (wave
   // uniform addresses).  The packed buffer has a 256-row tail, so row blocks
@@ -136,7 +170,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     const int set = NSETS == 2 ? rb >> 3 : 0;
     const int64_t nb = n0 / 16 + (NSETS == 2 ? (rb & 7) : rb);
     const unsigned char* w = static_cast<const unsigned char*>(set == 0 ? g.w0 : g.w1);
-    b_base[j] = w + (static_cast<int64_t>(ti.expert) * nblocks + nb) * kblocks * 1024;
+    b_base[j] = w + ((static_cast<int64_t>(ti.expert) * nblocks + nb) * kblocks + k_first) * 1024;
   }
   const uint32_t b_lane = lane * 16;
 
@@ -174,7 +208,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   // Prologue: stages 0..3 in flight (4 loads per wave each); wait for 0 and 1.
 #pragma unroll
   for (int s = 0; s < kStages; ++s) issue_stage(s < KT ? s : KT - 1, s);
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitVm8);
   asm volatile("s_barrier" ::: "memory");
   u32x4_t fa0[4], fb0[8], fa1[4], fb1[8];
   read_frags(0, fa0, fb0);
@@ -186,26 +220,37 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   //   tail re-reads the last stage into idle buffers, keeping the wait
   //   count constant), multiply stage kt, wait until only the 8 loads of
   //   stages kt+3 and kt+4 are outstanding (stage kt+2 has landed), barrier.
+  // sched_barrier(0) keeps each stage's instructions between its barriers;
+  // stage_schedule() orders them inside.  This stage's MFMA operands are
+  // already in registers, so the next stage's LDS reads overlap the MFMAs.
   for (int kt = 0; kt < KT; kt += 2) {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this stage's fragments (read a stage ago)
     read_frags((kt + 1) & 3, fa1, fb1);
     issue_stage(kt + 4 < KT ? kt + 4 : KT - 1, kt & 3);
 #pragma unroll
     for (int n = 0; n < 8; ++n)
 #pragma unroll
       for (int m = 0; m < 4; ++m) acc[n][m] = mfma16(fb0[n], fa0[m], acc[n][m]);
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    stage_schedule();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm8);
     asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     read_frags((kt + 2) & 3, fa0, fb0);
     issue_stage(kt + 5 < KT ? kt + 5 : KT - 1, (kt + 1) & 3);
 #pragma unroll
     for (int n = 0; n < 8; ++n)
 #pragma unroll
       for (int m = 0; m < 4; ++m) acc[n][m] = mfma16(fb1[n], fa1[m], acc[n][m]);
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    stage_schedule();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm8);
     asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
   // ---- epilogue: lane holds assignment row (lane & 15) of each 16-row
   // group and 4 consecutive weight rows 4*(lane >> 4) .. +4.
@@ -223,10 +268,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
       const f32x4_t a0 = acc[n][m];
       if (EPI == EPI_SWIGLU) {
         const f32x4_t a1 = acc[n + 4][m];
-        store4<EPI>(g, p, col, silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]),
+        store4<EPI>(g, split, p, col, silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]),
                     silu_mul(a0[3], a1[3]));
       } else {
-        store4<EPI>(g, p, col, a0[0], a0[1], a0[2], a0[3]);
+        store4<EPI>(g, split, p, col, a0[0], a0[1], a0[2], a0[3]);
       }
     }
   }
@@ -243,7 +288,7 @@ hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
   (void)configured;
   const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
   const int col_tiles = static_cast<int>((g.N + kBN / NSETS - 1) / (kBN / NSETS));
-  const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles;
+  const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles * g.ksplit;
   const unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
   hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS>), dim3(blocks), dim3(kThreads), kLds, s, g, row_tiles,
                      col_tiles);
@@ -252,9 +297,20 @@ hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
 
 }  // namespace
 
+int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
+  // Split K in two when the tiles would fill the 256 CUs fewer than ~4 times
+  // (the down projection at Mixtral shapes: 4096 outputs, 14336 inputs) and
+  // the caller provided room for fp32 partials.
+  if (g.epi != EPI_SCATTER_WEIGHTED || g.out_dtype != DT_F32 || g.split_stride == 0) return 1;
+  const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
+  const int64_t tiles = static_cast<int64_t>(row_tiles) * ((g.N + kBN - 1) / kBN);
+  if (tiles < 1024 && g.K % (4 * kBK) == 0 && g.K >= 2048) return 2;
+  return 1;
+}
+
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
   if (g.act_dtype != DT_BF16 || g.w_dtype != DT_BF16 || g.w_format != WF_MFMA16) return false;
-  if (g.K <= 0 || g.K % (2 * kBK) || g.N % 16 || g.lda % 8 || g.ldo % 4) return false;
+  if (g.K <= 0 || g.K % (2 * kBK * g.ksplit) || g.N % 16 || g.lda % 8 || g.ldo % 4) return false;
   // 32-bit byte offsets of A rows
   const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;
   if (a_rows * g.lda * 2 >= (int64_t(1) << 32)) return false;

@@ -88,6 +88,11 @@ struct GroupedGemmArgs {
   int w_dtype = DT_F32;
   int w_format = WF_ROWMAJOR;   // packed_format(N, K, w_dtype)
   int out_dtype = DT_F32;
+  // Split of K over ksplit partial products written to out + s * split_stride
+  // (s < ksplit).  Only the 256-tile kernel splits; launchers report the
+  // split they used.
+  int ksplit = 1;
+  int64_t split_stride = 0;
 };
 
 // Upper bound on the number of bm-row tiles of a grouping of n_assign rows
@@ -112,7 +117,9 @@ hipError_t launch_gemm_generic(const GroupedGemmArgs& g, hipStream_t stream);
 // Returns hipErrorNotSupported when the shape or dtype is outside what the
 // MFMA kernels handle; the caller then uses the generic kernel.
 enum TiledVariant { TILED_AUTO = 0, TILED_128 = 1, TILED_256 = 2 };
-// TILED_AUTO picks 256x256 tiles when experts average >= 512 rows.
+// The tiled kernel that `variant` resolves to for g (TILED_AUTO picks
+// 256x256 tiles when experts average >= 512 rows), or -1 if none applies.
+int resolve_tiled_variant(const GroupedGemmArgs& g, int variant);
 hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t stream, int variant);
 hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t stream);
 bool gemm_tiled_supported(const GroupedGemmArgs& g);
@@ -121,12 +128,16 @@ bool gemm_stream_supported(const GroupedGemmArgs& g);
 // when it applies.
 bool gemm_tiled256_supported(const GroupedGemmArgs& g);
 hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t stream);
+// K split the 256-tile kernel would use for g (1 when it does not apply).
+int gemm_tiled256_ksplit(const GroupedGemmArgs& g);
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
                          int dtype, hipStream_t stream);
-// out[t, :] = sum over s = 0..k-1 (in order) of y[s*n_tokens + t, :]
+// out[t, :] = sum over s = 0..k-1 (in order) of the K-split sum
+// (y_0 + y_1 + ...)[s*n_tokens + t, :], partials split_stride elements apart.
 hipError_t launch_combine(const void* y, int y_dtype, void* out, int out_dtype,
-                          int n_tokens, int k, int n_embd, hipStream_t stream);
+                          int n_tokens, int k, int n_embd, int nsplit, int64_t split_stride,
+                          hipStream_t stream);
 // out[c, r] = in[r, c] for an in[rows, cols] matrix (same dtype).
 hipError_t launch_transpose(const void* in, void* out, int64_t rows, int64_t cols,
                             int dtype, hipStream_t stream);

@@ -22,11 +22,13 @@ constexpr int kMfmaMaxExpert = 128;
 
 // Softmax + top-k + optional renormalisation of kTok tokens whose logits
 // are in lds_logits[kTok][ld].
+// The block's n_waves waves take tokens wave, wave + n_waves, ...
 __device__ void softmax_topk(const float* lds_logits, int ld, int tok0, int n_tokens,
-                             int n_expert, int k, bool normalize, int* ids, float* weights) {
+                             int n_expert, int k, bool normalize, int* ids, float* weights,
+                             int n_waves) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  for (int tt = wave; tt < kTok; tt += kThreads / kWave) {
+  for (int tt = wave; tt < kTok; tt += n_waves) {
     const int t = tok0 + tt;
     if (t >= n_tokens) break;
     float p[4];
@@ -124,18 +126,23 @@ __global__ __launch_bounds__(kThreads) void router_simt_kernel(
     lds[tt * ld + e] = acc;
   }
   __syncthreads();
-  softmax_topk(lds, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights);
+  softmax_topk(lds, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights, kThreads / kWave);
 }
 
-// MFMA logits for bf16 inputs, n_embd % 128 == 0, n_expert <= 128.
+// MFMA logits for bf16 inputs, n_embd % 32 == 0, n_expert <= 128.
 // v_mfma_f32_16x16x32_bf16 with A = 16 tokens x 32 hidden, B = 32 hidden x
-// 16 experts; the 4 waves split the hidden axis (wave w takes chunks
-// w, w+4, ...) and their partial logits are summed in wave order in LDS.
-__global__ __launch_bounds__(kThreads) void router_mfma_bf16_kernel(
+// 16 experts.  The 16 waves of the block split the hidden axis (wave w takes
+// 32-wide chunks w, w+16, ...), so a decode-sized batch still spreads its
+// dot products over a whole block; partial logits are summed in wave order.
+constexpr int kMfmaWaves = 16;
+constexpr int kMfmaThreads = kMfmaWaves * kWave;
+
+__global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, int n_tokens, int n_embd,
     int n_expert, int k, int normalize, int* __restrict__ ids, float* __restrict__ weights) {
-  __shared__ float part[4][kTok][kMfmaMaxExpert + 4];
-  __shared__ float logits[kTok][kMfmaMaxExpert + 1];
+  extern __shared__ float part[];  // [kMfmaWaves][kTok][ld], then logits [kTok][ld]
+  const int ld = ((n_expert + 15) / 16) * 16 + 1;
+  float* logits = part + kMfmaWaves * kTok * ld;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int tok0 = blockIdx.x * kTok;
@@ -149,38 +156,40 @@ __global__ __launch_bounds__(kThreads) void router_mfma_bf16_kernel(
   const int kofs = (lane >> 4) * 8;  // 8 consecutive hidden elements
   const int t = tok0 + row;
   const bool t_ok = t < n_tokens;
-  const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t_ok ? t : 0) * n_embd + kofs);
-  for (int h0 = wave * 32; h0 < n_embd; h0 += 4 * 32) {
-    uint4 av = t_ok ? xrow[h0 / 8] : uint4{0, 0, 0, 0};
+  const bf16_t* xrow = x + static_cast<int64_t>(t_ok ? t : 0) * n_embd + kofs;
+  for (int h0 = wave * 32; h0 < n_embd; h0 += kMfmaWaves * 32) {
+    const u32x4_t av = t_ok ? *reinterpret_cast<const u32x4_t*>(xrow + h0) : u32x4_t{0u, 0u, 0u, 0u};
     const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
 #pragma unroll
     for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
       if (c < n_chunks) {
         const int e = c * 16 + row;
-        uint4 bv = uint4{0, 0, 0, 0};
+        u32x4_t bv = u32x4_t{0u, 0u, 0u, 0u};
         if (e < n_expert)
-          bv = *reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(e) * n_embd + h0 + kofs);
+          bv = *reinterpret_cast<const u32x4_t*>(wr + static_cast<int64_t>(e) * n_embd + h0 + kofs);
         acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv), acc[c], 0, 0, 0);
       }
     }
   }
   // D[token][expert]: lane holds expert (lane & 15), tokens 4*(lane>>4)+i.
+  float* mine = part + wave * kTok * ld;
 #pragma unroll
   for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
     if (c < n_chunks) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part[wave][(lane >> 4) * 4 + i][c * 16 + (lane & 15)] = acc[c][i];
+      for (int i = 0; i < 4; ++i) mine[((lane >> 4) * 4 + i) * ld + c * 16 + (lane & 15)] = acc[c][i];
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < kTok * n_expert; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < kTok * n_expert; idx += kMfmaThreads) {
     const int tt = idx / n_expert;
     const int e = idx - tt * n_expert;
-    logits[tt][e] = ((part[0][tt][e] + part[1][tt][e]) + part[2][tt][e]) + part[3][tt][e];
+    float v = part[tt * ld + e];
+    for (int w = 1; w < kMfmaWaves; ++w) v += part[(w * kTok + tt) * ld + e];
+    logits[tt * ld + e] = v;
   }
   __syncthreads();
-  softmax_topk(&logits[0][0], kMfmaMaxExpert + 1, tok0, n_tokens, n_expert, k, normalize != 0, ids,
-               weights);
+  softmax_topk(logits, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights, kMfmaWaves);
 }
 
 }  // namespace
@@ -193,8 +202,17 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
   const dim3 grid((n_tokens + kTok - 1) / kTok);
   const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(wr) % 16 == 0);
-  if (dtype == DT_BF16 && n_embd % 128 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
-    hipLaunchKernelGGL(router_mfma_bf16_kernel, grid, dim3(kThreads), 0, stream,
+  if (dtype == DT_BF16 && n_embd % 32 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
+    const int ld = ((n_expert + 15) / 16) * 16 + 1;
+    const size_t lds = static_cast<size_t>(kMfmaWaves + 1) * kTok * ld * sizeof(float);
+    static const bool configured = [] {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(router_mfma_bf16_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      (void)hipGetLastError();
+      return true;
+    }();
+    (void)configured;
+    hipLaunchKernelGGL(router_mfma_bf16_kernel, grid, dim3(kMfmaThreads), lds, stream,
                        static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens,
                        n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
   } else {
