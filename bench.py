@@ -66,7 +66,10 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None):
         torch.cuda.synchronize()
         log(f"weights drawn in {time.perf_counter() - t0:.1f}s")
         t0 = time.perf_counter()
-        packed = [fm.pack_expert_weights(w) for w in dev_w]
+        if cfg.weights == "fp8":
+            packed = [fm.quantize_expert_weights(w) for w in dev_w]
+        else:
+            packed = [fm.pack_expert_weights(w) for w in dev_w]
         torch.cuda.synchronize()
         pack_s = time.perf_counter() - t0
         weights = (dev_w, packed, pack_s)
@@ -130,6 +133,32 @@ def cpu_baseline(torch, cfg, res, sample):
     }
 
 
+def all_configs(fm, wl, torch, args):
+    """Every BASELINE configuration and token count: ms/step, tokens/s, block
+    MFMA fraction (bf16/fp8 peak) and HBM fraction of the touched weights."""
+    rows = []
+    for name in ("C2", "C3", "C4", "C5"):
+        cfg = wl.CONFIGS[name]
+        H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
+        weights = None
+        for T in cfg.tokens:
+            res = run_config(fm, wl, torch, cfg, T, max(5, args.steps // 2), 2, weights=weights)
+            weights = res["weights"]
+            wb = 1 if cfg.weights == "fp8" else 2
+            flops = block_flops(T, H, F, E, k)
+            nbytes = block_bytes(T, H, F, E, k, res["touched"], wbytes=wb)
+            row = {"config": name, "tokens": T, "ms": res["ms"], "tokens_per_s": res["tok_s"],
+                   "mfma_frac": flops / (res["ms"] * 1e-3) / PEAK_BF16_FLOPS,
+                   "hbm_frac": nbytes / (res["ms"] * 1e-3) / PEAK_HBM_BYTES,
+                   "experts_touched": res["touched"], "kernels_ms": res["kernels"]}
+            rows.append(row)
+            log(f"{name} T={T:5d}: {res['ms']:.3f} ms  {res['tok_s']:.0f} tok/s  mfma {row['mfma_frac']:.3f}  "
+                f"hbm {row['hbm_frac']:.3f}  {res['kernels']}")
+        del weights
+        torch.cuda.empty_cache()
+    return rows
+
+
 def read_traffic(kernel_name):
     """HBM bytes per launch of `kernel_name` from a committed rocprofv3 PMC
     summary (profiles/pmc_<name>.json), or None."""
@@ -152,6 +181,8 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--all-configs", action="store_true",
+                    help="also time C3/C4/C5 at every token count (table on stderr, 'configs' in the JSON)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -217,6 +248,9 @@ def main():
             "kernels_ms": dec["kernels"],
         }
         log(f"decode {dec['ms']:.3f} ms/step, {result['decode']['hbm_frac']:.3f} of HBM peak")
+
+    if args.all_configs:
+        result["configs"] = all_configs(fm, wl, torch, args)
 
     if not args.no_cpu_baseline:
         log(f"cpu baseline on {args.cpu_sample} tokens")
