@@ -9,7 +9,10 @@
 // 512-thread block; 4x2 waves, each 64 x 128 = 4 x 8 v_mfma_f32_16x16x32_bf16
 // tiles, 128 fp32 accumulators per lane (AGPRs).  Two waves per SIMD, so one
 // wave's LDS reads overlap the other's MFMAs.  Per 32-input stage a wave reads
-// 12 fragments (12 KiB) from LDS for 32 MFMAs.
+// 12 fragments (12 KiB) from LDS for 32 MFMAs.  A wave's four 16-row groups
+// are interleaved (wm, wm+4, wm+8, wm+12), and a wave skips the reads and
+// MFMAs of groups past the expert's last row, so the last (partial) row tile
+// of an expert costs in proportion to its rows.
 //
 // Pipeline: a 4-deep LDS ring of 32-input stages (32 KiB each: 256 token rows
 // x 64 B + 16 weight blocks x 1 KiB).  Global data goes straight to LDS
@@ -51,6 +54,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g * (u / (1
 // builtin so the compiler's own wait insertion accounts for them.
 constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
 constexpr int kWaitVm8 = 0x0F70 | 8;                // vmcnt(8)
+constexpr int kWaitVm8Lgkm0 = 0x0070 | 8;           // vmcnt(8) lgkmcnt(0)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
 
 __device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
@@ -107,22 +111,136 @@ __device__ __forceinline__ void store4(const GroupedGemmArgs& g, int split, int 
   }
 }
 
-// Instruction order within one stage: the 12 fragment reads of the next
-// stage and the 4 global->LDS loads of a later stage are spread between this
-// stage's 32 MFMAs (1 read, 2 MFMAs; then 1 load, 2 MFMAs), so the LDS and
-// memory pipes work while the matrix cores do.  Masks: 0x100 DS read,
+// Instruction order within one stage of a wave with NM active 16-row groups:
+// the NM + 8 fragment reads of the next stage and the 4 global->LDS loads of
+// a later stage are spread between this stage's 8 * NM MFMAs, so the LDS and
+// memory pipes work while the matrix cores do.  A full wave (NM = 4) does
+// 12 x (1 read, 2 MFMAs) then 4 x (1 load, 2 MFMAs).  Masks: 0x100 DS read,
 // 0x010 VMEM, 0x008 MFMA.
+template <int NM>
 __device__ __forceinline__ void stage_schedule() {
+  if constexpr (NM == 4) {
 #pragma unroll
-  for (int i = 0; i < 12; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-  }
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+  } else if constexpr (NM > 0) {
+    // Loads first (they have the longest latency), then reads and MFMAs
+    // alternating; the MFMAs left over once the reads run out come last.
+    constexpr int kReads = NM + 8;
+    constexpr int kMfma = 8 * NM;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+#pragma unroll
+    for (int i = 0; i < kReads; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i < kMfma) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    if constexpr (kMfma > kReads) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kReads, 0);
   }
+}
+
+// Everything one wave needs to stage and read tiles: computed once per block.
+struct WaveCtx {
+  unsigned char* lds;
+  const unsigned char* a_base;
+  uint32_t a_off[2];           // byte offsets of this wave's two staged token rows
+  const unsigned char* b_base[2];  // this wave's two staged weight row blocks
+  uint32_t b_lane;
+  int a_lane;                  // LDS byte offset of this lane's A fragment in a 16-row group
+  int wave, wm, wn;
+  int KT;                      // stages of 32 inputs in this block's K range
+};
+
+template <int NSETS>
+__device__ __forceinline__ void issue_stage(const WaveCtx& c, int kt, int buf) {
+  unsigned char* st = c.lds + buf * kStage;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + kt * 64), st + (c.wave * 2 + j) * 1024, 16, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    __builtin_amdgcn_global_load_lds(c.b_base[j] + (static_cast<uint32_t>(kt) * 1024 + c.b_lane),
+                                     st + kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
+}
+
+// Fragment m of a wave covers 16-row group wm + 4 m of the tile, so the
+// groups of a partial tile are spread over all four SIMDs.
+template <int NM, int NSETS>
+__device__ __forceinline__ void read_frags(const WaveCtx& c, int buf, u32x4_t* fa, u32x4_t* fb) {
+  const unsigned char* st = c.lds + buf * kStage;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+    fa[m] = *reinterpret_cast<const u32x4_t*>(st + (c.wm + 4 * m) * 16 * 64 + c.a_lane);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int rb = NSETS == 2 ? ((n >> 2) * 8 + c.wn * 4 + (n & 3)) : (c.wn * 8 + n);
+    fb[n] = *reinterpret_cast<const u32x4_t*>(st + kAStage + rb * 1024 + c.b_lane);
+  }
+}
+
+// The pipelined K loop of one wave with NM active 16-row groups (0..4).
+// Every wave stages its share of every stage and joins every barrier; only
+// the fragment reads and MFMAs depend on NM.
+template <int NM, int NSETS>
+__device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
+  const int KT = c.KT;
+  // Prologue: stages 0..3 in flight (4 loads per wave each); wait for 0 and 1.
+#pragma unroll
+  for (int s = 0; s < kStages; ++s) issue_stage<NSETS>(c, s < KT ? s : KT - 1, s);
+  __builtin_amdgcn_s_waitcnt(kWaitVm8);
+  asm volatile("s_barrier" ::: "memory");
+  u32x4_t fa0[4], fb0[8], fa1[4], fb1[8];
+  if constexpr (NM > 0) read_frags<NM, NSETS>(c, 0, fa0, fb0);
+  // Stage 0 refills buffer 0: every wave's reads of it must be done first.
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  asm volatile("s_barrier" ::: "memory");
+
+  // One iteration = two stages (KT is even), so the two fragment sets swap
+  // roles without register copies.  Per stage kt:
+  //   read stage kt+1's fragments (it became visible at the last barrier),
+  //   refill the buffer stage kt came from with stage kt+4 (clamped: the
+  //   tail re-reads the last stage into idle buffers, keeping the wait
+  //   count constant), multiply stage kt, then wait until this wave's
+  //   fragment reads are done and only the 8 loads of stages kt+3 and kt+4
+  //   are outstanding (stage kt+2 has landed), barrier.  Waiting for the
+  //   reads before the barrier means no wave refills a buffer (next stage)
+  //   while another wave may still be reading it.
+  // sched_barrier(0) keeps each stage's instructions between its barriers;
+  // stage_schedule() orders them inside.  This stage's MFMA operands are
+  // already in registers, so the next stage's LDS reads overlap the MFMAs.
+  for (int kt = 0; kt < KT; kt += 2) {
+    if constexpr (NM > 0) read_frags<NM, NSETS>(c, (kt + 1) & 3, fa1, fb1);
+    issue_stage<NSETS>(c, kt + 4 < KT ? kt + 4 : KT - 1, kt & 3);
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb0[n], fa0[m], acc[n][m]);
+    stage_schedule<NM>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (NM > 0) read_frags<NM, NSETS>(c, (kt + 2) & 3, fa0, fb0);
+    issue_stage<NSETS>(c, kt + 5 < KT ? kt + 5 : KT - 1, (kt + 1) & 3);
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb1[n], fa1[m], acc[n][m]);
+    stage_schedule<NM>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
 
 template <int EPI, int NSETS>
@@ -137,7 +255,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1;  // rows wm*64 .. +64
+  const int wm = wave >> 1;  // 16-row groups wm, wm+4, wm+8, wm+12
   const int wn = wave & 1;   // weight rows of each set: wn half
   const int64_t N = g.N, K = g.K;
   const int64_t n0 = static_cast<int64_t>(col_tile) * (kBN / NSETS);
@@ -149,55 +267,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 
   // ---- global -> LDS sources.  Token rows: this wave stages rows
   // (wave*2 + j)*16 + (lane >> 2), 16-byte physical chunk (lane & 3), which
-  // holds logical chunk (lane & 3) ^ ((lane >> 3) & 3).  Byte offsets from
-  // the A base fit 32 bits (checked on the host).
-  const unsigned char* a_base = static_cast<const unsigned char*>(g.a);
-  uint32_t a_off[2];
+  // holds logical chunk (lane & 3) ^ ((lane >> 3) & 3).  Rows past the tile
+  // re-read its first row.  Byte offsets from the A base fit 32 bits
+  // (checked on the host).
+  WaveCtx c;
+  c.lds = lds;
+  c.a_base = static_cast<const unsigned char*>(g.a);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = (wave * 2 + j) * 16 + (lane >> 2);
     const int p = ti.row0 + (r < ti.rows ? r : 0);
-    const int c = (lane & 3) ^ ((lane >> 3) & 3);
-    a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + c * 16 + k_first * 64);
+    const int ch = (lane & 3) ^ ((lane >> 3) & 3);
+    c.a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + k_first * 64);
   }
   // Weight blocks: this wave stages row blocks wave*2 + j of the stage (wave
   // uniform addresses).  The packed buffer has a 256-row tail, so row blocks
   // past N stay in bounds (their columns are never stored).
-  const unsigned char* b_base[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int rb = wave * 2 + j;
     const int set = NSETS == 2 ? rb >> 3 : 0;
     const int64_t nb = n0 / 16 + (NSETS == 2 ? (rb & 7) : rb);
     const unsigned char* w = static_cast<const unsigned char*>(set == 0 ? g.w0 : g.w1);
-    b_base[j] = w + ((static_cast<int64_t>(ti.expert) * nblocks + nb) * kblocks + k_first) * 1024;
+    c.b_base[j] = w + ((static_cast<int64_t>(ti.expert) * nblocks + nb) * kblocks + k_first) * 1024;
   }
-  const uint32_t b_lane = lane * 16;
-
-  auto issue_stage = [&](int kt, int buf) __attribute__((always_inline)) {
-    unsigned char* st = lds + buf * kStage;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_global_load_lds(a_base + (a_off[j] + kt * 64), st + (wave * 2 + j) * 1024, 16, 0, 0);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_global_load_lds(b_base[j] + (static_cast<uint32_t>(kt) * 1024 + b_lane),
-                                       st + kAStage + (wave * 2 + j) * 1024, 16, 0, 0);
-  };
-
-  // ---- fragment reads
-  const int a_lane = (lane & 15) * 64 + ((((lane >> 4) ^ (((lane & 15) >> 1) & 3))) << 4);
-  auto read_frags = [&](int buf, u32x4_t* fa, u32x4_t* fb) __attribute__((always_inline)) {
-    const unsigned char* st = lds + buf * kStage;
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      fa[m] = *reinterpret_cast<const u32x4_t*>(st + (wm * 64 + m * 16) * 64 + a_lane);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const int rb = NSETS == 2 ? ((n >> 2) * 8 + wn * 4 + (n & 3)) : (wn * 8 + n);
-      fb[n] = *reinterpret_cast<const u32x4_t*>(st + kAStage + rb * 1024 + lane * 16);
-    }
-  };
+  c.b_lane = lane * 16;
+  // A fragment: row (lane & 15) of a 16-row group, logical chunk lane >> 4
+  // (the XOR swizzle depends only on the row within the group).
+  c.a_lane = (lane & 15) * 64 + ((((lane >> 4) ^ (((lane & 15) >> 1) & 3))) << 4);
+  c.wave = wave;
+  c.wm = wm;
+  c.wn = wn;
+  c.KT = KT;
 
   f32x4_t acc[8][4];
 #pragma unroll
@@ -205,52 +306,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 #pragma unroll
     for (int m = 0; m < 4; ++m) acc[n][m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Prologue: stages 0..3 in flight (4 loads per wave each); wait for 0 and 1.
-#pragma unroll
-  for (int s = 0; s < kStages; ++s) issue_stage(s < KT ? s : KT - 1, s);
-  __builtin_amdgcn_s_waitcnt(kWaitVm8);
-  asm volatile("s_barrier" ::: "memory");
-  u32x4_t fa0[4], fb0[8], fa1[4], fb1[8];
-  read_frags(0, fa0, fb0);
-
-  // One iteration = two stages (KT is even), so the two fragment sets swap
-  // roles without register copies.  Per stage kt:
-  //   read stage kt+1's fragments (it became visible at the last barrier),
-  //   refill the buffer stage kt came from with stage kt+4 (clamped: the
-  //   tail re-reads the last stage into idle buffers, keeping the wait
-  //   count constant), multiply stage kt, wait until only the 8 loads of
-  //   stages kt+3 and kt+4 are outstanding (stage kt+2 has landed), barrier.
-  // sched_barrier(0) keeps each stage's instructions between its barriers;
-  // stage_schedule() orders them inside.  This stage's MFMA operands are
-  // already in registers, so the next stage's LDS reads overlap the MFMAs.
-  for (int kt = 0; kt < KT; kt += 2) {
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this stage's fragments (read a stage ago)
-    read_frags((kt + 1) & 3, fa1, fb1);
-    issue_stage(kt + 4 < KT ? kt + 4 : KT - 1, kt & 3);
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) acc[n][m] = mfma16(fb0[n], fa0[m], acc[n][m]);
-    stage_schedule();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm8);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    read_frags((kt + 2) & 3, fa0, fb0);
-    issue_stage(kt + 5 < KT ? kt + 5 : KT - 1, (kt + 1) & 3);
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) acc[n][m] = mfma16(fb1[n], fa1[m], acc[n][m]);
-    stage_schedule();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm8);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
+  // Active 16-row groups of this wave: groups wm, wm+4, wm+8, wm+12 below
+  // ceil(rows / 16).  Wave-uniform, so each wave runs one specialisation.
+  const int groups = (ti.rows + 15) >> 4;
+  const int nm = groups > wm ? min(4, (groups - wm + 3) >> 2) : 0;
+  switch (nm) {
+    case 4: k_loop<4, NSETS>(c, acc); break;
+    case 3: k_loop<3, NSETS>(c, acc); break;
+    case 2: k_loop<2, NSETS>(c, acc); break;
+    case 1: k_loop<1, NSETS>(c, acc); break;
+    default: k_loop<0, NSETS>(c, acc); break;
   }
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
   // ---- epilogue: lane holds assignment row (lane & 15) of each 16-row
   // group and 4 consecutive weight rows 4*(lane >> 4) .. +4.
@@ -262,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     if (col >= N) continue;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const int r = wm * 64 + m * 16 + (lane & 15);
+      const int r = (wm + 4 * m) * 16 + (lane & 15);
       if (r >= ti.rows) continue;
       const int p = ti.row0 + r;
       const f32x4_t a0 = acc[n][m];
