@@ -36,6 +36,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Two e4m3fn codes (bytes 0-1 of w, or 2-3 when HI) -> two bf16 packed in a
+// dword, low element first.  Exact: every e4m3fn value is a bf16 value.
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt2_e4m3fn_bf16(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+
+// 8 e4m3fn codes in two dwords -> a bf16x8 fragment (same element order).
+__device__ __forceinline__ u32x4_t f8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  return u32x4_t{cvt2_e4m3fn_bf16<false>(lo), cvt2_e4m3fn_bf16<true>(lo), cvt2_e4m3fn_bf16<false>(hi),
+                 cvt2_e4m3fn_bf16<true>(hi)};
+}
+
 // OCP FP8 E4M3 (e4m3fn) code -> float: (8+m) * 2^(e-10) for e>0, m * 2^-9 for
 // e=0, NaN for S.1111.111.
 __device__ __forceinline__ float e4m3fn_to_f32(uint32_t c) {

@@ -30,18 +30,10 @@
 namespace fmoe {
 namespace {
 
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-
-// Two e4m3fn codes (bytes 0-1, or 2-3 when HI) -> two bf16, exact (scale 1).
-template <bool HI>
-__device__ __forceinline__ uint32_t cvt2(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
-}
-
 // 16 e4m3fn codes (two 32-input steps of one lane) -> two bf16x8 fragments.
 __device__ __forceinline__ void f8x16_to_bf16(const u32x4_t q, u32x4_t& s0, u32x4_t& s1) {
-  s0 = u32x4_t{cvt2<false>(q.x), cvt2<true>(q.x), cvt2<false>(q.y), cvt2<true>(q.y)};
-  s1 = u32x4_t{cvt2<false>(q.z), cvt2<true>(q.z), cvt2<false>(q.w), cvt2<true>(q.w)};
+  s0 = f8x8_to_bf16x8(q.x, q.y);
+  s1 = f8x8_to_bf16x8(q.z, q.w);
 }
 
 __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {

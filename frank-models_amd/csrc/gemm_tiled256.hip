@@ -40,6 +40,11 @@ constexpr int kAStage = kBM * kBK * 2;       // 16 KiB
 constexpr int kBStage = (kBN / 16) * 1024;   // 16 KiB
 constexpr int kStage = kAStage + kBStage;    // 32 KiB
 constexpr int kLds = kStages * kStage;       // 128 KiB
+// fp8 weights: 64-input stages (A as two 32-input halves in the bf16 layout,
+// then 16 fp8 weight blocks of 16 rows x 64 inputs), 3-deep ring.
+constexpr int kStagesF8 = 3;
+constexpr int kStageF8 = 2 * kAStage + kBStage;  // 48 KiB
+constexpr int kLdsF8 = kStagesF8 * kStageF8;     // 144 KiB
 constexpr int kGroupN = 4;                   // column tiles swept together
 
 __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {
@@ -55,6 +60,8 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g * (u / (1
 constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
 constexpr int kWaitVm8 = 0x0F70 | 8;                // vmcnt(8)
 constexpr int kWaitVm8Lgkm0 = 0x0070 | 8;           // vmcnt(8) lgkmcnt(0)
+constexpr int kWaitVm6Lgkm0 = 0x0070 | 6;           // vmcnt(6) lgkmcnt(0)
+constexpr int kWaitVm12 = 0x0F70 | 12;              // vmcnt(12)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
 
 __device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
@@ -243,7 +250,134 @@ __device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
 
-template <int EPI, int NSETS>
+// ---------------------------------------------------------------- fp8 weights
+// Stage kt (64 inputs) in buffer buf: A halves h = 0, 1 (inputs 32 h .. +32)
+// at h * kAStage in the bf16 layout, the 16 fp8 weight blocks after them.
+// One of the 6 global->LDS loads of an fp8 stage (d = 0..3: A half d >> 1,
+// row set d & 1; d = 4, 5: weight blocks).
+__device__ __forceinline__ void issue_one_f8(const WaveCtx& c, int kt, int buf, int d) {
+  unsigned char* st = c.lds + buf * kStageF8;
+  if (d < 4) {
+    const int h = d >> 1, j = d & 1;
+    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + (2 * kt + h) * 64),
+                                     st + h * kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
+  } else {
+    const int j = d - 4;
+    __builtin_amdgcn_global_load_lds(c.b_base[j] + (static_cast<uint32_t>(kt) * 1024 + c.b_lane),
+                                     st + 2 * kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ u32x4_t read_a_frag(const WaveCtx& c, const unsigned char* half_base, int m) {
+  return *reinterpret_cast<const u32x4_t*>(half_base + (c.wm + 4 * m) * 16 * 64 + c.a_lane);
+}
+
+// Weight fragment n of a stage, still fp8: lane bytes 0-7 feed the first
+// 32-input half, bytes 8-15 the second.
+template <int NSETS>
+__device__ __forceinline__ u32x4_t read_b_frag(const WaveCtx& c, const unsigned char* b_base, int n) {
+  const int rb = NSETS == 2 ? ((n >> 2) * 8 + c.wn * 4 + (n & 3)) : (c.wn * 8 + n);
+  return *reinterpret_cast<const u32x4_t*>(b_base + rb * 1024 + c.b_lane);
+}
+
+template <int H>
+__device__ __forceinline__ u32x4_t convert_frag(const u32x4_t q) {
+  return f8x8_to_bf16x8(q[2 * H], q[2 * H + 1]);
+}
+
+// One 32-input half of an fp8 stage for a wave with NM active row groups,
+// as 8 chunks (weight fragment n = 0..7).  Chunk n converts fragment n+1's
+// half H from fp8 (fragment 0 before the first chunk), runs fragment n's NM
+// MFMAs, and between them issues this half's share of reads and loads:
+//   H = 0: A half 1 of the current stage (chunks 0..NM-1);
+//   H = 1: A half 0 and weight fragment n of the next stage (fragment n's
+//          old codes were converted a chunk earlier, so the read can reuse
+//          its registers), and the 6 loads that refill a buffer (chunks 0-5).
+// A scheduling fence closes each chunk, so the interleave does not depend on
+// the scheduler's global choices.
+template <int NM, int NSETS, int H>
+__device__ __forceinline__ void half_f8(const WaveCtx& c, f32x4_t (&acc)[8][4], const u32x4_t (&fa)[4],
+                                        u32x4_t (&fa_rd)[4], u32x4_t (&fq)[8], const unsigned char* a_rd,
+                                        const unsigned char* b_rd, int issue_kt, int issue_buf) {
+  u32x4_t cur{};
+  if constexpr (NM > 0) cur = convert_frag<H>(fq[0]);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    u32x4_t nxt = cur;
+    if constexpr (NM > 0) {
+      if (n < 7) nxt = convert_frag<H>(fq[n + 1]);
+      acc[n][0] = mfma16(cur, fa[0], acc[n][0]);
+      if (n < NM) fa_rd[n] = read_a_frag(c, a_rd, n);
+      if (H == 1) fq[n] = read_b_frag<NSETS>(c, b_rd, n);
+    }
+    if (NM > 1) acc[n][1] = mfma16(cur, fa[1], acc[n][1]);
+    if (H == 1 && n < 6) issue_one_f8(c, issue_kt, issue_buf, n);
+    if (NM > 2) acc[n][2] = mfma16(cur, fa[2], acc[n][2]);
+    if (NM > 3) acc[n][3] = mfma16(cur, fa[3], acc[n][3]);
+    if constexpr (NM == 4) {
+      if (n < 7) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (n < 4 && H == 1)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      else if (n < 4 || H == 1)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (H == 1 && n < 6) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    cur = nxt;
+  }
+}
+
+// K loop for fp8 weights.  Per stage kt (buffer kt % 3), two halves with a
+// barrier each:
+//   half 0: multiply half 0 while reading A half 1 of stage kt; wait until
+//           this wave's reads are done and stage kt+1 has landed (only stage
+//           kt+2's 6 loads outstanding), barrier.
+//   half 1: multiply half 1 while reading stage kt+1's A half 0 and weight
+//           fragments and refilling buffer kt % 3 with stage kt+3 (every
+//           wave's reads of it finished before the half-0 barrier); wait for
+//           the reads, barrier.
+// Stage kt+3 then has a stage and a half to land.  The tail re-reads the
+// last stage into idle buffers, keeping the wait counts constant.
+template <int NM, int NSETS>
+__device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
+  const int KT = c.KT;
+#pragma unroll
+  for (int s = 0; s < kStagesF8; ++s)
+#pragma unroll
+    for (int d = 0; d < 6; ++d) issue_one_f8(c, s < KT ? s : KT - 1, s, d);
+  __builtin_amdgcn_s_waitcnt(kWaitVm12);  // stage 0 landed
+  asm volatile("s_barrier" ::: "memory");
+  u32x4_t fa0[4], fa1[4], fq[8];
+  if constexpr (NM > 0) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) fa0[m] = read_a_frag(c, c.lds, m);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) fq[n] = read_b_frag<NSETS>(c, c.lds + 2 * kAStage, n);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  int buf = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int next = buf == kStagesF8 - 1 ? 0 : buf + 1;
+    const unsigned char* cur_st = c.lds + buf * kStageF8;
+    const unsigned char* next_st = c.lds + next * kStageF8;
+    half_f8<NM, NSETS, 0>(c, acc, fa0, fa1, fq, cur_st + kAStage, nullptr, 0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    half_f8<NM, NSETS, 1>(c, acc, fa1, fa0, fq, next_st, next_st + 2 * kAStage, kt + 3 < KT ? kt + 3 : KT - 1,
+                          buf);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    buf = next;
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+}
+
+template <int EPI, int NSETS, bool F8>
 __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmArgs g, int n_row_tiles,
                                                                      int n_col_tiles) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
@@ -260,8 +394,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   const int64_t N = g.N, K = g.K;
   const int64_t n0 = static_cast<int64_t>(col_tile) * (kBN / NSETS);
   const int64_t nblocks = N / 16;
-  const int64_t kblocks = K / 32;
-  // This block's share of K: stages [k_first, k_first + KT) of 32 inputs.
+  constexpr int kStageInputs = F8 ? 64 : 32;  // one packed weight block
+  const int64_t kblocks = K / kStageInputs;
+  // This block's share of K: stages [k_first, k_first + KT).
   const int KT = static_cast<int>(kblocks / g.ksplit);
   const int k_first = split * KT;
 
@@ -278,7 +413,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     const int r = (wave * 2 + j) * 16 + (lane >> 2);
     const int p = ti.row0 + (r < ti.rows ? r : 0);
     const int ch = (lane & 3) ^ ((lane >> 3) & 3);
-    c.a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + k_first * 64);
+    c.a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + k_first * kStageInputs * 2);
   }
   // Weight blocks: this wave stages row blocks wave*2 + j of the stage (wave
   // uniform addresses).  The packed buffer has a 256-row tail, so row blocks
@@ -310,30 +445,45 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   // ceil(rows / 16).  Wave-uniform, so each wave runs one specialisation.
   const int groups = (ti.rows + 15) >> 4;
   const int nm = groups > wm ? min(4, (groups - wm + 3) >> 2) : 0;
-  switch (nm) {
-    case 4: k_loop<4, NSETS>(c, acc); break;
-    case 3: k_loop<3, NSETS>(c, acc); break;
-    case 2: k_loop<2, NSETS>(c, acc); break;
-    case 1: k_loop<1, NSETS>(c, acc); break;
-    default: k_loop<0, NSETS>(c, acc); break;
+  if constexpr (F8) {
+    switch (nm) {
+      case 4: k_loop_f8<4, NSETS>(c, acc); break;
+      case 3: k_loop_f8<3, NSETS>(c, acc); break;
+      case 2: k_loop_f8<2, NSETS>(c, acc); break;
+      case 1: k_loop_f8<1, NSETS>(c, acc); break;
+      default: k_loop_f8<0, NSETS>(c, acc); break;
+    }
+  } else {
+    switch (nm) {
+      case 4: k_loop<4, NSETS>(c, acc); break;
+      case 3: k_loop<3, NSETS>(c, acc); break;
+      case 2: k_loop<2, NSETS>(c, acc); break;
+      case 1: k_loop<1, NSETS>(c, acc); break;
+      default: k_loop<0, NSETS>(c, acc); break;
+    }
   }
 
   // ---- epilogue: lane holds assignment row (lane & 15) of each 16-row
-  // group and 4 consecutive weight rows 4*(lane >> 4) .. +4.
+  // group and 4 consecutive weight rows 4*(lane >> 4) .. +4.  fp8 weights:
+  // the per-output-channel scale multiplies the fp32 dot product.
   const int64_t e = ti.expert;
-  (void)e;
 #pragma unroll
   for (int n = 0; n < (NSETS == 2 ? 4 : 8); ++n) {
     const int64_t col = n0 + (NSETS == 2 ? wn * 64 : wn * 128) + n * 16 + 4 * (lane >> 4);
     if (col >= N) continue;
+    f32x4_t sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
+    if constexpr (F8) {
+      sc0 = *reinterpret_cast<const f32x4_t*>(g.s0 + e * N + col);
+      if (NSETS == 2) sc1 = *reinterpret_cast<const f32x4_t*>(g.s1 + e * N + col);
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int r = (wm + 4 * m) * 16 + (lane & 15);
       if (r >= ti.rows) continue;
       const int p = ti.row0 + r;
-      const f32x4_t a0 = acc[n][m];
+      const f32x4_t a0 = acc[n][m] * sc0;
       if (EPI == EPI_SWIGLU) {
-        const f32x4_t a1 = acc[n + 4][m];
+        const f32x4_t a1 = acc[n + 4][m] * sc1;
         store4<EPI>(g, split, p, col, silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]),
                     silu_mul(a0[3], a1[3]));
       } else {
@@ -343,11 +493,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   }
 }
 
-template <int EPI, int NSETS>
+template <int EPI, int NSETS, bool F8>
 hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
+  constexpr int lds_bytes = F8 ? kLdsF8 : kLds;
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS, F8>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     (void)hipGetLastError();
     return true;
   }();
@@ -356,8 +507,8 @@ hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
   const int col_tiles = static_cast<int>((g.N + kBN / NSETS - 1) / (kBN / NSETS));
   const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles * g.ksplit;
   const unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
-  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS>), dim3(blocks), dim3(kThreads), kLds, s, g, row_tiles,
-                     col_tiles);
+  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
+                     row_tiles, col_tiles);
   return hipGetLastError();
 }
 
@@ -375,8 +526,11 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
 }
 
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
-  if (g.act_dtype != DT_BF16 || g.w_dtype != DT_BF16 || g.w_format != WF_MFMA16) return false;
+  if (g.act_dtype != DT_BF16 || (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) || g.w_format != WF_MFMA16)
+    return false;
+  // bf16: an even number of 32-input stages per split; fp8: whole 64-input blocks.
   if (g.K <= 0 || g.K % (2 * kBK * g.ksplit) || g.N % 16 || g.lda % 8 || g.ldo % 4) return false;
+  if (g.w_dtype == DT_F8 && (!g.s0 || (g.epi == EPI_SWIGLU && !g.s1))) return false;
   // 32-bit byte offsets of A rows
   const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;
   if (a_rows * g.lda * 2 >= (int64_t(1) << 32)) return false;
@@ -388,9 +542,11 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
 hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t s) {
   if (!gemm_tiled256_supported(g)) return hipErrorNotSupported;
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
-  if (g.epi == EPI_SWIGLU) return launch_t<EPI_SWIGLU, 2>(g, s);
-  if (g.epi == EPI_SCATTER_WEIGHTED) return launch_t<EPI_SCATTER_WEIGHTED, 1>(g, s);
-  return launch_t<EPI_SCATTER, 1>(g, s);
+  const bool f8 = g.w_dtype == DT_F8;
+  if (g.epi == EPI_SWIGLU) return f8 ? launch_t<EPI_SWIGLU, 2, true>(g, s) : launch_t<EPI_SWIGLU, 2, false>(g, s);
+  if (g.epi == EPI_SCATTER_WEIGHTED)
+    return f8 ? launch_t<EPI_SCATTER_WEIGHTED, 1, true>(g, s) : launch_t<EPI_SCATTER_WEIGHTED, 1, false>(g, s);
+  return f8 ? launch_t<EPI_SCATTER, 1, true>(g, s) : launch_t<EPI_SCATTER, 1, false>(g, s);
 }
 
 }  // namespace fmoe
