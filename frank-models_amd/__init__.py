@@ -7,6 +7,11 @@ Public API (same signatures as the reference's components/oracles):
   n_expert, n_expert_used, n_embd, n_ff, normalize_weights)``
 * ``mul_mat_id(weights, input, ids)``
 * ``swiglu(gate, up)``
+* ``rms_norm(x, weight, eps)`` (oracles/normalization.py:10)
+* ``moe_ffn_sublayer(residual, ffn_norm_w, rms_eps, gate_inp_w, up_exps_w,
+  gate_exps_w, down_exps_w, n_expert, n_expert_used, n_embd, n_ff,
+  normalize_weights)``: ffn_norm, block and residual add of a transformer
+  layer (transformer_layer_moe_prefill.mlir:205-242)
 
 plus ``router``, ``permute``, ``pack_expert_weights``,
 ``quantize_expert_weights``, ``QuantizedExpertWeights``,
@@ -29,10 +34,12 @@ from .api import (  # noqa: F401
     PackedExpertWeights,
     QuantizedExpertWeights,
     moe_ffn_block,
+    moe_ffn_sublayer,
     mul_mat_id,
     pack_expert_weights,
     permute,
     quantize_expert_weights,
+    rms_norm,
     router,
     swiglu,
 )
@@ -44,6 +51,8 @@ __all__ = [
     "moe_ffn_block",
     "mul_mat_id",
     "swiglu",
+    "rms_norm",
+    "moe_ffn_sublayer",
     "router",
     "permute",
     "pack_expert_weights",

@@ -42,7 +42,7 @@ PATH_TILED_LARGE = 4
 
 
 # fmoe_timer
-TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id")
+TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id", "norm")
 
 
 class FmoeError(RuntimeError):
@@ -94,6 +94,13 @@ SIGNATURES = {
     "fmoe_moe_ffn_block": (
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp, _sz, _vp],
+    ),
+    "fmoe_rms_norm": (_c_int, [_vp, _vp, ctypes.c_float, _vp, _c_i64, _c_i64, _c_int, _vp]),
+    "fmoe_moe_ffn_sublayer_workspace_bytes": (_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "fmoe_moe_ffn_sublayer": (
+        _c_int,
+        [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp, _sz, _vp],
     ),
     "fmoe_moe_ffn_block_routing": (

@@ -281,6 +281,26 @@ def swiglu(gate, up):
     return _finish(out, g_np)
 
 
+def rms_norm(x, weight, eps: float = 1e-6):
+    """``(x / sqrt(mean(x^2, axis=-1) + eps)) * weight`` per row, positional
+    signature of oracles/normalization.py:10-14 (components/normalization/
+    rms_norm.mlir:18-85).  x ``[..., n_embd]``, weight ``[n_embd]``; fp32
+    arithmetic, output in x's dtype."""
+    _check_float(x, "x")
+    _check_float(weight, "weight")
+    xs, ws = _shape(x), _shape(weight)
+    if len(xs) < 1 or ws != (xs[-1],):
+        raise ValueError(f"weight shape {ws} != [{xs[-1] if xs else '?'}]")
+    t, t_np = _to_device(x, "x")
+    w, _ = _to_device(weight, "weight")
+    w = w.to(t.dtype).contiguous()
+    out = torch.empty_like(t)
+    H = xs[-1]
+    rows = t.numel() // H if H else 0
+    L.call("fmoe_rms_norm", _ptr(t), _ptr(w), float(eps), _ptr(out), rows, H, _TORCH_TO_DT[t.dtype], _stream())
+    return _finish(out, t_np)
+
+
 # ---------------------------------------------------------------- router / permutation
 def router(input, gate_inp_w, n_expert_used: int, normalize_weights: bool):
     """Steps 1-4 of the block (moe_ffn_block.mlir:50-128): returns
@@ -404,12 +424,12 @@ class MoEFFNBlock:
         self._ws = None
         self._ws_key = None
 
-    def workspace_bytes(self, n_tokens: int) -> int:
-        return L.lib().fmoe_moe_ffn_block_workspace_bytes(
-            n_tokens, self.n_expert, self.k, self.n_embd, self.n_ff, self.act, self.wdt)
+    def workspace_bytes(self, n_tokens: int, sublayer: bool = False) -> int:
+        fn = "fmoe_moe_ffn_sublayer_workspace_bytes" if sublayer else "fmoe_moe_ffn_block_workspace_bytes"
+        return getattr(L.lib(), fn)(n_tokens, self.n_expert, self.k, self.n_embd, self.n_ff, self.act, self.wdt)
 
-    def _get_ws(self, n_tokens):
-        nbytes = self.workspace_bytes(n_tokens)
+    def _get_ws(self, n_tokens, sublayer=False):
+        nbytes = self.workspace_bytes(n_tokens, sublayer)
         key = (torch.cuda.current_device(), nbytes)
         if self._ws is None or self._ws_key[0] != key[0] or self._ws.numel() < nbytes:
             self._ws = _workspace(nbytes)
@@ -430,6 +450,35 @@ class MoEFFNBlock:
                _ptr(self.down.data), _ptr(self.up.scales), _ptr(self.gate.scales), _ptr(self.down.scales),
                self.wdt, _ptr(out), T, self.n_expert, self.k, self.n_embd, self.n_ff,
                int(self.normalize), self.act, _ptr(ws), ws.numel(), _stream())
+        return out
+
+    def sublayer(self, residual: torch.Tensor, ffn_norm_w, rms_eps: float,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The MoE FFN sub-layer of a transformer layer,
+        ``residual + block(rms_norm(residual, ffn_norm_w, rms_eps))``
+        (transformer_layer_moe_prefill.mlir:205-242), on a device tensor
+        ``[n_tokens, n_embd]``.  ``out=residual`` updates in place."""
+        dt = _DT_TO_TORCH[self.act]
+        if residual.dtype != dt or residual.device.type != "cuda":
+            raise TypeError(f"residual must be a {dt} device tensor")
+        if residual.dim() != 2 or residual.shape[1] != self.n_embd:
+            raise ValueError(f"residual must be [n_tokens, {self.n_embd}]")
+        _check_float(ffn_norm_w, "ffn_norm_w")
+        if _shape(ffn_norm_w) != (self.n_embd,):
+            raise ValueError(f"ffn_norm_w shape {_shape(ffn_norm_w)} != [{self.n_embd}]")
+        nw, _ = _to_device(ffn_norm_w, "ffn_norm_w")
+        nw = nw.to(dt).contiguous()
+        residual = residual.contiguous()
+        T = int(residual.shape[0])
+        if out is None:
+            out = torch.empty((T, self.n_embd), dtype=dt, device=residual.device)
+        elif out.dtype != dt or tuple(out.shape) != (T, self.n_embd) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous {dt} [{T}, {self.n_embd}] tensor")
+        ws = self._get_ws(T, sublayer=True)
+        L.call("fmoe_moe_ffn_sublayer", _ptr(residual), _ptr(nw), float(rms_eps), _ptr(self.wr),
+               _ptr(self.up.data), _ptr(self.gate.data), _ptr(self.down.data), _ptr(self.up.scales),
+               _ptr(self.gate.scales), _ptr(self.down.scales), self.wdt, _ptr(out), T, self.n_expert, self.k,
+               self.n_embd, self.n_ff, int(self.normalize), self.act, _ptr(ws), ws.numel(), _stream())
         return out
 
     def routing(self, n_tokens: int):
@@ -495,3 +544,33 @@ def moe_ffn_block(input, gate_inp_w, up_exps_w, gate_exps_w, down_exps_w, n_expe
                       n_embd, n_ff, normalize_weights, act_dtype=x.dtype)
     out = blk(x)
     return _finish(out, x_np)
+
+
+def moe_ffn_sublayer(residual, ffn_norm_w, rms_eps: float, gate_inp_w, up_exps_w, gate_exps_w, down_exps_w,
+                     n_expert: int, n_expert_used: int, n_embd: int, n_ff: int, normalize_weights: bool):
+    """``residual + moe_ffn_block(rms_norm(residual, ffn_norm_w, rms_eps), ...)``:
+    the MoE FFN sub-layer of architectures/llm/transformer_layer_moe_prefill.mlir:205-242
+    (decode: transformer_layer_moe_decode.mlir:227-255) on the flattened
+    residual stream ``[n_tokens, n_embd]``.  NumPy in, NumPy out; device
+    tensors stay on the device."""
+    _check_float(residual, "residual")
+    _check_float(ffn_norm_w, "ffn_norm_w")
+    _check_float(gate_inp_w, "gate_inp_w")
+    for name, w in (("up_exps_w", up_exps_w), ("gate_exps_w", gate_exps_w), ("down_exps_w", down_exps_w)):
+        if not isinstance(w, (PackedExpertWeights, QuantizedExpertWeights)):
+            _check_float(w, name)
+    rs = _shape(residual)
+    if len(rs) != 2 or rs[1] != int(n_embd):
+        raise ValueError(f"residual shape {rs} != [n_tokens, {n_embd}]")
+    if _shape(ffn_norm_w) != (int(n_embd),):
+        raise ValueError(f"ffn_norm_w shape {_shape(ffn_norm_w)} != [{n_embd}]")
+    _check_block_shapes(_shape(gate_inp_w), _shape(up_exps_w), _shape(gate_exps_w), _shape(down_exps_w),
+                        int(n_expert), int(n_embd), int(n_ff))
+    k = int(n_expert_used)
+    if not 1 <= k <= int(n_expert):
+        raise ValueError(f"n_expert_used={k} outside [1, {n_expert}]")
+    r, r_np = _to_device(residual, "residual")
+    blk = MoEFFNBlock(gate_inp_w, up_exps_w, gate_exps_w, down_exps_w, n_expert, n_expert_used,
+                      n_embd, n_ff, normalize_weights, act_dtype=r.dtype)
+    out = blk.sublayer(r, ffn_norm_w, rms_eps)
+    return _finish(out, r_np)

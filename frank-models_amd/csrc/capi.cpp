@@ -293,6 +293,176 @@ int check_dims(const char* what, int64_t v, int64_t lo, int64_t hi) {
     if (r_ != FMOE_OK) return r_; \
   } while (0)
 
+int validate_router(int64_t T, int64_t H, int64_t E, int64_t k) {
+  FMOE_TRY(check_dims("n_tokens", T, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_embd", H, 1, kMaxDim));
+  FMOE_TRY(check_dims("n_expert", E, 1, kMaxExpert));
+  FMOE_TRY(check_dims("n_expert_used", k, 1, E < kMaxExpertUsed ? E : kMaxExpertUsed));
+  if (k * T > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_expert_used * n_tokens exceeds 2^31-1");
+  return FMOE_OK;
+}
+
+struct BlockCall {
+  const void* input;
+  const void* w_router;
+  const void* packed_up;
+  const void* packed_gate;
+  const void* packed_down;
+  const float* up_scales;
+  const float* gate_scales;
+  const float* down_scales;
+  int w_dtype;
+  void* out;
+  const void* residual;  // added to the block output by combine (may be null)
+  int64_t n_tokens, n_expert, n_expert_used, n_embd, n_ff;
+  int normalize_weights;
+  int act_dtype;
+  void* workspace;
+  size_t workspace_bytes;
+  void* stream;
+};
+
+// The block's workspace followed by the normalised input rows.
+struct SublayerLayout {
+  BlockLayout block;
+  size_t xn, total;
+};
+
+SublayerLayout sublayer_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act, int wdt) {
+  SublayerLayout SL;
+  SL.block = block_layout(T, E, k, H, F, act, wdt);
+  SL.xn = SL.block.total;
+  SL.total = SL.xn + align_up(static_cast<size_t>(T) * H * dtype_bytes(act));
+  return SL;
+}
+
+int check_workspace(const void* ws, size_t bytes, size_t need) {
+  if (bytes < need) return fail(FMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", bytes, need);
+  if (reinterpret_cast<uintptr_t>(ws) % kAlign)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
+  return FMOE_OK;
+}
+
+// Argument checks shared by the block and the sub-layer (the reference
+// checks none of these; moe_ffn_block.mlir:34-45 only declares the types).
+int validate_block(const BlockCall& c) {
+  if (!act_dtype_ok(c.act_dtype)) return fail(FMOE_ERR_DTYPE, "activation dtype %d", c.act_dtype);
+  if (!w_dtype_ok(c.w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", c.w_dtype);
+  if (c.act_dtype == FMOE_F32 && c.w_dtype != FMOE_F32)
+    return fail(FMOE_ERR_DTYPE, "f32 activations need f32 weights");
+  FMOE_TRY(validate_router(c.n_tokens, c.n_embd, c.n_expert, c.n_expert_used));
+  FMOE_TRY(check_dims("n_ff", c.n_ff, 0, kMaxDim));
+  if (c.normalize_weights != 0 && c.normalize_weights != 1)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "normalize_weights must be 0 or 1");
+  if (c.n_tokens == 0) return FMOE_OK;
+  if (!c.input || !c.w_router || !c.packed_up || !c.packed_gate || !c.packed_down || !c.out || !c.workspace)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (c.w_dtype == FMOE_F8E4M3FN && (!c.up_scales || !c.gate_scales || !c.down_scales))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
+  if (!aligned_for(c.input, c.act_dtype) || !aligned_for(c.out, c.act_dtype) ||
+      !aligned_for(c.w_router, c.act_dtype))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  return FMOE_OK;
+}
+
+// The MoE FFN block's kernel sequence (moe_ffn_block.mlir:47-208) on a
+// validated call whose workspace holds layout L.
+int run_block(const BlockCall& c, const BlockLayout& L) {
+  hipStream_t s = static_cast<hipStream_t>(c.stream);
+  void* workspace = c.workspace;
+  const int64_t n_embd = c.n_embd, n_ff = c.n_ff, n_expert = c.n_expert, n_expert_used = c.n_expert_used;
+  const int act_dtype = c.act_dtype, w_dtype = c.w_dtype;
+  const int T = static_cast<int>(c.n_tokens);
+  const int n = static_cast<int>(c.n_tokens * n_expert_used);
+  int* ids = at<int>(workspace, L.ids);
+  float* rw = at<float>(workspace, L.weights);
+  int* err = at<int>(workspace, L.perm.err);
+  int* order = at<int>(workspace, L.perm.order);
+  int* offsets = at<int>(workspace, L.perm.offsets);
+  void* h = at<char>(workspace, L.h);
+  void* y = at<char>(workspace, L.y);
+
+  // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128).
+  {
+    ScopedTimer t(FMOE_TIMER_ROUTER, s);
+    FMOE_HIP(launch_router(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
+                           static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype, ids, rw, s));
+  }
+  // Group the slot-major assignments by expert (replaces the gather, mul_mat_id.mlir:50-61).
+  {
+    ScopedTimer t(FMOE_TIMER_PERMUTE, s);
+    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err, s));
+  }
+
+  // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
+  GroupedGemmArgs g;
+  g.a = c.input;
+  g.lda = n_embd;
+  g.a_mode = A_GATHER_TOKEN;
+  g.order = order;
+  g.offsets = offsets;
+  g.n_tokens = T;
+  g.n_assign = n;
+  g.n_expert = static_cast<int>(n_expert);
+  g.w0 = c.packed_gate;
+  g.w1 = c.packed_up;
+  if (w_dtype == FMOE_F8E4M3FN) {
+    g.s0 = c.gate_scales;
+    g.s1 = c.up_scales;
+  }
+  g.N = n_ff;
+  g.K = n_embd;
+  g.out = h;
+  g.ldo = n_ff;
+  g.epi = EPI_SWIGLU;
+  g.act_dtype = act_dtype;
+  g.w_dtype = w_dtype;
+  g.w_format = packed_format(n_ff, n_embd, w_dtype);
+  g.out_dtype = L.h_dtype;
+  {
+    ScopedTimer t(FMOE_TIMER_GATE_UP, s);
+    FMOE_TRY(run_grouped_gemm(g, s));
+  }
+
+  // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
+  GroupedGemmArgs d;
+  d.a = h;
+  d.lda = n_ff;
+  d.a_mode = A_DIRECT;
+  d.order = order;
+  d.offsets = offsets;
+  d.n_tokens = T;
+  d.n_assign = n;
+  d.n_expert = static_cast<int>(n_expert);
+  d.w0 = c.packed_down;
+  d.s0 = w_dtype == FMOE_F8E4M3FN ? c.down_scales : nullptr;
+  d.N = n_embd;
+  d.K = n_ff;
+  d.out = y;
+  d.ldo = n_embd;
+  d.epi = EPI_SCATTER_WEIGHTED;
+  d.route_w = rw;
+  d.act_dtype = L.h_dtype;
+  d.w_dtype = w_dtype;
+  d.w_format = packed_format(n_embd, n_ff, w_dtype);
+  d.out_dtype = L.y_dtype;
+  d.split_stride = L.y_parts > 1 ? L.y_part_elems : 0;
+  int down_split = 1;
+  {
+    ScopedTimer t(FMOE_TIMER_DOWN, s);
+    FMOE_TRY(run_grouped_gemm(d, s, &down_split));
+  }
+
+  // Step 11: slot-ordered sum + transpose to [n_tokens, n_embd] (mlir:179-206),
+  // plus the residual for the sub-layer.
+  {
+    ScopedTimer t(FMOE_TIMER_COMBINE, s);
+    FMOE_HIP(launch_combine(y, L.y_dtype, c.residual, c.out, act_dtype, T, static_cast<int>(n_expert_used),
+                            static_cast<int>(n_embd), down_split, L.y_part_elems, s));
+  }
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -355,15 +525,6 @@ int fmoe_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtyp
   FMOE_TRY(ensure_device());
   FMOE_HIP(launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)));
   return ok();
-}
-
-static int validate_router(int64_t T, int64_t H, int64_t E, int64_t k) {
-  FMOE_TRY(check_dims("n_tokens", T, 0, kMaxDim));
-  FMOE_TRY(check_dims("n_embd", H, 1, kMaxDim));
-  FMOE_TRY(check_dims("n_expert", E, 1, kMaxExpert));
-  FMOE_TRY(check_dims("n_expert_used", k, 1, E < kMaxExpertUsed ? E : kMaxExpertUsed));
-  if (k * T > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_expert_used * n_tokens exceeds 2^31-1");
-  return FMOE_OK;
 }
 
 int fmoe_router(const void* input, const void* w_router, int64_t n_tokens, int64_t n_embd,
@@ -544,118 +705,69 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
                        int64_t n_tokens, int64_t n_expert, int64_t n_expert_used, int64_t n_embd,
                        int64_t n_ff, int normalize_weights, int act_dtype, void* workspace,
                        size_t workspace_bytes, void* stream) {
-  if (!act_dtype_ok(act_dtype)) return fail(FMOE_ERR_DTYPE, "activation dtype %d", act_dtype);
-  if (!w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", w_dtype);
-  if (act_dtype == FMOE_F32 && w_dtype != FMOE_F32)
-    return fail(FMOE_ERR_DTYPE, "f32 activations need f32 weights");
-  FMOE_TRY(validate_router(n_tokens, n_embd, n_expert, n_expert_used));
-  FMOE_TRY(check_dims("n_ff", n_ff, 0, kMaxDim));
-  if (normalize_weights != 0 && normalize_weights != 1)
-    return fail(FMOE_ERR_INVALID_ARGUMENT, "normalize_weights must be 0 or 1");
+  const BlockCall c{input,     w_router,   packed_up,     packed_gate, packed_down,       up_scales,
+                    gate_scales, down_scales, w_dtype,    out,         nullptr,           n_tokens,
+                    n_expert,  n_expert_used, n_embd,     n_ff,        normalize_weights, act_dtype,
+                    workspace, workspace_bytes, stream};
+  FMOE_TRY(validate_block(c));
   if (n_tokens == 0) return ok();
-  if (!input || !w_router || !packed_up || !packed_gate || !packed_down || !out || !workspace)
-    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
-  if (w_dtype == FMOE_F8E4M3FN && (!up_scales || !gate_scales || !down_scales))
-    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
   const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
-  if (workspace_bytes < L.total)
-    return fail(FMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, L.total);
-  if (reinterpret_cast<uintptr_t>(workspace) % kAlign)
-    return fail(FMOE_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
-  if (!aligned_for(input, act_dtype) || !aligned_for(out, act_dtype) ||
-      !aligned_for(w_router, act_dtype))
+  FMOE_TRY(check_workspace(workspace, workspace_bytes, L.total));
+  FMOE_TRY(ensure_device());
+  return run_block(c, L);
+}
+
+int fmoe_rms_norm(const void* input, const void* weight, float eps, void* out, int64_t n_rows,
+                  int64_t n_embd, int dtype, void* stream) {
+  if (!act_dtype_ok(dtype)) return fail(FMOE_ERR_DTYPE, "dtype %d", dtype);
+  FMOE_TRY(check_dims("n_rows", n_rows, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_embd", n_embd, 1, kMaxDim));
+  if (n_rows == 0) return ok();
+  if (!input || !weight || !out) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!aligned_for(input, dtype) || !aligned_for(weight, dtype) || !aligned_for(out, dtype))
     return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
   FMOE_TRY(ensure_device());
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int T = static_cast<int>(n_tokens);
-  const int n = static_cast<int>(n_tokens * n_expert_used);
-  int* ids = at<int>(workspace, L.ids);
-  float* rw = at<float>(workspace, L.weights);
-  int* err = at<int>(workspace, L.perm.err);
-  int* order = at<int>(workspace, L.perm.order);
-  int* offsets = at<int>(workspace, L.perm.offsets);
-  void* h = at<char>(workspace, L.h);
-  void* y = at<char>(workspace, L.y);
-
-  // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128).
-  {
-    ScopedTimer t(FMOE_TIMER_ROUTER, s);
-    FMOE_HIP(launch_router(input, w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
-                         static_cast<int>(n_expert_used), normalize_weights != 0, act_dtype, ids,
-                           rw, s));
-  }
-  // Group the slot-major assignments by expert (replaces the gather, mul_mat_id.mlir:50-61).
-  {
-    ScopedTimer t(FMOE_TIMER_PERMUTE, s);
-    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err, s));
-  }
-
-  // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
-  GroupedGemmArgs g;
-  g.a = input;
-  g.lda = n_embd;
-  g.a_mode = A_GATHER_TOKEN;
-  g.order = order;
-  g.offsets = offsets;
-  g.n_tokens = T;
-  g.n_assign = n;
-  g.n_expert = static_cast<int>(n_expert);
-  g.w0 = packed_gate;
-  g.w1 = packed_up;
-  if (w_dtype == FMOE_F8E4M3FN) {
-    g.s0 = gate_scales;
-    g.s1 = up_scales;
-  }
-  g.N = n_ff;
-  g.K = n_embd;
-  g.out = h;
-  g.ldo = n_ff;
-  g.epi = EPI_SWIGLU;
-  g.act_dtype = act_dtype;
-  g.w_dtype = w_dtype;
-  g.w_format = packed_format(n_ff, n_embd, w_dtype);
-  g.out_dtype = L.h_dtype;
-  {
-    ScopedTimer t(FMOE_TIMER_GATE_UP, s);
-    FMOE_TRY(run_grouped_gemm(g, s));
-  }
-
-  // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
-  GroupedGemmArgs d;
-  d.a = h;
-  d.lda = n_ff;
-  d.a_mode = A_DIRECT;
-  d.order = order;
-  d.offsets = offsets;
-  d.n_tokens = T;
-  d.n_assign = n;
-  d.n_expert = static_cast<int>(n_expert);
-  d.w0 = packed_down;
-  d.s0 = w_dtype == FMOE_F8E4M3FN ? down_scales : nullptr;
-  d.N = n_embd;
-  d.K = n_ff;
-  d.out = y;
-  d.ldo = n_embd;
-  d.epi = EPI_SCATTER_WEIGHTED;
-  d.route_w = rw;
-  d.act_dtype = L.h_dtype;
-  d.w_dtype = w_dtype;
-  d.w_format = packed_format(n_embd, n_ff, w_dtype);
-  d.out_dtype = L.y_dtype;
-  d.split_stride = L.y_parts > 1 ? L.y_part_elems : 0;
-  int down_split = 1;
-  {
-    ScopedTimer t(FMOE_TIMER_DOWN, s);
-    FMOE_TRY(run_grouped_gemm(d, s, &down_split));
-  }
-
-  // Step 11: slot-ordered sum + transpose to [n_tokens, n_embd] (mlir:179-206).
-  {
-    ScopedTimer t(FMOE_TIMER_COMBINE, s);
-    FMOE_HIP(launch_combine(y, L.y_dtype, out, act_dtype, T, static_cast<int>(n_expert_used),
-                            static_cast<int>(n_embd), down_split, L.y_part_elems, s));
-  }
+  FMOE_HIP(launch_rms_norm(input, weight, eps, out, n_rows, static_cast<int>(n_embd), dtype,
+                           static_cast<hipStream_t>(stream)));
   return ok();
+}
+
+size_t fmoe_moe_ffn_sublayer_workspace_bytes(int64_t n_tokens, int64_t n_expert, int64_t n_expert_used,
+                                             int64_t n_embd, int64_t n_ff, int act_dtype, int w_dtype) {
+  if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
+      n_expert_used < 1 || n_embd < 1 || n_ff < 0)
+    return 0;
+  return sublayer_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype).total;
+}
+
+int fmoe_moe_ffn_sublayer(const void* residual, const void* ffn_norm_w, float rms_eps, const void* w_router,
+                          const void* packed_up, const void* packed_gate, const void* packed_down,
+                          const float* up_scales, const float* gate_scales, const float* down_scales,
+                          int w_dtype, void* out, int64_t n_tokens, int64_t n_expert, int64_t n_expert_used,
+                          int64_t n_embd, int64_t n_ff, int normalize_weights, int act_dtype, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  BlockCall c{residual,  w_router,   packed_up,     packed_gate, packed_down,       up_scales,
+              gate_scales, down_scales, w_dtype,    out,         residual,          n_tokens,
+              n_expert,  n_expert_used, n_embd,     n_ff,        normalize_weights, act_dtype,
+              workspace, workspace_bytes, stream};
+  FMOE_TRY(validate_block(c));
+  if (n_tokens == 0) return ok();
+  if (!ffn_norm_w) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!aligned_for(ffn_norm_w, act_dtype)) return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  const SublayerLayout SL = sublayer_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
+  FMOE_TRY(check_workspace(workspace, workspace_bytes, SL.total));
+  FMOE_TRY(ensure_device());
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // ffn_norm (transformer_layer_moe_prefill.mlir:211-213): the normalised
+  // rows feed the router and the gate/up GEMM; the residual goes to combine.
+  void* xn = at<char>(workspace, SL.xn);
+  {
+    ScopedTimer t(FMOE_TIMER_NORM, s);
+    FMOE_HIP(launch_rms_norm(residual, ffn_norm_w, rms_eps, xn, n_tokens, static_cast<int>(n_embd), act_dtype,
+                             s));
+  }
+  c.input = xn;
+  return run_block(c, SL.block);
 }
 
 int fmoe_moe_ffn_block_routing(void* workspace, int64_t n_tokens, int64_t n_expert,

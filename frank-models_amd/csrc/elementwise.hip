@@ -5,7 +5,12 @@
 //   combine  out[t, :] = sum_{s=0..k-1} y[s*T + t, :] in slot order: the
 //            routing-weight product is applied by the down GEMM's epilogue,
 //            this is the slot reduction + transpose of
-//            moe_ffn_block.mlir:179-206 (oracles/moe.py:126-132)
+//            moe_ffn_block.mlir:179-206 (oracles/moe.py:126-132); optionally
+//            plus the layer's residual, residual + moe_out
+//            (transformer_layer_moe_prefill.mlir:229-242)
+//   rms_norm (x / sqrt(mean(x^2) + eps)) * weight per row
+//            (components/normalization/rms_norm.mlir:18-85,
+//            oracles/normalization.py:10-43)
 //   transpose / zero rows / fill: layout plumbing of the standalone
 //            mul_mat_id, whose input and output are feature-major
 //            [n, k, T] (mul_mat_id.mlir:63-117).
@@ -43,24 +48,112 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const T* __restrict__ 
   }
 }
 
-// out[t, c] = sum_s (y_0 + y_1 + ...)[s*T + t, c]: slots in order, K-split
-// partials summed first in split order.
-template <typename TY, typename TO>
+// V consecutive elements (V = 4: one 16-byte fp32 load per partial).
+template <int V>
+__device__ __forceinline__ void ldv(const float* p, int64_t i, float* v) {
+  if constexpr (V == 4) {
+    const f32x4_t q = *reinterpret_cast<const f32x4_t*>(p + i);
+    v[0] = q[0], v[1] = q[1], v[2] = q[2], v[3] = q[3];
+  } else {
+    v[0] = p[i];
+  }
+}
+template <int V>
+__device__ __forceinline__ void ldv(const bf16_t* p, int64_t i, float* v) {
+  if constexpr (V == 4) {
+    const u32x2_t q = *reinterpret_cast<const u32x2_t*>(p + i);
+    v[0] = __uint_as_float(q[0] << 16), v[1] = __uint_as_float(q[0] & 0xFFFF0000u);
+    v[2] = __uint_as_float(q[1] << 16), v[3] = __uint_as_float(q[1] & 0xFFFF0000u);
+  } else {
+    v[0] = bf16_to_f32(p[i]);
+  }
+}
+template <int V>
+__device__ __forceinline__ void stv(float* p, int64_t i, const float* v) {
+  if constexpr (V == 4)
+    *reinterpret_cast<f32x4_t*>(p + i) = f32x4_t{v[0], v[1], v[2], v[3]};
+  else
+    p[i] = v[0];
+}
+template <int V>
+__device__ __forceinline__ void stv(bf16_t* p, int64_t i, const float* v) {
+  if constexpr (V == 4)
+    *reinterpret_cast<u32x2_t*>(p + i) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  else
+    p[i] = f32_to_bf16(v[0]);
+}
+
+// out[t, c] = [residual[t, c] +] sum_s (y_0 + y_1 + ...)[s*T + t, c]: K-split
+// partials summed first in split order, then slots in order, in fp32; one
+// rounding to the output type.
+// out may alias residual: each element is read and then written by one thread.
+template <typename TY, typename TO, int V>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const TY* __restrict__ y,
-                                                           TO* __restrict__ out, int n_tokens,
+                                                           const TO* residual,
+                                                           TO* out, int n_tokens,
                                                            int k, int n_embd, int nsplit,
                                                            int64_t split_stride) {
   const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
   const int64_t slot_stride = total;  // y rows s*T + t -> element offset s*T*H + t*H
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * kThreads) {
-    float acc = 0.f;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * V; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kThreads * V) {
+    float acc[V], v[V], p[V];
     for (int s = 0; s < k; ++s) {
-      float v = ldf(y, i + s * slot_stride);
-      for (int p = 1; p < nsplit; ++p) v += ldf(y, i + s * slot_stride + p * split_stride);
-      acc = s == 0 ? v : acc + v;
+      ldv<V>(y, i + s * slot_stride, v);
+      for (int q = 1; q < nsplit; ++q) {
+        ldv<V>(y, i + s * slot_stride + q * split_stride, p);
+#pragma unroll
+        for (int j = 0; j < V; ++j) v[j] += p[j];
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = s == 0 ? v[j] : acc[j] + v[j];
     }
-    stf(out, i, acc);
+    if (residual) {
+      ldv<V>(residual, i, p);
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = p[j] + acc[j];
+    }
+    stv<V>(out, i, acc);
+  }
+}
+
+// One block per row (grid-stride over rows).  Sum of squares in fp32 (per
+// thread, then across the block), rms = sqrt(sum / H + eps), then
+// out = (x / rms) * weight, the reference's operation order.  out may alias
+// x: a thread writes only the elements it read in both passes.
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const T* x,
+                                                            const T* __restrict__ weight, float eps,
+                                                            T* out, int64_t n_rows,
+                                                            int n_embd) {
+  __shared__ float partial[kThreads / kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  for (int64_t r = blockIdx.x; r < n_rows; r += gridDim.x) {
+    const T* xr = x + r * n_embd;
+    float ss = 0.f;
+    for (int c = threadIdx.x * V; c < n_embd; c += kThreads * V) {
+      float v[V];
+      ldv<V>(xr, c, v);
+#pragma unroll
+      for (int j = 0; j < V; ++j) ss += v[j] * v[j];
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) partial[wave] = ss;
+    __syncthreads();
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) sum += partial[w];
+    __syncthreads();  // partial[] is rewritten by the next row
+    const float rms = sqrtf(sum / static_cast<float>(n_embd) + eps);
+    for (int c = threadIdx.x * V; c < n_embd; c += kThreads * V) {
+      float v[V], w[V];
+      ldv<V>(xr, c, v);
+      ldv<V>(weight, c, w);
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[j] = (v[j] / rms) * w[j];
+      stv<V>(out + r * n_embd, c, v);
+    }
   }
 }
 
@@ -125,27 +218,64 @@ hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
   return hipGetLastError();
 }
 
-hipError_t launch_combine(const void* y, int y_dtype, void* out, int out_dtype, int n_tokens,
-                          int k, int n_embd, int nsplit, int64_t split_stride, hipStream_t stream) {
+namespace {
+template <typename TY, typename TO>
+void combine_t(const void* y, const void* residual, void* out, int n_tokens, int k, int n_embd, int nsplit,
+               int64_t split_stride, hipStream_t stream) {
+  const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
+  // 4-wide when rows, partial strides and every pointer allow 16/8-byte access.
+  const bool vec = n_embd % 4 == 0 && split_stride % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % (4 * sizeof(TY)) == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % (4 * sizeof(TO)) == 0 &&
+                   reinterpret_cast<uintptr_t>(residual) % (4 * sizeof(TO)) == 0;
+  if (vec)
+    hipLaunchKernelGGL((combine_kernel<TY, TO, 4>), dim3(grid_for(total / 4)), dim3(kThreads), 0, stream,
+                       static_cast<const TY*>(y), static_cast<const TO*>(residual), static_cast<TO*>(out),
+                       n_tokens, k, n_embd, nsplit, split_stride);
+  else
+    hipLaunchKernelGGL((combine_kernel<TY, TO, 1>), dim3(grid_for(total)), dim3(kThreads), 0, stream,
+                       static_cast<const TY*>(y), static_cast<const TO*>(residual), static_cast<TO*>(out),
+                       n_tokens, k, n_embd, nsplit, split_stride);
+}
+
+template <typename T>
+void rms_norm_t(const void* x, const void* w, float eps, void* out, int64_t n_rows, int n_embd,
+                hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>(n_rows < 65536 ? n_rows : 65536);
+  const bool vec = n_embd % 4 == 0 && reinterpret_cast<uintptr_t>(x) % (4 * sizeof(T)) == 0 &&
+                   reinterpret_cast<uintptr_t>(w) % (4 * sizeof(T)) == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % (4 * sizeof(T)) == 0;
+  if (vec)
+    hipLaunchKernelGGL((rms_norm_kernel<T, 4>), dim3(grid), dim3(kThreads), 0, stream, static_cast<const T*>(x),
+                       static_cast<const T*>(w), eps, static_cast<T*>(out), n_rows, n_embd);
+  else
+    hipLaunchKernelGGL((rms_norm_kernel<T, 1>), dim3(grid), dim3(kThreads), 0, stream, static_cast<const T*>(x),
+                       static_cast<const T*>(w), eps, static_cast<T*>(out), n_rows, n_embd);
+}
+}  // namespace
+
+hipError_t launch_combine(const void* y, int y_dtype, const void* residual, void* out, int out_dtype,
+                          int n_tokens, int k, int n_embd, int nsplit, int64_t split_stride, hipStream_t stream) {
   const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
   if (total == 0) return hipSuccess;
-  const dim3 grid(grid_for(total));
   if (y_dtype == DT_F32 && out_dtype == DT_F32)
-    hipLaunchKernelGGL((combine_kernel<float, float>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const float*>(y), static_cast<float*>(out), n_tokens, k, n_embd, nsplit,
-                       split_stride);
+    combine_t<float, float>(y, residual, out, n_tokens, k, n_embd, nsplit, split_stride, stream);
   else if (y_dtype == DT_F32)
-    hipLaunchKernelGGL((combine_kernel<float, bf16_t>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const float*>(y), static_cast<bf16_t*>(out), n_tokens, k, n_embd, nsplit,
-                       split_stride);
+    combine_t<float, bf16_t>(y, residual, out, n_tokens, k, n_embd, nsplit, split_stride, stream);
   else if (out_dtype == DT_F32)
-    hipLaunchKernelGGL((combine_kernel<bf16_t, float>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const bf16_t*>(y), static_cast<float*>(out), n_tokens, k, n_embd, nsplit,
-                       split_stride);
+    combine_t<bf16_t, float>(y, residual, out, n_tokens, k, n_embd, nsplit, split_stride, stream);
   else
-    hipLaunchKernelGGL((combine_kernel<bf16_t, bf16_t>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const bf16_t*>(y), static_cast<bf16_t*>(out), n_tokens, k, n_embd, nsplit,
-                       split_stride);
+    combine_t<bf16_t, bf16_t>(y, residual, out, n_tokens, k, n_embd, nsplit, split_stride, stream);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const void* x, const void* weight, float eps, void* out, int64_t n_rows, int n_embd,
+                           int dtype, hipStream_t stream) {
+  if (n_rows == 0 || n_embd == 0) return hipSuccess;
+  if (dtype == DT_F32)
+    rms_norm_t<float>(x, weight, eps, out, n_rows, n_embd, stream);
+  else
+    rms_norm_t<bf16_t>(x, weight, eps, out, n_rows, n_embd, stream);
   return hipGetLastError();
 }
 

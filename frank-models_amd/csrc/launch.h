@@ -133,11 +133,15 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g);
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
                          int dtype, hipStream_t stream);
-// out[t, :] = sum over s = 0..k-1 (in order) of the K-split sum
-// (y_0 + y_1 + ...)[s*n_tokens + t, :], partials split_stride elements apart.
-hipError_t launch_combine(const void* y, int y_dtype, void* out, int out_dtype,
+// out[t, :] = [residual[t, :] +] sum over s = 0..k-1 (in order) of the
+// K-split sum (y_0 + y_1 + ...)[s*n_tokens + t, :], partials split_stride
+// elements apart; residual (out_dtype) may be null.
+hipError_t launch_combine(const void* y, int y_dtype, const void* residual, void* out, int out_dtype,
                           int n_tokens, int k, int n_embd, int nsplit, int64_t split_stride,
                           hipStream_t stream);
+// out[r, :] = (x[r, :] / sqrt(mean(x[r, :]^2) + eps)) * weight, fp32 arithmetic.
+hipError_t launch_rms_norm(const void* x, const void* weight, float eps, void* out, int64_t n_rows,
+                           int n_embd, int dtype, hipStream_t stream);
 // out[c, r] = in[r, c] for an in[rows, cols] matrix (same dtype).
 hipError_t launch_transpose(const void* in, void* out, int64_t rows, int64_t cols,
                             int dtype, hipStream_t stream);

@@ -121,15 +121,72 @@ def router_inputs(cfg: Config, n_tokens: int, seed: int | None = None, max_round
     return x, wr, {"redrawn_rows": int(redrawn)}
 
 
-def expert_weights(cfg: Config, device, seed: int | None = None, dtype=torch.float32):
-    """(up [F,H,E], gate [F,H,E], down [H,F,E]) ~ N(0, 0.02^2), drawn with a
-    seeded torch generator on `device`, returned in `dtype`."""
+def expert_weights(cfg: Config, device, seed: int | None = None, dtype=torch.float32, std: float = 0.02):
+    """(up [F,H,E], gate [F,H,E], down [H,F,E]) ~ N(0, std^2) (0.02 by
+    default), drawn with a seeded torch generator on `device`, returned in
+    `dtype`."""
     H, F, E = cfg.n_embd, cfg.n_ff, cfg.n_expert
     g = torch.Generator(device=device)
     g.manual_seed(cfg.seed * 7919 + 17 if seed is None else seed)
     out = []
     for shape in ((F, H, E), (F, H, E), (H, F, E)):
         w = torch.empty(shape, dtype=torch.float32, device=device)
-        w.normal_(0.0, 0.02, generator=g)
+        w.normal_(0.0, std, generator=g)
         out.append(w.to(dtype))
     return tuple(out)
+
+
+def _rms_norm64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = x.astype(np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + eps) * w.astype(np.float64)
+
+
+def sublayer_inputs(cfg: Config, n_tokens: int, seed: int | None = None, eps: float = 1e-5,
+                    scale_range=(0.25, 4.0), max_rounds: int = 200):
+    """Inputs of the MoE FFN sub-layer (ffn_norm -> block -> residual add):
+    -> (residual [T, H], ffn_norm_w [H], wr [E, H], eps, stats), rounded to the
+    activation dtype.
+
+    Residual rows are N(0, 1) times a per-row scale, log-uniform in
+    ``scale_range`` (so the norm has work to do; the block's output does not
+    depend on it); the norm weight is 1 + N(0, 0.1^2).  The router margin is
+    enforced on the NORMALISED rows -- what the router sees -- both exact and
+    rounded to the activation dtype.  For the Zipf configuration channel 0 of
+    the residual equals the row's RMS scale and its norm weight is 1, so the
+    normalised channel 0 stays near 1 and router column 0 keeps its bias."""
+    rng = np.random.default_rng(cfg.seed * 1000033 + n_tokens + 7 if seed is None else seed)
+    H, E, k = cfg.n_embd, cfg.n_expert, cfg.n_expert_used
+    rnd = bf16_round_np if cfg.act == "bf16" else (lambda a: np.asarray(a, np.float32))
+    wr = (rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    if cfg.zipf:
+        rank = rng.permutation(E) + 1
+        wr[:, 0] = (-cfg.zipf * np.log(rank)).astype(np.float32)
+    wr = rnd(wr)
+    nw = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    if cfg.zipf:
+        nw[0] = 1.0
+    nw = rnd(nw)
+
+    def draw(n):
+        lo, hi = scale_range
+        scale = np.exp(rng.uniform(np.log(lo), np.log(hi), (n, 1))).astype(np.float32)
+        x = rng.standard_normal((n, H), dtype=np.float32) * scale
+        if cfg.zipf:
+            x[:, 0] = scale[:, 0]
+        return rnd(x)
+
+    def gap(rows):
+        xn = _rms_norm64(rows, nw, eps)
+        return np.minimum(min_adjacent_gap(xn, wr, k), min_adjacent_gap(rnd(xn.astype(np.float32)), wr, k))
+
+    res = draw(n_tokens)
+    redrawn = 0
+    for _ in range(max_rounds):
+        bad = np.nonzero(gap(res) < cfg.margin)[0]
+        if bad.size == 0:
+            break
+        redrawn += bad.size
+        res[bad] = draw(bad.size)
+    else:
+        raise RuntimeError(f"{cfg.name}: could not meet router margin {cfg.margin}")
+    return res, nw, wr, eps, {"redrawn_rows": int(redrawn)}

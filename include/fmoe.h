@@ -5,6 +5,11 @@
  *   moe_ffn_block  components/moe/moe_ffn_block.mlir:34-209, oracles/moe.py:51-132
  *   mul_mat_id     components/moe/mul_mat_id.mlir:22-120,   oracles/moe.py:9-48
  *   swiglu         components/activation/swiglu.mlir:16-51, oracles/activation.py:11-21
+ * and the layer glue around the block:
+ *   rms_norm       components/normalization/rms_norm.mlir:18-85, oracles/normalization.py:10-43
+ *   MoE FFN sub-layer (ffn_norm -> moe_ffn_block -> residual add)
+ *                  architectures/llm/transformer_layer_moe_prefill.mlir:205-242,
+ *                  transformer_layer_moe_decode.mlir:227-255
  *
  * Conventions
  *   - Every pointer is a device pointer unless stated otherwise; every call is
@@ -93,7 +98,8 @@ typedef enum fmoe_timer {
   FMOE_TIMER_DOWN = 3,    /* grouped GEMM: down projection + routing weight */
   FMOE_TIMER_COMBINE = 4,
   FMOE_TIMER_MUL_MAT_ID = 5,
-  FMOE_TIMER_COUNT = 6
+  FMOE_TIMER_NORM = 6,    /* ffn_norm RMSNorm of the sub-layer */
+  FMOE_TIMER_COUNT = 7
 } fmoe_timer;
 int fmoe_timing_enable(int on);
 int fmoe_timing_read(double *ms_out, int64_t *launches_out, int n);
@@ -194,8 +200,39 @@ int fmoe_moe_ffn_block(const void *input, const void *w_router, const void *pack
                        int act_dtype, void *workspace, size_t workspace_bytes,
                        void *stream);
 
-/* Views into a block workspace after fmoe_moe_ffn_block on it: the routing it
- * computed (ids/weights [k, n_tokens]), the permutation (order [k*n_tokens],
+/* RMS normalisation of each row: out = (x / sqrt(mean(x^2) + eps)) * weight,
+ * x and out [n_rows, n_embd], weight [n_embd], all of `dtype` (F32 or BF16),
+ * fp32 arithmetic.  Replaces @rms_norm_linalg
+ * (components/normalization/rms_norm.mlir:18-85; oracles/normalization.py:10-43).
+ * out may alias x. */
+int fmoe_rms_norm(const void *input, const void *weight, float eps, void *out,
+                  int64_t n_rows, int64_t n_embd, int dtype, void *stream);
+
+/* The MoE FFN sub-layer of a transformer layer:
+ *   out = residual + moe_ffn_block(rms_norm(residual, ffn_norm_w, rms_eps), ...)
+ * (architectures/llm/transformer_layer_moe_prefill.mlir:205-242 on the
+ * flattened [n_tokens, n_embd] residual; transformer_layer_moe_decode.mlir:227-255).
+ * residual, out [n_tokens, n_embd] and ffn_norm_w [n_embd] are act_dtype; the
+ * other arguments are those of fmoe_moe_ffn_block.  The residual is added in
+ * fp32 by the block's final reduction (one rounding of the output).  out may
+ * alias residual (in-place residual update).  Workspace: fmoe_moe_ffn_sublayer_workspace_bytes; it
+ * begins with a block workspace, so fmoe_moe_ffn_block_routing reads the
+ * routing of the last call from it. */
+size_t fmoe_moe_ffn_sublayer_workspace_bytes(int64_t n_tokens, int64_t n_expert,
+                                             int64_t n_expert_used, int64_t n_embd,
+                                             int64_t n_ff, int act_dtype, int w_dtype);
+int fmoe_moe_ffn_sublayer(const void *residual, const void *ffn_norm_w, float rms_eps,
+                          const void *w_router, const void *packed_up,
+                          const void *packed_gate, const void *packed_down,
+                          const float *up_scales, const float *gate_scales,
+                          const float *down_scales, int w_dtype, void *out,
+                          int64_t n_tokens, int64_t n_expert, int64_t n_expert_used,
+                          int64_t n_embd, int64_t n_ff, int normalize_weights,
+                          int act_dtype, void *workspace, size_t workspace_bytes,
+                          void *stream);
+
+/* Views into a block (or sub-layer) workspace after a call on it: the routing
+ * it computed (ids/weights [k, n_tokens]), the permutation (order [k*n_tokens],
  * offsets [n_expert+1]).  Pointers are device pointers inside `workspace`. */
 int fmoe_moe_ffn_block_routing(void *workspace, int64_t n_tokens, int64_t n_expert,
                                int64_t n_expert_used, int64_t n_embd, int64_t n_ff,

@@ -108,6 +108,45 @@ def test_workspace_sizes(fm):
 
 
 @pytest.mark.skipif(not NO_GPU, reason="checks the no-device path")
+def test_layer_glue_entry_points(fm):
+    """fmoe_rms_norm and fmoe_moe_ffn_sublayer validate before touching a device."""
+    ll = fm.lowlevel
+    lib = ll.lib()
+    assert st(fm, "fmoe_rms_norm", None, None, 1e-6, None, 4, 8, ll.F8E4M3FN, None) == ll.ERR_DTYPE
+    assert st(fm, "fmoe_rms_norm", None, None, 1e-6, None, 4, 0, ll.F32, None) == ll.ERR_SHAPE
+    assert st(fm, "fmoe_rms_norm", None, None, 1e-6, None, 4, 8, ll.F32, None) == ll.ERR_INVALID_ARGUMENT
+    assert st(fm, "fmoe_rms_norm", None, None, 1e-6, None, 0, 8, ll.F32, None) == ll.OK  # no rows
+    # the sub-layer workspace is the block's plus the normalised rows
+    blk = lib.fmoe_moe_ffn_block_workspace_bytes(300, 8, 2, 4096, 14336, ll.BF16, ll.BF16)
+    sub = lib.fmoe_moe_ffn_sublayer_workspace_bytes(300, 8, 2, 4096, 14336, ll.BF16, ll.BF16)
+    assert sub == blk + (300 * 4096 * 2 + 255) // 256 * 256
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    args = [fake, fake, fake, fake, fake, None, None, None, ll.BF16, fake, 16, 8, 2, 64, 128, 0, ll.BF16]
+    # null norm weight
+    assert st(fm, "fmoe_moe_ffn_sublayer", fake, None, 1e-6, *args[1:], fake, sub, None) == ll.ERR_INVALID_ARGUMENT
+    # workspace sized for the block only
+    need = lib.fmoe_moe_ffn_sublayer_workspace_bytes(16, 8, 2, 64, 128, ll.BF16, ll.BF16)
+    blk16 = lib.fmoe_moe_ffn_block_workspace_bytes(16, 8, 2, 64, 128, ll.BF16, ll.BF16)
+    assert need > blk16
+    assert st(fm, "fmoe_moe_ffn_sublayer", fake, fake, 1e-6, *args[1:], fake, blk16, None) == ll.ERR_WORKSPACE
+    # the block's own checks apply (f32 activations with bf16 weights)
+    bad = list(args)
+    bad[16] = ll.F32
+    assert st(fm, "fmoe_moe_ffn_sublayer", fake, fake, 1e-6, *bad[1:], fake, need, None) == ll.ERR_DTYPE
+    # Python side: shapes are checked before any device work
+    with pytest.raises(ValueError):
+        fm.rms_norm(np.zeros((4, 8), np.float32), np.zeros(7, np.float32))
+    wr = np.zeros((4, 8), np.float32)
+    w3 = np.zeros((16, 8, 4), np.float32)
+    wd = np.zeros((8, 16, 4), np.float32)
+    with pytest.raises(ValueError):
+        fm.moe_ffn_sublayer(np.zeros((3, 8), np.float32), np.zeros(9, np.float32), 1e-6, wr, w3, w3, wd,
+                            4, 2, 8, 16, False)
+    with pytest.raises(TypeError):
+        fm.moe_ffn_sublayer(np.zeros((3, 8), np.float64), np.zeros(8, np.float32), 1e-6, wr, w3, w3, wd,
+                            4, 2, 8, 16, False)
+
+
 def test_no_device_is_an_error_not_a_crash(fm):
     ll = fm.lowlevel
     fake = ctypes.c_void_p(0x1000)  # validation passes; the device check must fail before any launch

@@ -356,3 +356,93 @@ def test_per_channel_quantisation():
     # e4m3 has 3 mantissa bits: relative error <= 2^-4 for normals
     big = np.abs(w) > s[:, None, :] * 2.0**-6
     assert np.all(np.abs(deq - w)[big] <= np.abs(w)[big] * 2.0**-4 + 1e-12)
+
+
+# ------------------------------------------------------------------ rms_norm / sub-layer
+def _rms_norm_mistakes():
+    """Plausible mistakes in an RMSNorm, each of which the pins below catch."""
+    def sum_not_mean(x, w, eps=1e-6):
+        return x / np.sqrt(np.sum(x * x, -1, keepdims=True) + eps) * w
+
+    def eps_outside_sqrt(x, w, eps=1e-6):
+        return x / (np.sqrt(np.mean(x * x, -1, keepdims=True)) + eps) * w
+
+    def weight_dropped(x, w, eps=1e-6):
+        return x / np.sqrt(np.mean(x * x, -1, keepdims=True) + eps)
+
+    return [sum_not_mean, eps_outside_sqrt, weight_dropped]
+
+
+def _rms_norm_pins(f):
+    """Closed forms that an RMSNorm must meet; returns the failures."""
+    bad = []
+    H = 16
+    w = np.linspace(0.5, 2.0, H)
+    # a constant row c: mean(x^2) = c^2, so out = c / sqrt(c^2 + eps) * w
+    for c, eps in ((3.0, 1e-6), (0.01, 1e-2), (-2.0, 0.5)):
+        x = np.full((1, H), c)
+        if not np.allclose(f(x, w, eps), c / math.sqrt(c * c + eps) * w, rtol=1e-12, atol=0):
+            bad.append(("constant", c, eps))
+    # a one-hot row v e_i: mean(x^2) = v^2 / H
+    x = np.zeros((1, H))
+    x[0, 5] = 4.0
+    ref = np.zeros(H)
+    ref[5] = 4.0 / math.sqrt(16.0 / H + 1e-3) * w[5]
+    if not np.allclose(f(x, w, 1e-3), ref, rtol=1e-12, atol=0):
+        bad.append("one-hot")
+    return bad
+
+
+def test_rms_norm_closed_forms():
+    assert _rms_norm_pins(oracle.rms_norm) == []
+    for mistake in _rms_norm_mistakes():
+        assert _rms_norm_pins(mistake), mistake.__name__
+
+
+def test_rms_norm_invariants_and_torch():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((5, 64)) * rng.uniform(0.1, 10.0, (5, 1))
+    w = rng.standard_normal(64)
+    # eps = 0: invariant under a positive per-row scale; unit weight gives unit RMS
+    np.testing.assert_allclose(oracle.rms_norm(x * 37.0, w, 0.0), oracle.rms_norm(x, w, 0.0), rtol=1e-12)
+    y = oracle.rms_norm(x, np.ones(64), 0.0)
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, -1)), 1.0, rtol=1e-12)
+    # torch's own RMSNorm
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x), (64,), torch.from_numpy(w), eps=1e-5).numpy()
+    np.testing.assert_allclose(oracle.rms_norm(x, w, 1e-5), ref, rtol=1e-12, atol=1e-14)
+    # float32 evaluation stays close to float64
+    np.testing.assert_allclose(oracle.rms_norm(x, w, 1e-5, dtype=np.float32), ref, rtol=1e-5, atol=1e-6)
+
+
+def _tiny_layer(rng, T=6, H=16, F=24, E=4, k=2):
+    res = rng.standard_normal((T, H)) * 2.0
+    nw = rng.uniform(0.5, 1.5, H)
+    wr = rng.standard_normal((E, H)) * 0.3
+    up = rng.standard_normal((F, H, E)) * 0.2
+    gate = rng.standard_normal((F, H, E)) * 0.2
+    down = rng.standard_normal((H, F, E)) * 0.2
+    return res, nw, wr, up, gate, down, E, k, H, F
+
+
+def test_sublayer_zero_experts_is_identity():
+    rng = np.random.default_rng(8)
+    res, nw, wr, up, gate, down, E, k, H, F = _tiny_layer(rng)
+    z = np.zeros_like(up)
+    out = oracle.moe_ffn_sublayer(res, nw, 1e-6, wr, z, z, np.zeros_like(down), E, k, H, F, True)
+    np.testing.assert_array_equal(out, res)
+
+
+def test_sublayer_is_residual_plus_block_of_norm():
+    rng = np.random.default_rng(9)
+    res, nw, wr, up, gate, down, E, k, H, F = _tiny_layer(rng)
+    out, ids, _ = oracle.moe_ffn_sublayer(res, nw, 1e-5, wr, up, gate, down, E, k, H, F, False,
+                                          return_routing=True)
+    # the pinned block (literal reference formula) on the pinned norm's output
+    xn = oracle.rms_norm(res, nw, 1e-5)
+    block = om.moe_ffn_block_literal(xn, wr, up, gate, down, E, k, H, F, False, dtype=np.float64)
+    np.testing.assert_allclose(out - res, block, rtol=1e-10, atol=1e-12)
+    ref_ids, _ = om.router(xn, wr, k, False)
+    np.testing.assert_array_equal(ids, ref_ids)
+    # planted mistake: routing on the un-normalised residual changes the output
+    wrong = res + om.moe_ffn_block_literal(res, wr, up, gate, down, E, k, H, F, False, dtype=np.float64)
+    assert not np.allclose(out, wrong, rtol=1e-6, atol=1e-8)
