@@ -13,6 +13,9 @@ Public API (same signatures as the reference's components/oracles):
   normalize_weights)``: ffn_norm, block and residual add of a transformer
   layer (transformer_layer_moe_prefill.mlir:205-242)
 
+and per-layer loading of GGUF-named MoE parameters (``load_moe_layers``,
+``save_packed`` / ``load_packed``, ``quantize_fp8``; see ``params``),
+
 plus ``router``, ``permute``, ``pack_expert_weights``,
 ``quantize_expert_weights``, ``QuantizedExpertWeights``,
 ``PackedExpertWeights`` and ``MoEFFNBlock`` (packed weights + reusable
@@ -44,6 +47,16 @@ from .api import (  # noqa: F401
     swiglu,
 )
 from . import _lib as lowlevel  # noqa: F401
+from . import params  # noqa: F401
+from .params import (  # noqa: F401
+    HPARAMS,
+    MoEFFNLayer,
+    MoEHParams,
+    load_moe_layers,
+    load_packed,
+    quantize_fp8,
+    save_packed,
+)
 
 _load_lib()
 
@@ -60,6 +73,13 @@ __all__ = [
     "QuantizedExpertWeights",
     "PackedExpertWeights",
     "MoEFFNBlock",
+    "MoEFFNLayer",
+    "MoEHParams",
+    "HPARAMS",
+    "load_moe_layers",
+    "save_packed",
+    "load_packed",
+    "quantize_fp8",
     "FmoeError",
     "NoDeviceError",
 ]
