@@ -55,8 +55,9 @@ def block_bytes(T, H, F, E, k, touched, wbytes=2, abytes=2):
     return touched * 3.0 * H * F * wbytes + E * H * abytes + 2.0 * T * H * abytes + 2.0 * T * k * 4
 
 
-def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None):
-    """Times `steps` block calls at T tokens; returns a dict of measurements."""
+def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=False):
+    """Times `steps` block calls at T tokens (and, with `sublayer`, the
+    norm + block + residual sub-layer); returns a dict of measurements."""
     x_np, wr_np, gen = wl.router_inputs(cfg, T)
     x = torch.from_numpy(x_np).to("cuda", torch.bfloat16)
     wr = torch.from_numpy(wr_np).to("cuda", torch.bfloat16)
@@ -96,9 +97,31 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None):
     ll.timing_enable(False)
     ids = block.routing(T)[0]
     touched = int(torch.unique(ids).numel())
-    return dict(T=T, elapsed=elapsed, ms=elapsed / steps * 1e3, tok_s=steps * T / elapsed,
-                kernels={k: (v[0] / v[1] if v[1] else 0.0) for k, v in kernels.items() if v[1]},
-                touched=touched, pack_s=pack_s, gen=gen, x_np=x_np, wr_np=wr_np, weights=weights)
+    res = dict(T=T, elapsed=elapsed, ms=elapsed / steps * 1e3, tok_s=steps * T / elapsed,
+               kernels={k: (v[0] / v[1] if v[1] else 0.0) for k, v in kernels.items() if v[1]},
+               touched=touched, pack_s=pack_s, gen=gen, x_np=x_np, wr_np=wr_np, weights=weights)
+    if sublayer:
+        # The MoE FFN sub-layer on the same batch as residual stream: ffn_norm,
+        # block, residual add (unit norm weight; routing is not checked here).
+        nw = torch.ones(cfg.n_embd, dtype=torch.bfloat16, device="cuda")
+        sub_out = torch.empty_like(out)
+        for _ in range(warmup):
+            block.sublayer(x, nw, 1e-5, out=sub_out)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            block.sublayer(x, nw, 1e-5, out=sub_out)
+        torch.cuda.synchronize()
+        res["sublayer_ms"] = (time.perf_counter() - t0) / steps * 1e3
+        ll.timing_read()
+        ll.timing_enable(True)
+        for _ in range(steps):
+            block.sublayer(x, nw, 1e-5, out=sub_out)
+        torch.cuda.synchronize()
+        k2 = ll.timing_read()
+        ll.timing_enable(False)
+        res["sublayer_kernels"] = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in k2.items() if v[1]}
+    return res
 
 
 def cpu_baseline(torch, cfg, res, sample):
@@ -142,7 +165,7 @@ def all_configs(fm, wl, torch, args):
         H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
         weights = None
         for T in cfg.tokens:
-            res = run_config(fm, wl, torch, cfg, T, max(5, args.steps // 2), 2, weights=weights)
+            res = run_config(fm, wl, torch, cfg, T, max(5, args.steps // 2), 5, weights=weights, sublayer=True)
             weights = res["weights"]
             wb = 1 if cfg.weights == "fp8" else 2
             flops = block_flops(T, H, F, E, k)
@@ -150,10 +173,14 @@ def all_configs(fm, wl, torch, args):
             row = {"config": name, "tokens": T, "ms": res["ms"], "tokens_per_s": res["tok_s"],
                    "mfma_frac": flops / (res["ms"] * 1e-3) / PEAK_BF16_FLOPS,
                    "hbm_frac": nbytes / (res["ms"] * 1e-3) / PEAK_HBM_BYTES,
-                   "experts_touched": res["touched"], "kernels_ms": res["kernels"]}
+                   "experts_touched": res["touched"], "kernels_ms": res["kernels"],
+                   "sublayer_ms": res["sublayer_ms"], "sublayer_kernels_ms": res["sublayer_kernels"]}
             rows.append(row)
             log(f"{name} T={T:5d}: {res['ms']:.3f} ms  {res['tok_s']:.0f} tok/s  mfma {row['mfma_frac']:.3f}  "
                 f"hbm {row['hbm_frac']:.3f}  {res['kernels']}")
+            log(f"{name} T={T:5d}: sub-layer {res['sublayer_ms']:.3f} ms  "
+                f"norm {res['sublayer_kernels'].get('norm', 0.0):.4f} ms  "
+                f"combine {res['sublayer_kernels'].get('combine', 0.0):.4f} ms")
         del weights
         torch.cuda.empty_cache()
     return rows
