@@ -188,7 +188,7 @@ int run_grouped_gemm(GroupedGemmArgs g, hipStream_t s, int* ksplit_used = nullpt
 
 // ------------------------------------------------------------ workspaces
 struct PermuteLayout {
-  size_t order, offsets, err, total;
+  size_t order, offsets, err, scratch, total;
 };
 
 PermuteLayout permute_layout(int64_t n_assign, int64_t n_expert, size_t base = 0) {
@@ -196,6 +196,8 @@ PermuteLayout permute_layout(int64_t n_assign, int64_t n_expert, size_t base = 0
   size_t off = base;
   L.err = off;
   off += align_up(16);
+  L.scratch = off;  // chunk histograms of a large batch
+  off += align_up(permute_scratch_bytes(static_cast<int>(n_assign), static_cast<int>(n_expert)));
   L.order = off;
   off += align_up(static_cast<size_t>(n_assign) * 4);
   L.offsets = off;
@@ -391,7 +393,8 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   // Group the slot-major assignments by expert (replaces the gather, mul_mat_id.mlir:50-61).
   {
     ScopedTimer t(FMOE_TIMER_PERMUTE, s);
-    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err, s));
+    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err,
+                            at<int>(workspace, L.perm.scratch), s));
   }
 
   // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
@@ -546,10 +549,11 @@ int fmoe_router(const void* input, const void* w_router, int64_t n_tokens, int64
 }
 
 size_t fmoe_permute_workspace_bytes(int64_t n_expert_used, int64_t n_tokens, int64_t n_expert) {
-  (void)n_expert_used;
-  (void)n_tokens;
-  (void)n_expert;
-  return align_up(16);
+  // error word, then the chunk histograms of a large batch
+  if (n_expert_used < 1 || n_tokens < 0 || n_expert < 1 || n_expert > 512 || n_expert_used * n_tokens > kMaxDim)
+    return align_up(16);
+  return align_up(16) + align_up(permute_scratch_bytes(static_cast<int>(n_expert_used * n_tokens),
+                                                       static_cast<int>(n_expert)));
 }
 
 int fmoe_permute(const int32_t* ids, int64_t n_expert_used, int64_t n_tokens, int64_t n_expert,
@@ -567,7 +571,8 @@ int fmoe_permute(const int32_t* ids, int64_t n_expert_used, int64_t n_tokens, in
   FMOE_TRY(ensure_device());
   FMOE_HIP(launch_permute(ids, static_cast<int>(n_expert_used * n_tokens),
                           static_cast<int>(n_expert), order_out, offsets_out,
-                          static_cast<int*>(workspace), static_cast<hipStream_t>(stream)));
+                          static_cast<int*>(workspace), at<int>(workspace, align_up(16)),
+                          static_cast<hipStream_t>(stream)));
   return ok();
 }
 
@@ -658,7 +663,8 @@ int fmoe_mul_mat_id(const void* packed_w, const float* w_scales, int w_dtype, co
   void* y = at<char>(workspace, L.y);
   // input [n_in, k*T] -> x [k*T, n_in]: row f = s*T + t (mul_mat_id.mlir:63-90)
   if (n_in > 0) FMOE_HIP(launch_transpose(input, x, n_in, n, act_dtype, s));
-  FMOE_HIP(launch_permute(ids, static_cast<int>(n), static_cast<int>(n_expert), order, offsets, err, s));
+  FMOE_HIP(launch_permute(ids, static_cast<int>(n), static_cast<int>(n_expert), order, offsets, err,
+                          at<int>(workspace, L.perm.scratch), s));
   GroupedGemmArgs g;
   g.a = x;
   g.lda = n_in;

@@ -106,8 +106,12 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
                          int n_expert, int k, bool normalize, int dtype, int* ids,
                          float* weights, hipStream_t stream);
 
+// Batches above kPermuteChunk assignments run chunked, with a histogram
+// scratch of permute_scratch_bytes() (0 for smaller batches).
+constexpr int kPermuteChunk = 2048;
+size_t permute_scratch_bytes(int n_assign, int n_expert);
 hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order,
-                          int* offsets, int* err_count, hipStream_t stream);
+                          int* offsets, int* err_count, int* scratch, hipStream_t stream);
 
 hipError_t launch_pack(const void* src, int src_dtype, const float* src_scales,
                        int n_out, int n_in, int n_expert, int dst_dtype, void* dst,

@@ -7,7 +7,7 @@
 // Grouping that order by expert, stably, lets every expert's weights be read
 // once per row tile instead of once per assignment.
 //
-// One block of 1024 threads (16 waves):
+// Small batches (n <= kChunk): one block of 1024 threads (16 waves):
 //   1. histogram with LDS atomics (counts are order-independent),
 //   2. exclusive scan of the counts -> offsets,
 //   3. tiles of 1024 ids in flat order: each wave ranks its lanes among the
@@ -16,6 +16,12 @@
 //      and a running per-expert base gives the rank among earlier tiles.
 //      Position = offset + earlier tiles + earlier waves + rank in wave,
 //      which is exactly the stable order.
+// Larger batches split the flat order into chunks of kChunk ids, one block
+// each, in two launches:
+//   a. per-chunk expert histograms (and a count of invalid ids),
+//   b. each chunk's block sums the histograms into the expert offsets and
+//      its own per-expert base (offset + the counts of earlier chunks), then
+//      runs step 3 over its chunk.  Chunk 0 writes the offsets.
 #include "common.h"
 #include "launch.h"
 
@@ -25,6 +31,51 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxExpert = 512;
+constexpr int kHistThreads = 256;
+
+// Step 3 over ids [f_begin, f_end): base[e] holds the position of the first
+// id of expert e at or after f_begin; wcnt[][] must be zero on entry and is
+// zero on exit.
+__device__ __forceinline__ void scatter_range(const int* __restrict__ ids, int f_begin, int f_end, int n_expert,
+                                              int* base, int (*wcnt)[kMaxExpert], int* __restrict__ order) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  int nbits = 0;
+  while ((1 << nbits) < n_expert) ++nbits;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+
+  for (int f0 = f_begin; f0 < f_end; f0 += kThreads) {
+    const int f = f0 + tid;
+    const int e = f < f_end ? ids[f] : -1;
+    const bool valid = e >= 0 && e < n_expert;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = __popcll(peers & lt_mask);
+    if (valid && rank == 0) wcnt[wave][e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int pre = 0;
+      for (int w = 0; w < wave; ++w) pre += wcnt[w][e];
+      order[base[e] + pre + rank] = f;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < n_expert; ee += kThreads) {
+      int tot = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        tot += wcnt[w][ee];
+        wcnt[w][ee] = 0;
+      }
+      base[ee] += tot;
+    }
+    __syncthreads();
+  }
+}
 
 __global__ __launch_bounds__(kThreads) void permute_kernel(const int* __restrict__ ids, int n,
                                                            int n_expert, int* __restrict__ order,
@@ -72,50 +123,104 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const int* __restrict
     }
   }
   __syncthreads();
+  scatter_range(ids, 0, n, n_expert, base, wcnt, order);
+}
 
-  int nbits = 0;
-  while ((1 << nbits) < n_expert) ++nbits;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-
-  for (int f0 = 0; f0 < n; f0 += kThreads) {
-    const int f = f0 + tid;
-    const int e = f < n ? ids[f] : -1;
-    const bool valid = e >= 0 && e < n_expert;
-    uint64_t peers = __ballot(valid);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = valid && ((e >> b) & 1);
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
-    }
-    const int rank = __popcll(peers & lt_mask);
-    if (valid && rank == 0) wcnt[wave][e] = __popcll(peers);
-    __syncthreads();
-    if (valid) {
-      int pre = 0;
-      for (int w = 0; w < wave; ++w) pre += wcnt[w][e];
-      order[base[e] + pre + rank] = f;
-    }
-    __syncthreads();
-    for (int ee = tid; ee < n_expert; ee += kThreads) {
-      int tot = 0;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        tot += wcnt[w][ee];
-        wcnt[w][ee] = 0;
-      }
-      base[ee] += tot;
-    }
-    __syncthreads();
+// counts[c * (n_expert + 1) + e]: ids of expert e in chunk c; entry n_expert
+// counts the invalid ids.
+__global__ __launch_bounds__(kHistThreads) void chunk_hist_kernel(const int* __restrict__ ids, int n,
+                                                                  int n_expert, int* __restrict__ counts) {
+  __shared__ int h[kMaxExpert + 1];
+  for (int e = threadIdx.x; e <= n_expert; e += kHistThreads) h[e] = 0;
+  __syncthreads();
+  const int f0 = blockIdx.x * kPermuteChunk;
+  const int f1 = min(n, f0 + kPermuteChunk);
+  for (int f = f0 + threadIdx.x; f < f1; f += kHistThreads) {
+    const int e = ids[f];
+    atomicAdd(&h[(e >= 0 && e < n_expert) ? e : n_expert], 1);
   }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= n_expert; e += kHistThreads)
+    counts[static_cast<int64_t>(blockIdx.x) * (n_expert + 1) + e] = h[e];
+}
+
+__global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __restrict__ ids, int n,
+                                                                 int n_expert, const int* __restrict__ counts,
+                                                                 int n_chunks, int* __restrict__ order,
+                                                                 int* __restrict__ offsets,
+                                                                 int* __restrict__ err_count) {
+  __shared__ int base[kMaxExpert];
+  __shared__ int total[kMaxExpert];
+  __shared__ int wcnt[kWaves][kMaxExpert];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int chunk = blockIdx.x;
+  const int stride = n_expert + 1;
+
+  for (int e = tid; e < n_expert; e += kThreads) {
+    int tot = 0, pre = 0;
+    for (int c = 0; c < n_chunks; ++c) {
+      const int v = counts[c * stride + e];
+      tot += v;
+      pre += c < chunk ? v : 0;
+    }
+    total[e] = tot;
+    base[e] = pre;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) wcnt[w][e] = 0;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int running = 0;
+    for (int c = 0; c < n_expert; c += kWave) {
+      const int e = c + lane;
+      const int v = e < n_expert ? total[e] : 0;
+      const int incl = wave_inclusive_scan(v);
+      if (e < n_expert) {
+        const int off = running + incl - v;
+        base[e] += off;
+        if (chunk == 0) offsets[e] = off;
+      }
+      running += __shfl(incl, kWave - 1, kWave);
+    }
+    if (chunk == 0) {
+      int bad = 0;
+      for (int c = lane; c < n_chunks; c += kWave) bad += counts[c * stride + n_expert];
+      bad = wave_sum(bad);
+      if (lane == 0) {
+        offsets[n_expert] = running;
+        err_count[0] = bad;
+      }
+    }
+  }
+  __syncthreads();
+  const int f0 = chunk * kPermuteChunk;
+  scatter_range(ids, f0, min(n, f0 + kPermuteChunk), n_expert, base, wcnt, order);
 }
 
 }  // namespace
 
+size_t permute_scratch_bytes(int n_assign, int n_expert) {
+  if (n_assign <= kPermuteChunk) return 0;
+  const int64_t chunks = (static_cast<int64_t>(n_assign) + kPermuteChunk - 1) / kPermuteChunk;
+  return static_cast<size_t>(chunks * (n_expert + 1)) * sizeof(int);
+}
+
 hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order, int* offsets,
-                          int* err_count, hipStream_t stream) {
+                          int* err_count, int* scratch, hipStream_t stream) {
   if (n_expert > kMaxExpert || n_expert <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
-                     order, offsets, err_count);
+  if (n_assign <= kPermuteChunk) {
+    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
+                       order, offsets, err_count);
+    return hipGetLastError();
+  }
+  if (!scratch) return hipErrorInvalidValue;
+  const int chunks = (n_assign + kPermuteChunk - 1) / kPermuteChunk;
+  hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks), dim3(kHistThreads), 0, stream, ids, n_assign, n_expert,
+                     scratch);
+  hipLaunchKernelGGL(chunk_scatter_kernel, dim3(chunks), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
+                     scratch, chunks, order, offsets, err_count);
   return hipGetLastError();
 }
 

@@ -105,6 +105,10 @@ def test_workspace_sizes(fm):
     assert lib.fmoe_packed_weight_bytes(14336, 4096, 8, ll.BF16) == 14336 * 4096 * 8 * 2 + 256 * 4096 * 2
     assert lib.fmoe_packed_weight_bytes(14336, 4096, 8, ll.F8E4M3FN) == 14336 * 4096 * 8 + 256 * 4096 * 2
     assert lib.fmoe_mul_mat_id_workspace_bytes(64, 32, 8, 2, 16, ll.F32) > 0
+    # permutation: an error word; above 2048 assignments also a histogram per
+    # chunk of 2048 (n_expert + 1 counts each)
+    assert lib.fmoe_permute_workspace_bytes(2, 1024, 8) == 256
+    assert lib.fmoe_permute_workspace_bytes(8, 8192, 128) == 256 + (32 * 129 * 4 + 255) // 256 * 256
 
 
 @pytest.mark.skipif(not NO_GPU, reason="checks the no-device path")

@@ -85,6 +85,38 @@ def test_router_configs(fm, wl, cfg_name, T):
         _router_check(fm, x, wr, cfg.n_expert_used, cfg.normalize)
 
 
+# Large batches with 33..128 experts and uneven expert counts (33, 40, 80
+# leave MFMA columns partly unused).
+@pytest.mark.parametrize("E,k,H,T", [(128, 8, 2048, 8192), (64, 6, 2048, 512), (80, 4, 256, 300),
+                                     (40, 2, 128, 256), (33, 1, 64, 1000)])
+def test_router_wide(fm, wl, E, k, H, T):
+    cfg = wl.Config("R", H, 64, E, k, (T,), "bf16", "bf16", True, 1e-4, seed=E)
+    x, wr, _ = wl.router_inputs(cfg, T)
+    xt = torch.from_numpy(x).to("cuda", torch.bfloat16)
+    wt = torch.from_numpy(wr).to("cuda", torch.bfloat16)
+    ids, w = fm.router(xt, wt, k, True)
+    rids, rw = om.router(x, wr, k, True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+
+
+def test_router_wide_ties_lower_index(fm):
+    # one-hot rows over a large batch: token t's logits are router column
+    # t % 3, exactly
+    E, H, T = 48, 64, 300
+    wr = np.zeros((E, H), np.float32)
+    wr[[7, 20, 33], 0] = 5.0   # three-way tie at the top
+    wr[[41, 40], 2] = 1.0      # two-way tie; column 1 is all equal
+    x = np.zeros((T, H), np.float32)
+    x[np.arange(T), np.arange(T) % 3] = 1.0
+    ids, _ = fm.router(torch.from_numpy(x).to("cuda", torch.bfloat16), torch.from_numpy(wr).to("cuda", torch.bfloat16),
+                       2, False)
+    want = {0: [7, 20], 1: [0, 1], 2: [40, 41]}
+    got = ids.cpu().numpy()
+    for t in range(T):
+        assert list(got[:, t]) == want[t % 3], t
+
+
 def test_router_ties_lower_index(fm):
     # identity inputs make the logits equal to the router columns exactly
     logits = np.array([[1.0, 0.0, 5.0], [2.0, 0.0, 5.0], [2.0, 0.0, 5.0], [0.0, 0.0, 5.0]], np.float32)
@@ -121,8 +153,11 @@ def test_permute_reference_ids(fm, case):
     np.testing.assert_array_equal(offsets, roff)
 
 
+# Batches above 2048 assignments take the chunked two-kernel path; 2048 and
+# 2049 sit on either side of the switch.
 @pytest.mark.parametrize("E,k,T,skew", [(8, 2, 4096, 0), (128, 8, 8192, 1.1), (64, 6, 64, 0),
-                                        (8, 2, 1, 0), (512, 1, 3000, 0), (4, 4, 1500, 0), (2, 1, 70000, 0)])
+                                        (8, 2, 1, 0), (512, 1, 3000, 0), (4, 4, 1500, 0), (2, 1, 70000, 0),
+                                        (4, 1, 2048, 0), (4, 1, 2049, 0), (16, 2, 1025, 0)])
 def test_permute_random(fm, E, k, T, skew):
     rng = np.random.default_rng(E * 7 + k + T)
     if skew:
@@ -152,6 +187,26 @@ def test_permute_device_ids_out_of_range(fm):
     ids = torch.tensor([[0, 9, 1], [2, -1, 3]], dtype=torch.int32, device="cuda")
     with pytest.raises(IndexError):
         fm.permute(ids, 8)
+    # chunked path: invalid ids in two different chunks are counted, the valid
+    # ones still grouped stably
+    ll = fm.lowlevel
+    host = np.random.default_rng(5).integers(0, 8, (2, 3000)).astype(np.int32)
+    host[0, 10] = 8
+    host[1, 2900] = -3
+    d = torch.from_numpy(host).cuda()
+    with pytest.raises(IndexError, match="2 expert id"):
+        fm.permute(d, 8)
+    order = torch.empty(6000, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(9, dtype=torch.int32, device="cuda")
+    ws = torch.empty(ll.lib().fmoe_permute_workspace_bytes(2, 3000, 8), dtype=torch.uint8, device="cuda")
+    ll.call("fmoe_permute", d.data_ptr(), 2, 3000, 8, order.data_ptr(), offsets.data_ptr(), ws.data_ptr(),
+            ws.numel(), torch.cuda.current_stream().cuda_stream)
+    flat = host.reshape(-1)
+    valid = np.nonzero((flat >= 0) & (flat < 8))[0]
+    ref = valid[np.argsort(flat[valid], kind="stable")]
+    off = offsets.cpu().numpy()
+    assert off[-1] == valid.size
+    np.testing.assert_array_equal(order.cpu().numpy()[: valid.size], ref)
 
 
 # ------------------------------------------------------------------ packing
