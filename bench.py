@@ -236,7 +236,7 @@ def main():
     achieved = gu_flops / (gu_ms * 1e-3) / 1e12 if gu_ms else 0.0
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
                 "frac": achieved * 1e12 / PEAK_BF16_FLOPS, "traffic": read_traffic("gate_up_prefill"),
-                "kernel": "gemm_tiled_kernel<SWIGLU> (gate+up grouped GEMM, SwiGLU epilogue)",
+                "kernel": "gemm_tiled256_kernel<SWIGLU> (gate+up grouped GEMM, SwiGLU epilogue)",
                 "kernel_ms": gu_ms, "flops_per_launch": gu_flops}
     flops = block_flops(T, H, F, E, k)
     result = {

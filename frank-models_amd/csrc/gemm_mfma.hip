@@ -451,8 +451,10 @@ bool gemm_stream_supported(const GroupedGemmArgs& g) {
 int resolve_tiled_variant(const GroupedGemmArgs& g, int variant) {
   const bool large_ok = gemm_tiled256_supported(g);
   const bool small_ok = mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0 && g.ksplit == 1;
-  if (variant == TILED_AUTO)
-    variant = (large_ok && static_cast<int64_t>(g.n_assign) >= 512ll * g.n_expert) ? TILED_256 : TILED_128;
+  // The 256-tile kernel skips the MFMAs of empty row groups, so it wins at
+  // every batch the tiled path serves (measured from ~64 rows per expert);
+  // the 128-row kernel covers what it does not support.
+  if (variant == TILED_AUTO) variant = large_ok ? TILED_256 : TILED_128;
   if (variant == TILED_256 && large_ok) return TILED_256;
   if (small_ok) return TILED_128;
   return large_ok ? TILED_256 : -1;

@@ -121,8 +121,8 @@ hipError_t launch_gemm_generic(const GroupedGemmArgs& g, hipStream_t stream);
 // Returns hipErrorNotSupported when the shape or dtype is outside what the
 // MFMA kernels handle; the caller then uses the generic kernel.
 enum TiledVariant { TILED_AUTO = 0, TILED_128 = 1, TILED_256 = 2 };
-// The tiled kernel that `variant` resolves to for g (TILED_AUTO picks
-// 256x256 tiles when experts average >= 512 rows), or -1 if none applies.
+// The tiled kernel that `variant` resolves to for g (TILED_AUTO picks the
+// 256x256-tile kernel wherever it applies), or -1 if none applies.
 int resolve_tiled_variant(const GroupedGemmArgs& g, int variant);
 hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t stream, int variant);
 hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t stream);
