@@ -422,6 +422,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   g.w_dtype = w_dtype;
   g.w_format = packed_format(n_ff, n_embd, w_dtype);
   g.out_dtype = L.h_dtype;
+  g.max_rows_per_expert = T;  // top-k experts are distinct per token
   {
     ScopedTimer t(FMOE_TIMER_GATE_UP, s);
     FMOE_TRY(run_grouped_gemm(g, s));
@@ -450,6 +451,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   d.w_format = packed_format(n_embd, n_ff, w_dtype);
   d.out_dtype = L.y_dtype;
   d.split_stride = L.y_parts > 1 ? L.y_part_elems : 0;
+  d.max_rows_per_expert = T;
   int down_split = 1;
   {
     ScopedTimer t(FMOE_TIMER_DOWN, s);

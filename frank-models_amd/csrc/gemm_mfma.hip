@@ -283,11 +283,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled_kernel(GroupedGemmArgs
 }
 
 // ======================================================================= stream
+// Weight blocks are read exactly once per launch (a pass covers up to 64 of
+// an expert's rows), so they are loaded non-temporally: they do not push the
+// token rows and outputs out of the caches.
+__device__ __forceinline__ u32x4_t stream_load(const u32x4_t* p) { return __builtin_nontemporal_load(p); }
+
 constexpr int kStreamRowsPerWave = 16;
 constexpr int kStreamRows = 4 * kStreamRowsPerWave;  // weight rows per set per block
 constexpr int kStreamUnroll = 8;                     // 32-input steps per iteration
 
-template <int EPI, int NSETS, bool F8>
+// Decode-sized grouped GEMM: block = (expert, 64 weight rows per set), wave =
+// 16 weight rows.  The weights stream from HBM straight into MFMA registers
+// (kStreamUnroll 1 KiB blocks per set in flight per wave) and each fragment
+// is applied to up to kStreamTiles 16-row tiles of the expert's token rows,
+// so an expert's weights are read once for up to 16 * kStreamTiles rows.  An
+// expert has at most n_tokens rows (top-k picks distinct experts), so the
+// launcher sizes kStreamTiles from n_tokens and decode batches keep the
+// one-tile register footprint.
+template <int EPI, int NSETS, bool F8, int kStreamTiles>
 __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   const int e = blockIdx.x / col_tiles;
   const int ct = blockIdx.x - e * col_tiles;
@@ -311,75 +324,99 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g
   }
   const int ksteps = static_cast<int>(K / 32);
   const int kq = (lane >> 4) * 8;  // this lane's 8 inputs within a 32-input step
+  const u32x4_t zero{0u, 0u, 0u, 0u};
 
-  for (int m0 = 0; m0 < count; m0 += 16) {
-    const int r = m0 + (lane & 15);
-    const bool r_ok = r < count;
-    const bf16_t* arow = static_cast<const bf16_t*>(g.a) +
-                         a_source_row(g, row_begin + (r_ok ? r : 0)) * g.lda + kq;
-    f32x4_t acc[NSETS];
+  for (int m0 = 0; m0 < count; m0 += 16 * kStreamTiles) {
+    const int nt = min(kStreamTiles, (count - m0 + 15) / 16);  // wave-uniform
+    const bf16_t* arow[kStreamTiles];
+    bool r_ok[kStreamTiles];
 #pragma unroll
-    for (int s = 0; s < NSETS; ++s) acc[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < kStreamTiles; ++mt) {
+      const int r = m0 + mt * 16 + (lane & 15);
+      r_ok[mt] = r < count;
+      arow[mt] = static_cast<const bf16_t*>(g.a) + a_source_row(g, row_begin + (r_ok[mt] ? r : 0)) * g.lda + kq;
+    }
+    f32x4_t acc[kStreamTiles][NSETS];
+#pragma unroll
+    for (int mt = 0; mt < kStreamTiles; ++mt)
+#pragma unroll
+      for (int s = 0; s < NSETS; ++s) acc[mt][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     int ks = 0;
     for (; ks + kStreamUnroll <= ksteps; ks += kStreamUnroll) {
-      u32x4_t tok[kStreamUnroll];
       u32x4_t wv[NSETS][kStreamUnroll];
-#pragma unroll
-      for (int u = 0; u < kStreamUnroll; ++u)
-        tok[u] = r_ok ? *reinterpret_cast<const u32x4_t*>(arow + (ks + u) * 32) : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int s = 0; s < NSETS; ++s) {
         if (F8) {
 #pragma unroll
           for (int u = 0; u < kStreamUnroll; u += 2) {
-            const u32x4_t q = *reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>((ks + u) / 2) * 1024);
+            const u32x4_t q =
+                stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>((ks + u) / 2) * 1024));
             f8x16_to_bf16(q, wv[s][u], wv[s][u + 1]);
           }
         } else {
 #pragma unroll
           for (int u = 0; u < kStreamUnroll; ++u)
-            wv[s][u] = *reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks + u) * 1024);
+            wv[s][u] = stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks + u) * 1024));
         }
       }
 #pragma unroll
-      for (int u = 0; u < kStreamUnroll; ++u)
+      for (int mt = 0; mt < kStreamTiles; ++mt) {
+        if (mt < nt) {
+          u32x4_t tok[kStreamUnroll];
 #pragma unroll
-        for (int s = 0; s < NSETS; ++s) acc[s] = mfma16(wv[s][u], tok[u], acc[s]);
-    }
-    for (; ks < ksteps; ks += F8 ? 2 : 1) {  // tail (K % 128 != 0)
-      const u32x4_t t0 = r_ok ? *reinterpret_cast<const u32x4_t*>(arow + ks * 32) : u32x4_t{0u, 0u, 0u, 0u};
-      if (F8) {
-        const u32x4_t t1 = r_ok ? *reinterpret_cast<const u32x4_t*>(arow + (ks + 1) * 32) : u32x4_t{0u, 0u, 0u, 0u};
+          for (int u = 0; u < kStreamUnroll; ++u)
+            tok[u] = r_ok[mt] ? *reinterpret_cast<const u32x4_t*>(arow[mt] + (ks + u) * 32) : zero;
 #pragma unroll
-        for (int s = 0; s < NSETS; ++s) {
-          u32x4_t w0, w1;
-          f8x16_to_bf16(*reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks / 2) * 1024), w0, w1);
-          acc[s] = mfma16(w0, t0, acc[s]);
-          acc[s] = mfma16(w1, t1, acc[s]);
+          for (int u = 0; u < kStreamUnroll; ++u)
+#pragma unroll
+            for (int s = 0; s < NSETS; ++s) acc[mt][s] = mfma16(wv[s][u], tok[u], acc[mt][s]);
         }
-      } else {
+      }
+    }
+    for (; ks < ksteps; ks += F8 ? 2 : 1) {  // tail (K % 256 != 0)
 #pragma unroll
-        for (int s = 0; s < NSETS; ++s)
-          acc[s] = mfma16(*reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks) * 1024), t0, acc[s]);
+      for (int s = 0; s < NSETS; ++s) {
+        u32x4_t w0, w1;
+        if (F8) {
+          f8x16_to_bf16(stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks / 2) * 1024)),
+                        w0, w1);
+        } else {
+          w0 = stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks) * 1024));
+          w1 = zero;
+        }
+#pragma unroll
+        for (int mt = 0; mt < kStreamTiles; ++mt) {
+          if (mt < nt) {
+            const u32x4_t t0 = r_ok[mt] ? *reinterpret_cast<const u32x4_t*>(arow[mt] + ks * 32) : zero;
+            acc[mt][s] = mfma16(w0, t0, acc[mt][s]);
+            if (F8) {
+              const u32x4_t t1 = r_ok[mt] ? *reinterpret_cast<const u32x4_t*>(arow[mt] + (ks + 1) * 32) : zero;
+              acc[mt][s] = mfma16(w1, t1, acc[mt][s]);
+            }
+          }
+        }
       }
     }
 
-    if (r_ok) {
-      const int64_t n = n_base + 4 * (lane >> 4);
-      float4 sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
-      if (F8) {
-        sc0 = *reinterpret_cast<const float4*>(g.s0 + static_cast<int64_t>(e) * N + n);
-        if (NSETS == 2) sc1 = *reinterpret_cast<const float4*>(g.s1 + static_cast<int64_t>(e) * N + n);
-      }
-      const int p = row_begin + r;
-      const f32x4_t a0 = acc[0];
-      if (EPI == EPI_SWIGLU) {
-        const f32x4_t a1 = acc[NSETS - 1];
-        store4<EPI>(g, p, n, silu_mul(a0[0] * sc0.x, a1[0] * sc1.x), silu_mul(a0[1] * sc0.y, a1[1] * sc1.y),
-                    silu_mul(a0[2] * sc0.z, a1[2] * sc1.z), silu_mul(a0[3] * sc0.w, a1[3] * sc1.w));
-      } else {
-        store4<EPI>(g, p, n, a0[0] * sc0.x, a0[1] * sc0.y, a0[2] * sc0.z, a0[3] * sc0.w);
+    const int64_t n = n_base + 4 * (lane >> 4);
+    float4 sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
+    if (F8) {
+      sc0 = *reinterpret_cast<const float4*>(g.s0 + static_cast<int64_t>(e) * N + n);
+      if (NSETS == 2) sc1 = *reinterpret_cast<const float4*>(g.s1 + static_cast<int64_t>(e) * N + n);
+    }
+#pragma unroll
+    for (int mt = 0; mt < kStreamTiles; ++mt) {
+      if (mt < nt && r_ok[mt]) {
+        const int p = row_begin + m0 + mt * 16 + (lane & 15);
+        const f32x4_t a0 = acc[mt][0];
+        if (EPI == EPI_SWIGLU) {
+          const f32x4_t a1 = acc[mt][NSETS - 1];
+          store4<EPI>(g, p, n, silu_mul(a0[0] * sc0.x, a1[0] * sc1.x), silu_mul(a0[1] * sc0.y, a1[1] * sc1.y),
+                      silu_mul(a0[2] * sc0.z, a1[2] * sc1.z), silu_mul(a0[3] * sc0.w, a1[3] * sc1.w));
+        } else {
+          store4<EPI>(g, p, n, a0[0] * sc0.x, a0[1] * sc0.y, a0[2] * sc0.z, a0[3] * sc0.w);
+        }
       }
     }
   }
@@ -424,17 +461,29 @@ hipError_t launch_tiled_t(const GroupedGemmArgs& g, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <bool F8, int TILES>
+void launch_stream_tiles(const GroupedGemmArgs& g, hipStream_t s, dim3 grid, int col_tiles) {
+  if (g.epi == EPI_SWIGLU)
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
+  else if (g.epi == EPI_SCATTER_WEIGHTED)
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER_WEIGHTED, 1, F8, TILES>), grid, dim3(kThreads), 0, s, g,
+                       col_tiles);
+  else
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER, 1, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
+}
+
 template <bool F8>
 hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
   const int col_tiles = static_cast<int>((g.N + kStreamRows - 1) / kStreamRows);
   const dim3 grid(static_cast<unsigned>(col_tiles * g.n_expert));
-  if (g.epi == EPI_SWIGLU)
-    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8>), grid, dim3(kThreads), 0, s, g, col_tiles);
-  else if (g.epi == EPI_SCATTER_WEIGHTED)
-    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER_WEIGHTED, 1, F8>), grid, dim3(kThreads), 0, s, g,
-                       col_tiles);
+  // Rows one pass must cover to read each expert's weights once.
+  const int rows = g.max_rows_per_expert > 0 ? g.max_rows_per_expert : g.n_assign;
+  if (rows <= 16)
+    launch_stream_tiles<F8, 1>(g, s, grid, col_tiles);
+  else if (rows <= 32)
+    launch_stream_tiles<F8, 2>(g, s, grid, col_tiles);
   else
-    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER, 1, F8>), grid, dim3(kThreads), 0, s, g, col_tiles);
+    launch_stream_tiles<F8, 4>(g, s, grid, col_tiles);
   return hipGetLastError();
 }
 

@@ -93,6 +93,10 @@ struct GroupedGemmArgs {
   // split they used.
   int ksplit = 1;
   int64_t split_stride = 0;
+  // Upper bound on any expert's row count when the caller knows one (the
+  // block: n_tokens, since top-k picks distinct experts per token); 0 =
+  // unknown.  A tuning hint: kernels are correct for any count.
+  int max_rows_per_expert = 0;
 };
 
 // Upper bound on the number of bm-row tiles of a grouping of n_assign rows
