@@ -64,6 +64,10 @@ constexpr int kWaitVm6Lgkm0 = 0x0070 | 6;           // vmcnt(6) lgkmcnt(0)
 constexpr int kWaitVm12 = 0x0F70 | 12;              // vmcnt(12)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
 
+__host__ __device__ __forceinline__ int split_boundary(int kblocks, int ksplit, int s) {
+  return s >= ksplit ? kblocks : (s * kblocks / ksplit) & ~1;
+}
+
 __device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
   if (g.a_mode == A_GATHER_TOKEN) return g.order[p] % g.n_tokens;
   if (g.a_mode == A_GATHER_FLAT) return g.order[p];
@@ -397,8 +401,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   constexpr int kStageInputs = F8 ? 64 : 32;  // one packed weight block
   const int64_t kblocks = K / kStageInputs;
   // This block's share of K: stages [k_first, k_first + KT).
-  const int KT = static_cast<int>(kblocks / g.ksplit);
-  const int k_first = split * KT;
+  // Split s covers stages [b(s), b(s+1)), b(s) = s * kblocks / ksplit rounded
+  // down to even (the bf16 loop runs two stages per trip).
+  const int k_first = split_boundary(static_cast<int>(kblocks), g.ksplit, split);
+  const int KT = split_boundary(static_cast<int>(kblocks), g.ksplit, split + 1) - k_first;
 
   // ---- global -> LDS sources.  Token rows: this wave stages rows
   // (wave*2 + j)*16 + (lane >> 2), 16-byte physical chunk (lane & 3), which
@@ -521,6 +527,8 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
   if (g.epi != EPI_SCATTER_WEIGHTED || g.out_dtype != DT_F32 || g.split_stride == 0) return 1;
   const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
   const int64_t tiles = static_cast<int64_t>(row_tiles) * ((g.N + kBN - 1) / kBN);
+  // (Three splits were measured too: the extra fp32 partial traffic and
+  // per-tile fixed costs outweigh the shorter last round.)
   if (tiles < 1024 && g.K % (4 * kBK) == 0 && g.K >= 2048) return 2;
   return 1;
 }
@@ -529,7 +537,9 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
   if (g.act_dtype != DT_BF16 || (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) || g.w_format != WF_MFMA16)
     return false;
   // bf16: an even number of 32-input stages per split; fp8: whole 64-input blocks.
-  if (g.K <= 0 || g.K % (2 * kBK * g.ksplit) || g.N % 16 || g.lda % 8 || g.ldo % 4) return false;
+  // whole 64-input blocks, and at least two stages per split
+  if (g.K <= 0 || g.K % (2 * kBK) || g.K / (2 * kBK) < 2 * g.ksplit || g.N % 16 || g.lda % 8 || g.ldo % 4)
+    return false;
   if (g.w_dtype == DT_F8 && (!g.s0 || (g.epi == EPI_SWIGLU && !g.s1))) return false;
   // 32-bit byte offsets of A rows
   const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;
