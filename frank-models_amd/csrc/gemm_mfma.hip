@@ -288,46 +288,54 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled_kernel(GroupedGemmArgs
 // token rows and outputs out of the caches.
 __device__ __forceinline__ u32x4_t stream_load(const u32x4_t* p) { return __builtin_nontemporal_load(p); }
 
-constexpr int kStreamRowsPerWave = 16;
-constexpr int kStreamRows = 4 * kStreamRowsPerWave;  // weight rows per set per block
-constexpr int kStreamUnroll = 8;                     // 32-input steps per iteration
+constexpr int kStreamRows = 16;     // weight rows per set per block
+constexpr int kStreamUnroll = 8;    // 32-input steps per iteration
+constexpr int kStreamWaves = kThreads / kWave;
 
-// Decode-sized grouped GEMM: block = (expert, 64 weight rows per set), wave =
-// 16 weight rows.  The weights stream from HBM straight into MFMA registers
-// (kStreamUnroll 1 KiB blocks per set in flight per wave) and each fragment
-// is applied to up to kStreamTiles 16-row tiles of the expert's token rows,
-// so an expert's weights are read once for up to 16 * kStreamTiles rows.  An
-// expert has at most n_tokens rows (top-k picks distinct experts), so the
-// launcher sizes kStreamTiles from n_tokens and decode batches keep the
-// one-tile register footprint.
+// Decode-sized grouped GEMM: block = (expert, 16 weight rows per set); its
+// 4 waves split the input axis in four and their partial sums are added in
+// wave order through LDS, so even a handful of active experts keeps many
+// waves streaming.  Each wave streams its weight blocks from HBM straight
+// into MFMA registers (kStreamUnroll 1 KiB blocks per set in flight) and
+// applies each fragment to up to kStreamTiles 16-row tiles of the expert's
+// token rows, so an expert's weights are read once for up to
+// 16 * kStreamTiles rows.  An expert has at most n_tokens rows (top-k picks
+// distinct experts), so the launcher sizes kStreamTiles from n_tokens and
+// decode batches keep the one-tile register footprint.
 template <int EPI, int NSETS, bool F8, int kStreamTiles>
 __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
+  __shared__ f32x4_t partial[kStreamWaves - 1][kStreamTiles][NSETS][kWave];
   const int e = blockIdx.x / col_tiles;
   const int ct = blockIdx.x - e * col_tiles;
   const int row_begin = g.offsets[e];
   const int count = g.offsets[e + 1] - row_begin;
-  if (count == 0) return;
+  if (count == 0) return;  // block-uniform
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int64_t N = g.N, K = g.K;
-  const int64_t n_base = static_cast<int64_t>(ct) * kStreamRows + wave * kStreamRowsPerWave;
-  if (n_base >= N) return;
+  const int64_t n_base = static_cast<int64_t>(ct) * kStreamRows;
   const int64_t nblocks = N / 16;
   const int64_t nb = n_base / 16;
   const int64_t kblocks = F8 ? K / 64 : K / 32;
+  // This wave's share of the input axis, in 32-input steps (whole fp8
+  // blocks of two steps for fp8 weights).
+  const int ksteps = static_cast<int>(K / 32);
+  const int unit = F8 ? 2 : 1;
+  const int units = ksteps / unit;
+  const int ks_begin = (wave * units / kStreamWaves) * unit;
+  const int ks_end = ((wave + 1) * units / kStreamWaves) * unit;
   const unsigned char* wsrc[NSETS];
 #pragma unroll
   for (int s = 0; s < NSETS; ++s) {
     const unsigned char* base = static_cast<const unsigned char*>(s == 0 ? g.w0 : g.w1);
     wsrc[s] = base + ((static_cast<int64_t>(e) * nblocks + nb) * kblocks) * 1024 + lane * 16;
   }
-  const int ksteps = static_cast<int>(K / 32);
   const int kq = (lane >> 4) * 8;  // this lane's 8 inputs within a 32-input step
   const u32x4_t zero{0u, 0u, 0u, 0u};
 
   for (int m0 = 0; m0 < count; m0 += 16 * kStreamTiles) {
-    const int nt = min(kStreamTiles, (count - m0 + 15) / 16);  // wave-uniform
+    const int nt = min(kStreamTiles, (count - m0 + 15) / 16);  // block-uniform
     const bf16_t* arow[kStreamTiles];
     bool r_ok[kStreamTiles];
 #pragma unroll
@@ -342,22 +350,28 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g
 #pragma unroll
       for (int s = 0; s < NSETS; ++s) acc[mt][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    int ks = 0;
-    for (; ks + kStreamUnroll <= ksteps; ks += kStreamUnroll) {
+    // kStreamUnroll steps per trip, all loads first; a short last trip is
+    // predicated per step (wave-uniform), so it keeps its loads in flight too.
+    for (int ks = ks_begin; ks < ks_end; ks += kStreamUnroll) {
       u32x4_t wv[NSETS][kStreamUnroll];
 #pragma unroll
       for (int s = 0; s < NSETS; ++s) {
         if (F8) {
+          // all loads, then all conversions (a conversion waits for its load)
+          u32x4_t q[kStreamUnroll / 2];
 #pragma unroll
-          for (int u = 0; u < kStreamUnroll; u += 2) {
-            const u32x4_t q =
-                stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>((ks + u) / 2) * 1024));
-            f8x16_to_bf16(q, wv[s][u], wv[s][u + 1]);
-          }
+          for (int u = 0; u < kStreamUnroll; u += 2)
+            q[u / 2] = ks + u < ks_end ? stream_load(reinterpret_cast<const u32x4_t*>(
+                                             wsrc[s] + static_cast<int64_t>((ks + u) / 2) * 1024))
+                                       : zero;
+#pragma unroll
+          for (int u = 0; u < kStreamUnroll; u += 2) f8x16_to_bf16(q[u / 2], wv[s][u], wv[s][u + 1]);
         } else {
 #pragma unroll
           for (int u = 0; u < kStreamUnroll; ++u)
-            wv[s][u] = stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks + u) * 1024));
+            wv[s][u] = ks + u < ks_end
+                           ? stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks + u) * 1024))
+                           : zero;
         }
       }
 #pragma unroll
@@ -366,59 +380,55 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GroupedGemmArgs g
           u32x4_t tok[kStreamUnroll];
 #pragma unroll
           for (int u = 0; u < kStreamUnroll; ++u)
-            tok[u] = r_ok[mt] ? *reinterpret_cast<const u32x4_t*>(arow[mt] + (ks + u) * 32) : zero;
+            tok[u] = (r_ok[mt] && ks + u < ks_end) ? *reinterpret_cast<const u32x4_t*>(arow[mt] + (ks + u) * 32) : zero;
 #pragma unroll
           for (int u = 0; u < kStreamUnroll; ++u)
+            if (ks + u < ks_end)
 #pragma unroll
-            for (int s = 0; s < NSETS; ++s) acc[mt][s] = mfma16(wv[s][u], tok[u], acc[mt][s]);
-        }
-      }
-    }
-    for (; ks < ksteps; ks += F8 ? 2 : 1) {  // tail (K % 256 != 0)
-#pragma unroll
-      for (int s = 0; s < NSETS; ++s) {
-        u32x4_t w0, w1;
-        if (F8) {
-          f8x16_to_bf16(stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks / 2) * 1024)),
-                        w0, w1);
-        } else {
-          w0 = stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks) * 1024));
-          w1 = zero;
-        }
-#pragma unroll
-        for (int mt = 0; mt < kStreamTiles; ++mt) {
-          if (mt < nt) {
-            const u32x4_t t0 = r_ok[mt] ? *reinterpret_cast<const u32x4_t*>(arow[mt] + ks * 32) : zero;
-            acc[mt][s] = mfma16(w0, t0, acc[mt][s]);
-            if (F8) {
-              const u32x4_t t1 = r_ok[mt] ? *reinterpret_cast<const u32x4_t*>(arow[mt] + (ks + 1) * 32) : zero;
-              acc[mt][s] = mfma16(w1, t1, acc[mt][s]);
-            }
-          }
+              for (int s = 0; s < NSETS; ++s) acc[mt][s] = mfma16(wv[s][u], tok[u], acc[mt][s]);
         }
       }
     }
 
-    const int64_t n = n_base + 4 * (lane >> 4);
-    float4 sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
-    if (F8) {
-      sc0 = *reinterpret_cast<const float4*>(g.s0 + static_cast<int64_t>(e) * N + n);
-      if (NSETS == 2) sc1 = *reinterpret_cast<const float4*>(g.s1 + static_cast<int64_t>(e) * N + n);
-    }
+    // Partial sums of waves 1..3 -> LDS; wave 0 adds them in wave order.
+    if (wave > 0) {
 #pragma unroll
-    for (int mt = 0; mt < kStreamTiles; ++mt) {
-      if (mt < nt && r_ok[mt]) {
-        const int p = row_begin + m0 + mt * 16 + (lane & 15);
-        const f32x4_t a0 = acc[mt][0];
-        if (EPI == EPI_SWIGLU) {
-          const f32x4_t a1 = acc[mt][NSETS - 1];
-          store4<EPI>(g, p, n, silu_mul(a0[0] * sc0.x, a1[0] * sc1.x), silu_mul(a0[1] * sc0.y, a1[1] * sc1.y),
-                      silu_mul(a0[2] * sc0.z, a1[2] * sc1.z), silu_mul(a0[3] * sc0.w, a1[3] * sc1.w));
-        } else {
-          store4<EPI>(g, p, n, a0[0] * sc0.x, a0[1] * sc0.y, a0[2] * sc0.z, a0[3] * sc0.w);
+      for (int mt = 0; mt < kStreamTiles; ++mt)
+#pragma unroll
+        for (int s = 0; s < NSETS; ++s)
+          if (mt < nt) partial[wave - 1][mt][s][lane] = acc[mt][s];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 1; w < kStreamWaves; ++w)
+#pragma unroll
+        for (int mt = 0; mt < kStreamTiles; ++mt)
+#pragma unroll
+          for (int s = 0; s < NSETS; ++s)
+            if (mt < nt) acc[mt][s] += partial[w - 1][mt][s][lane];
+      const int64_t n = n_base + 4 * (lane >> 4);
+      float4 sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
+      if (F8) {
+        sc0 = *reinterpret_cast<const float4*>(g.s0 + static_cast<int64_t>(e) * N + n);
+        if (NSETS == 2) sc1 = *reinterpret_cast<const float4*>(g.s1 + static_cast<int64_t>(e) * N + n);
+      }
+#pragma unroll
+      for (int mt = 0; mt < kStreamTiles; ++mt) {
+        if (mt < nt && r_ok[mt]) {
+          const int p = row_begin + m0 + mt * 16 + (lane & 15);
+          const f32x4_t a0 = acc[mt][0];
+          if (EPI == EPI_SWIGLU) {
+            const f32x4_t a1 = acc[mt][NSETS - 1];
+            store4<EPI>(g, p, n, silu_mul(a0[0] * sc0.x, a1[0] * sc1.x), silu_mul(a0[1] * sc0.y, a1[1] * sc1.y),
+                        silu_mul(a0[2] * sc0.z, a1[2] * sc1.z), silu_mul(a0[3] * sc0.w, a1[3] * sc1.w));
+          } else {
+            store4<EPI>(g, p, n, a0[0] * sc0.x, a0[1] * sc0.y, a0[2] * sc0.z, a0[3] * sc0.w);
+          }
         }
       }
     }
+    __syncthreads();  // partial[] is rewritten by the next pass
   }
 }
 

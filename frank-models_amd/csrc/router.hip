@@ -157,19 +157,39 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
   const int t = tok0 + row;
   const bool t_ok = t < n_tokens;
   const bf16_t* xrow = x + static_cast<int64_t>(t_ok ? t : 0) * n_embd + kofs;
-  for (int h0 = wave * 32; h0 < n_embd; h0 += kMfmaWaves * 32) {
-    const u32x4_t av = t_ok ? *reinterpret_cast<const u32x4_t*>(xrow + h0) : u32x4_t{0u, 0u, 0u, 0u};
-    const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+  // Operands of one 32-wide chunk of the hidden axis: the token fragment and
+  // one router fragment per 16 experts.  Loaded a trip ahead (two sets of
+  // registers), so each wave keeps a trip's loads in flight while it
+  // multiplies the previous one.
+  const u32x4_t zero{0u, 0u, 0u, 0u};
+  auto load = [&](int h0, u32x4_t& av, u32x4_t (&bv)[kMfmaMaxExpert / 16]) __attribute__((always_inline)) {
+    const bool in = h0 < n_embd;
+    av = (t_ok && in) ? *reinterpret_cast<const u32x4_t*>(xrow + h0) : zero;
 #pragma unroll
     for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
-      if (c < n_chunks) {
-        const int e = c * 16 + row;
-        u32x4_t bv = u32x4_t{0u, 0u, 0u, 0u};
-        if (e < n_expert)
-          bv = *reinterpret_cast<const u32x4_t*>(wr + static_cast<int64_t>(e) * n_embd + h0 + kofs);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv), acc[c], 0, 0, 0);
-      }
+      const int e = c * 16 + row;
+      bv[c] = (c < n_chunks && e < n_expert && in)
+                  ? *reinterpret_cast<const u32x4_t*>(wr + static_cast<int64_t>(e) * n_embd + h0 + kofs)
+                  : zero;
     }
+  };
+  auto multiply = [&](const u32x4_t& av, const u32x4_t (&bv)[kMfmaMaxExpert / 16]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < kMfmaMaxExpert / 16; ++c)
+      if (c < n_chunks)
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                         __builtin_bit_cast(bf16x8_t, bv[c]), acc[c], 0, 0, 0);
+  };
+  constexpr int kStep = kMfmaWaves * 32;
+  u32x4_t a0, b0[kMfmaMaxExpert / 16], a1, b1[kMfmaMaxExpert / 16];
+  int h0 = wave * 32;
+  load(h0, a0, b0);
+  for (; h0 < n_embd; h0 += 2 * kStep) {
+    load(h0 + kStep, a1, b1);
+    multiply(a0, b0);
+    if (h0 + kStep >= n_embd) break;
+    load(h0 + 2 * kStep, a0, b0);
+    multiply(a1, b1);
   }
   // D[token][expert]: lane holds expert (lane & 15), tokens 4*(lane>>4)+i.
   float* mine = part + wave * kTok * ld;
