@@ -7,19 +7,18 @@
 //
 // Tile: 256 assignment rows x 256 weight rows (gate/up: 128 + 128) per
 // 512-thread block; 4x2 waves, each 64 x 128 = 4 x 8 v_mfma_f32_16x16x32_bf16
-// tiles, 128 fp32 accumulators per lane (AGPRs).  Two waves per SIMD, so one
-// wave's LDS reads overlap the other's MFMAs.  Per 32-input stage a wave reads
-// 12 fragments (12 KiB) from LDS for 32 MFMAs.  A wave's four 16-row groups
-// are interleaved (wm, wm+4, wm+8, wm+12), and a wave skips the reads and
-// MFMAs of groups past the expert's last row, so the last (partial) row tile
-// of an expert costs in proportion to its rows.
+// tiles, 128 fp32 accumulators per lane.  Per 32-input stage a wave reads 12
+// fragments (12 KiB) from LDS for 32 MFMAs.  A wave's four 16-row groups are
+// interleaved (wm, wm+4, wm+8, wm+12), and a wave skips the reads and MFMAs
+// of groups past the expert's last row, so the last (partial) row tile of an
+// expert costs in proportion to its rows.
 //
-// Pipeline: a 4-deep LDS ring of 32-input stages (32 KiB each: 256 token rows
-// x 64 B + 16 weight blocks x 1 KiB).  Global data goes straight to LDS
-// (global_load_lds_dwordx4, no staging registers), three stages ahead of the
-// stage being multiplied, so HBM latency hides behind ~3000 cycles of MFMA.
-// Fragments of stage k+1 are read from LDS while stage k's MFMAs run.  One
-// barrier per stage.
+// Pipeline (bf16 weights): a 5-deep LDS ring of 32-input stages (32 KiB
+// each: 256 token rows x 64 B + 16 weight blocks x 1 KiB), filled straight
+// from global memory (global_load_lds_dwordx4, no staging registers).  The
+// two waves of each SIMD take turns: one multiplies two stages while the
+// other reads its next fragments and issues the loads of a stage two to
+// three stages ahead (k_loop).
 //
 // LDS layouts: weight blocks are copied as packed (lane-ordered 1 KiB blocks,
 // conflict-free 16-byte reads); token rows are 64 B with the 16-byte chunk
@@ -35,11 +34,11 @@ constexpr int kThreads = 512;
 constexpr int kBM = 256;
 constexpr int kBN = 256;   // weight rows per tile over all sets
 constexpr int kBK = 32;    // inputs per stage
-constexpr int kStages = 4;
+constexpr int kRing = 5;   // bf16: stages in the LDS ring
 constexpr int kAStage = kBM * kBK * 2;       // 16 KiB
 constexpr int kBStage = (kBN / 16) * 1024;   // 16 KiB
 constexpr int kStage = kAStage + kBStage;    // 32 KiB
-constexpr int kLds = kStages * kStage;       // 128 KiB
+constexpr int kLds = kRing * kStage;         // 160 KiB
 // fp8 weights: 64-input stages (A as two 32-input halves in the bf16 layout,
 // then 16 fp8 weight blocks of 16 rows x 64 inputs), 3-deep ring.
 constexpr int kStagesF8 = 3;
@@ -58,11 +57,13 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g * (u / (1
 // lgkmcnt 11:8; a field at its maximum does not wait).  Issued through the
 // builtin so the compiler's own wait insertion accounts for them.
 constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
-constexpr int kWaitVm8 = 0x0F70 | 8;                // vmcnt(8)
-constexpr int kWaitVm8Lgkm0 = 0x0070 | 8;           // vmcnt(8) lgkmcnt(0)
 constexpr int kWaitVm6Lgkm0 = 0x0070 | 6;           // vmcnt(6) lgkmcnt(0)
 constexpr int kWaitVm12 = 0x0F70 | 12;              // vmcnt(12)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
+// vmcnt(vm) (0..63), with or without lgkmcnt(0).
+__host__ __device__ constexpr int wait_vm(int vm, bool lgkm0) {
+  return (vm & 15) | ((vm >> 4) << 14) | 0x70 | (lgkm0 ? 0 : 0xF00);
+}
 
 __host__ __device__ __forceinline__ int split_boundary(int kblocks, int ksplit, int s) {
   return s >= ksplit ? kblocks : (s * kblocks / ksplit) & ~1;
@@ -122,64 +123,17 @@ __device__ __forceinline__ void store4(const GroupedGemmArgs& g, int split, int 
   }
 }
 
-// Instruction order within one stage of a wave with NM active 16-row groups:
-// the NM + 8 fragment reads of the next stage and the 4 global->LDS loads of
-// a later stage are spread between this stage's 8 * NM MFMAs, so the LDS and
-// memory pipes work while the matrix cores do.  A full wave (NM = 4) does
-// 12 x (1 read, 2 MFMAs) then 4 x (1 load, 2 MFMAs).  Masks: 0x100 DS read,
-// 0x010 VMEM, 0x008 MFMA.
-template <int NM>
-__device__ __forceinline__ void stage_schedule() {
-  if constexpr (NM == 4) {
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    }
-  } else if constexpr (NM > 0) {
-    // Loads first (they have the longest latency), then reads and MFMAs
-    // alternating; the MFMAs left over once the reads run out come last.
-    constexpr int kReads = NM + 8;
-    constexpr int kMfma = 8 * NM;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-#pragma unroll
-    for (int i = 0; i < kReads; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (i < kMfma) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    }
-    if constexpr (kMfma > kReads) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kReads, 0);
-  }
-}
-
 // Everything one wave needs to stage and read tiles: computed once per block.
 struct WaveCtx {
   unsigned char* lds;
   const unsigned char* a_base;
-  uint32_t a_off[2];           // byte offsets of this wave's two staged token rows
-  const unsigned char* b_base[2];  // this wave's two staged weight row blocks
+  uint32_t a_off[4];           // byte offsets of the staged token rows: this wave's share (0, 1), wave ^ 4's (2, 3)
+  const unsigned char* b_base[4];  // staged weight row blocks, same order
   uint32_t b_lane;
   int a_lane;                  // LDS byte offset of this lane's A fragment in a 16-row group
   int wave, wm, wn;
   int KT;                      // stages of 32 inputs in this block's K range
 };
-
-template <int NSETS>
-__device__ __forceinline__ void issue_stage(const WaveCtx& c, int kt, int buf) {
-  unsigned char* st = c.lds + buf * kStage;
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + kt * 64), st + (c.wave * 2 + j) * 1024, 16, 0, 0);
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-    __builtin_amdgcn_global_load_lds(c.b_base[j] + (static_cast<uint32_t>(kt) * 1024 + c.b_lane),
-                                     st + kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
-}
 
 // Fragment m of a wave covers 16-row group wm + 4 m of the tile, so the
 // groups of a partial tile are spread over all four SIMDs.
@@ -196,60 +150,123 @@ __device__ __forceinline__ void read_frags(const WaveCtx& c, int buf, u32x4_t* f
   }
 }
 
-// The pipelined K loop of one wave with NM active 16-row groups (0..4).
-// Every wave stages its share of every stage and joins every barrier; only
-// the fragment reads and MFMAs depend on NM.
-template <int NM, int NSETS>
+// One group's loads of a whole stage: this wave's share and wave ^ 4's.
+template <int NSETS>
+__device__ __forceinline__ void issue_full_stage(const WaveCtx& c, int kt, int buf) {
+  unsigned char* st = c.lds + buf * kStage;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int share = j < 2 ? c.wave : (c.wave ^ 4);
+    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + kt * 64), st + (share * 2 + (j & 1)) * 1024, 16, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int share = j < 2 ? c.wave : (c.wave ^ 4);
+    __builtin_amdgcn_global_load_lds(c.b_base[j] + (static_cast<uint32_t>(kt) * 1024 + c.b_lane),
+                                     st + kAStage + (share * 2 + (j & 1)) * 1024, 16, 0, 0);
+  }
+}
+
+// The K loop, ping-pong between two wave groups: G0 = waves 0-3 and G1 =
+// waves 4-7, one wave of each per SIMD.  Barriers cut time into slots.  In
+// every slot one group multiplies two 32-input stages (64 MFMAs per wave,
+// operands already in registers) while the other reads its next fragments
+// from LDS and loads a later stage, and the groups swap at each barrier, so
+// each SIMD's matrix core is fed by one wave while the other wave's LDS
+// traffic and barrier wait overlap it.  The ring holds kRing = 5 stages;
+// super-step j = stages 2j, 2j+1.
+//   Slot 2j:   G0 multiplies j; G1 reads j's fragments and loads stage 2j+4.
+//   Slot 2j+1: G1 multiplies j; G0 reads j+1's fragments and loads stage 2j+5.
+// Each stage is loaded whole by one group (8 loads per thread).  G1 ends its
+// memory slot 2j with stage 2j+2 complete (only stage 2j+4 in flight), G0
+// ends its compute slot 2j with stage 2j+3 complete, so stages 2j+2 and
+// 2j+3 are visible from the barrier that ends slot 2j, before G0 reads them
+// in slot 2j+1.  At slot 2j the live stages are 2j..2j+4, five distinct
+// buffers; the buffer G1 refills held stage 2j-1 (last read in slot 2j-2),
+// the one G0 refills in slot 2j+1 held stage 2j (last read in slot 2j).
+// Stages past the end are not loaded; the waits then drain everything.
+template <int NM, int NSETS, int G>
 __device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
-  const int KT = c.KT;
-  // Prologue: stages 0..3 in flight (4 loads per wave each); wait for 0 and 1.
-#pragma unroll
-  for (int s = 0; s < kStages; ++s) issue_stage<NSETS>(c, s < KT ? s : KT - 1, s);
-  __builtin_amdgcn_s_waitcnt(kWaitVm8);
+  constexpr int R = kRing;
+  const int KT = c.KT;  // even
+  const int JT = KT >> 1;
+  u32x4_t fa[2][4], fb[2][8];
+  const bool two = KT > 2;
+  issue_full_stage<NSETS>(c, 1 - G, 1 - G);
+  if (two) {
+    issue_full_stage<NSETS>(c, 3 - G, 3 - G);
+    __builtin_amdgcn_s_waitcnt(wait_vm(8, false));
+  } else {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  }
   asm volatile("s_barrier" ::: "memory");
-  u32x4_t fa0[4], fb0[8], fa1[4], fb1[8];
-  if constexpr (NM > 0) read_frags<NM, NSETS>(c, 0, fa0, fb0);
-  // Stage 0 refills buffer 0: every wave's reads of it must be done first.
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  if constexpr (G == 0) {
+    if constexpr (NM > 0) {
+      read_frags<NM, NSETS>(c, 0, fa[0], fb[0]);
+      read_frags<NM, NSETS>(c, 1, fa[1], fb[1]);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  }
   asm volatile("s_barrier" ::: "memory");
 
-  // One iteration = two stages (KT is even), so the two fragment sets swap
-  // roles without register copies.  Per stage kt:
-  //   read stage kt+1's fragments (it became visible at the last barrier),
-  //   refill the buffer stage kt came from with stage kt+4 (clamped: the
-  //   tail re-reads the last stage into idle buffers, keeping the wait
-  //   count constant), multiply stage kt, then wait until this wave's
-  //   fragment reads are done and only the 8 loads of stages kt+3 and kt+4
-  //   are outstanding (stage kt+2 has landed), barrier.  Waiting for the
-  //   reads before the barrier means no wave refills a buffer (next stage)
-  //   while another wave may still be reading it.
-  // sched_barrier(0) keeps each stage's instructions between its barriers;
-  // stage_schedule() orders them inside.  This stage's MFMA operands are
-  // already in registers, so the next stage's LDS reads overlap the MFMAs.
-  for (int kt = 0; kt < KT; kt += 2) {
-    if constexpr (NM > 0) read_frags<NM, NSETS>(c, (kt + 1) & 3, fa1, fb1);
-    issue_stage<NSETS>(c, kt + 4 < KT ? kt + 4 : KT - 1, kt & 3);
+  int b0 = 0;  // buffer of stage 2j
+  for (int j = 0; j < JT; ++j) {
+    const int b1 = b0 + 1 >= R ? b0 + 1 - R : b0 + 1;
+    const int b2 = b0 + 2 >= R ? b0 + 2 - R : b0 + 2;
+    const int b3 = b0 + 3 >= R ? b0 + 3 - R : b0 + 3;
+    const int b4 = b0 + 4 >= R ? b0 + 4 - R : b0 + 4;
+    if constexpr (G == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb0[n], fa0[m], acc[n][m]);
-    stage_schedule<NM>();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-
-    if constexpr (NM > 0) read_frags<NM, NSETS>(c, (kt + 2) & 3, fa0, fb0);
-    issue_stage<NSETS>(c, kt + 5 < KT ? kt + 5 : KT - 1, (kt + 1) & 3);
+        for (int n = 0; n < 8; ++n)
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+          for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb[h][n], fa[h][m], acc[n][m]);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NM > 0) {
+        if (j + 1 < JT) {
+          read_frags<NM, NSETS>(c, b2, fa[0], fb[0]);
+          read_frags<NM, NSETS>(c, b3, fa[1], fb[1]);
+        }
+      }
+      if (2 * j + 5 < KT) issue_full_stage<NSETS>(c, 2 * j + 5, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      asm volatile("s_barrier" ::: "memory");
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NM > 0) {
+        read_frags<NM, NSETS>(c, b0, fa[0], fb[0]);
+        read_frags<NM, NSETS>(c, b1, fa[1], fb[1]);
+      }
+      if (2 * j + 4 < KT) {
+        issue_full_stage<NSETS>(c, 2 * j + 4, b4);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_vm(8, true));
+      } else {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_vm(0, true));
+      }
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb1[n], fa1[m], acc[n][m]);
-    stage_schedule<NM>();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm8Lgkm0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int n = 0; n < 8; ++n)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb[h][n], fa[h][m], acc[n][m]);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
+    }
+    b0 = b2;
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
@@ -406,27 +423,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   const int k_first = split_boundary(static_cast<int>(kblocks), g.ksplit, split);
   const int KT = split_boundary(static_cast<int>(kblocks), g.ksplit, split + 1) - k_first;
 
-  // ---- global -> LDS sources.  Token rows: this wave stages rows
-  // (wave*2 + j)*16 + (lane >> 2), 16-byte physical chunk (lane & 3), which
-  // holds logical chunk (lane & 3) ^ ((lane >> 3) & 3).  Rows past the tile
-  // re-read its first row.  Byte offsets from the A base fit 32 bits
-  // (checked on the host).
+  // ---- global -> LDS sources.  A stage is staged in 8 shares; share w
+  // holds token rows (w*2 + j)*16 + (lane >> 2), 16-byte physical chunk
+  // (lane & 3), which holds logical chunk (lane & 3) ^ ((lane >> 3) & 3), and
+  // weight row blocks w*2 + j.  Each wave keeps the addresses of its own
+  // share (j = 0, 1) and of share wave ^ 4 (j = 2, 3): the bf16 loop has one
+  // group load a whole stage, the fp8 loop has every wave load its own share.
+  // Rows past the tile re-read its first row.  Byte offsets from the A base
+  // fit 32 bits (checked on the host).
   WaveCtx c;
   c.lds = lds;
   c.a_base = static_cast<const unsigned char*>(g.a);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = (wave * 2 + j) * 16 + (lane >> 2);
+  for (int j = 0; j < 4; ++j) {
+    const int share = j < 2 ? wave : (wave ^ 4);
+    const int r = (share * 2 + (j & 1)) * 16 + (lane >> 2);
     const int p = ti.row0 + (r < ti.rows ? r : 0);
     const int ch = (lane & 3) ^ ((lane >> 3) & 3);
     c.a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + k_first * kStageInputs * 2);
   }
-  // Weight blocks: this wave stages row blocks wave*2 + j of the stage (wave
-  // uniform addresses).  The packed buffer has a 256-row tail, so row blocks
-  // past N stay in bounds (their columns are never stored).
+  // Weight blocks (wave-uniform addresses).  The packed buffer has a
+  // 256-row tail, so row blocks past N stay in bounds (their columns are
+  // never stored).
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int rb = wave * 2 + j;
+  for (int j = 0; j < 4; ++j) {
+    const int rb = (j < 2 ? wave : (wave ^ 4)) * 2 + (j & 1);
     const int set = NSETS == 2 ? rb >> 3 : 0;
     const int64_t nb = n0 / 16 + (NSETS == 2 ? (rb & 7) : rb);
     const unsigned char* w = static_cast<const unsigned char*>(set == 0 ? g.w0 : g.w1);
@@ -460,12 +481,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
       default: k_loop_f8<0, NSETS>(c, acc); break;
     }
   } else {
-    switch (nm) {
-      case 4: k_loop<4, NSETS>(c, acc); break;
-      case 3: k_loop<3, NSETS>(c, acc); break;
-      case 2: k_loop<2, NSETS>(c, acc); break;
-      case 1: k_loop<1, NSETS>(c, acc); break;
-      default: k_loop<0, NSETS>(c, acc); break;
+    if (wave < 4) {  // the two ping-pong groups run mirrored loops
+      switch (nm) {
+        case 4: k_loop<4, NSETS, 0>(c, acc); break;
+        case 3: k_loop<3, NSETS, 0>(c, acc); break;
+        case 2: k_loop<2, NSETS, 0>(c, acc); break;
+        case 1: k_loop<1, NSETS, 0>(c, acc); break;
+        default: k_loop<0, NSETS, 0>(c, acc); break;
+      }
+    } else {
+      switch (nm) {
+        case 4: k_loop<4, NSETS, 1>(c, acc); break;
+        case 3: k_loop<3, NSETS, 1>(c, acc); break;
+        case 2: k_loop<2, NSETS, 1>(c, acc); break;
+        case 1: k_loop<1, NSETS, 1>(c, acc); break;
+        default: k_loop<0, NSETS, 1>(c, acc); break;
+      }
     }
   }
 
