@@ -30,6 +30,14 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(bf16_t, b);
 }
 
+// gate * silu(up) = g * u / (1 + exp(-u)) (components/activation/swiglu.mlir:37-47)
+// for the MFMA kernels, whose SwiGLU output is stored as bf16: the hardware
+// reciprocal (1 ulp) stands in for an IEEE division, far below bf16's
+// rounding.  The fp32 reference kernel divides exactly.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * (u * __builtin_amdgcn_rcpf(1.f + __expf(-u)));
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
   bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};

@@ -41,11 +41,6 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x
                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  // gate * silu(up) = g * u / (1 + exp(-u))
-  return g * (u / (1.f + __expf(-u)));
-}
-
 // Source row of assignment p (see AMode).
 __device__ __forceinline__ int64_t a_source_row(const GroupedGemmArgs& g, int p) {
   if (g.a_mode == A_GATHER_TOKEN) return g.order[p] % g.n_tokens;

@@ -51,8 +51,6 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x
                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g * (u / (1.f + __expf(-u))); }
-
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
 // lgkmcnt 11:8; a field at its maximum does not wait).  Issued through the
 // builtin so the compiler's own wait insertion accounts for them.
