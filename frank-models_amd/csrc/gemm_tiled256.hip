@@ -98,26 +98,80 @@ __device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, i
   return true;
 }
 
-template <int EPI>
-__device__ __forceinline__ void store4(const GroupedGemmArgs& g, int split, int p, int64_t n, float v0, float v1,
-                                       float v2, float v3) {
-  if (EPI == EPI_SWIGLU || g.out_dtype == DT_BF16) {
-    int64_t row = p;
-    if (EPI != EPI_SWIGLU) row = g.order[p];
-    if (EPI == EPI_SCATTER_WEIGHTED) {
-      const float w = g.route_w[row];
-      v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+// The epilogue, staged through LDS so that every global store writes whole
+// contiguous output rows (16 bytes per lane, 256 B - 1 KiB per row) instead
+// of 16 rows x 32-64 B.  The lane holds assignment row (lane & 15) of each
+// 16-row group and outputs 4*(lane >> 4) .. +4 of each 16-output fragment.
+// Two passes of 128 tile rows (groups m = 2P, 2P+1 of every wave): write the
+// finished values to LDS (row pitch = row bytes + 16), barrier, then the
+// block stores them row by row.  SwiGLU rows go to h in expert-sorted order
+// (row p); the scatter epilogues write row order[p], times the routing
+// weight for EPI_SCATTER_WEIGHTED, and fp32 K-split partials at
+// split * split_stride.  fp8 weights: the per-output-channel scale
+// multiplies the fp32 dot product.
+template <int EPI, int NSETS, bool F8, bool OUT_F32>
+__device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInfo& ti, int split, int64_t n0,
+                                         int wm, int wn, int lane, unsigned char* lds, const f32x4_t (&acc)[8][4]) {
+  constexpr int kFrags = NSETS == 2 ? 4 : 8;       // output fragments per wave
+  constexpr int kEsz = OUT_F32 ? 4 : 2;
+  constexpr int kRowBytes = (NSETS == 2 ? kBN / 2 : kBN) * kEsz;
+  constexpr int kPitch = kRowBytes + 16;
+  constexpr int kChunks = kRowBytes / 16;          // 16-byte chunks per row
+  const int64_t N = g.N;
+  const int colw = (NSETS == 2 ? wn * 64 : wn * 128) + 4 * (lane >> 4);
+  f32x4_t sc0[kFrags], sc1[kFrags];
+#pragma unroll
+  for (int n = 0; n < kFrags; ++n) {
+    sc0[n] = sc1[n] = f32x4_t{1.f, 1.f, 1.f, 1.f};
+    if constexpr (F8) {
+      const int64_t col = n0 + colw + n * 16;
+      if (col < N) {
+        sc0[n] = *reinterpret_cast<const f32x4_t*>(g.s0 + ti.expert * N + col);
+        if (NSETS == 2) sc1[n] = *reinterpret_cast<const f32x4_t*>(g.s1 + ti.expert * N + col);
+      }
     }
-    const u32x2_t pk{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-    *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(g.out) + row * g.ldo + n) = pk;
-  } else {
-    const int64_t row = g.order[p];
-    if (EPI == EPI_SCATTER_WEIGHTED) {
-      const float w = g.route_w[row];
-      v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+  }
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    __syncthreads();  // the ring (or the last pass's rows) is no longer read
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * pass + mm;
+      const int rl = (wm + 4 * mm) * 16 + (lane & 15);  // row within the pass
+      float w = 1.f;
+      if (EPI == EPI_SCATTER_WEIGHTED && pass * 128 + rl < ti.rows) w = g.route_w[g.order[ti.row0 + pass * 128 + rl]];
+      unsigned char* dst = lds + rl * kPitch + colw * kEsz;
+#pragma unroll
+      for (int n = 0; n < kFrags; ++n) {
+        const f32x4_t a0 = acc[n][m] * sc0[n];
+        f32x4_t v;
+        if constexpr (EPI == EPI_SWIGLU) {
+          const f32x4_t a1 = acc[n + 4][m] * sc1[n];
+          v = f32x4_t{silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]), silu_mul(a0[3], a1[3])};
+        } else {
+          v = a0 * w;
+        }
+        if constexpr (OUT_F32)
+          *reinterpret_cast<f32x4_t*>(dst + n * 16 * 4) = v;
+        else
+          *reinterpret_cast<u32x2_t*>(dst + n * 16 * 2) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      }
     }
-    *reinterpret_cast<f32x4_t*>(static_cast<float*>(g.out) + split * g.split_stride + row * g.ldo + n) =
-        f32x4_t{v0, v1, v2, v3};
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 128 * kChunks / kThreads; ++i) {
+      const int id = i * kThreads + static_cast<int>(threadIdx.x);
+      const int rl = id / kChunks, ch = id % kChunks;
+      const int r = pass * 128 + rl;
+      const int64_t col = n0 + ch * (16 / kEsz);
+      if (r >= ti.rows || col >= N) continue;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + rl * kPitch + ch * 16);
+      const int p = ti.row0 + r;
+      const int64_t row = EPI == EPI_SWIGLU ? static_cast<int64_t>(p) : static_cast<int64_t>(g.order[p]);
+      unsigned char* out = static_cast<unsigned char*>(g.out) +
+                           ((OUT_F32 ? split * g.split_stride : 0) + row * g.ldo + col) * kEsz;
+      *reinterpret_cast<u32x4_t*>(out) = v;
+    }
   }
 }
 
@@ -498,34 +552,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     }
   }
 
-  // ---- epilogue: lane holds assignment row (lane & 15) of each 16-row
-  // group and 4 consecutive weight rows 4*(lane >> 4) .. +4.  fp8 weights:
-  // the per-output-channel scale multiplies the fp32 dot product.
-  const int64_t e = ti.expert;
-#pragma unroll
-  for (int n = 0; n < (NSETS == 2 ? 4 : 8); ++n) {
-    const int64_t col = n0 + (NSETS == 2 ? wn * 64 : wn * 128) + n * 16 + 4 * (lane >> 4);
-    if (col >= N) continue;
-    f32x4_t sc0{1.f, 1.f, 1.f, 1.f}, sc1{1.f, 1.f, 1.f, 1.f};
-    if constexpr (F8) {
-      sc0 = *reinterpret_cast<const f32x4_t*>(g.s0 + e * N + col);
-      if (NSETS == 2) sc1 = *reinterpret_cast<const f32x4_t*>(g.s1 + e * N + col);
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int r = (wm + 4 * m) * 16 + (lane & 15);
-      if (r >= ti.rows) continue;
-      const int p = ti.row0 + r;
-      const f32x4_t a0 = acc[n][m] * sc0;
-      if (EPI == EPI_SWIGLU) {
-        const f32x4_t a1 = acc[n + 4][m] * sc1;
-        store4<EPI>(g, split, p, col, silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]),
-                    silu_mul(a0[3], a1[3]));
-      } else {
-        store4<EPI>(g, split, p, col, a0[0], a0[1], a0[2], a0[3]);
-      }
-    }
-  }
+  if constexpr (EPI == EPI_SWIGLU)
+    epilogue<EPI, NSETS, F8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
+  else if (g.out_dtype == DT_F32)
+    epilogue<EPI, NSETS, F8, true>(g, ti, split, n0, wm, wn, lane, lds, acc);
+  else
+    epilogue<EPI, NSETS, F8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
 }
 
 template <int EPI, int NSETS, bool F8>
@@ -565,10 +597,13 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
   if (g.act_dtype != DT_BF16 || (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) || g.w_format != WF_MFMA16)
     return false;
-  // bf16: an even number of 32-input stages per split; fp8: whole 64-input blocks.
-  // whole 64-input blocks, and at least two stages per split
+  // bf16: an even number of 32-input stages per split; fp8: whole 64-input
+  // blocks; at least two stages per split.
   if (g.K <= 0 || g.K % (2 * kBK) || g.K / (2 * kBK) < 2 * g.ksplit || g.N % 16 || g.lda % 8 || g.ldo % 4)
     return false;
+  // the epilogue stores 16-byte chunks: 8 bf16 or 4 fp32 outputs
+  const bool out_f32 = g.epi != EPI_SWIGLU && g.out_dtype == DT_F32;
+  if ((!out_f32 && g.ldo % 8) || (out_f32 && g.split_stride % 4)) return false;
   if (g.w_dtype == DT_F8 && (!g.s0 || (g.epi == EPI_SWIGLU && !g.s1))) return false;
   // 32-bit byte offsets of A rows
   const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;
