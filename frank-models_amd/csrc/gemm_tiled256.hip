@@ -107,7 +107,11 @@ __device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, i
 // block stores them row by row.  SwiGLU rows go to h in expert-sorted order
 // (row p); the scatter epilogues write row order[p], times the routing
 // weight for EPI_SCATTER_WEIGHTED, and fp32 K-split partials at
-// split * split_stride.  fp8 weights: the per-output-channel scale
+// split * split_stride.  The scatter epilogues first load the tile's
+// order[p] and routing weights once into an LDS table behind the staging
+// rows, so each pass waits on no global load.  fp32 outputs take the weight
+// as they are read back, bf16 outputs before rounding (the same fp32
+// product either way).  fp8 weights: the per-output-channel scale
 // multiplies the fp32 dot product.
 template <int EPI, int NSETS, bool F8, bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInfo& ti, int split, int64_t n0,
@@ -119,6 +123,24 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
   constexpr int kChunks = kRowBytes / 16;          // 16-byte chunks per row
   const int64_t N = g.N;
   const int colw = (NSETS == 2 ? wn * 64 : wn * 128) + 4 * (lane >> 4);
+  constexpr bool kScatter = EPI != EPI_SWIGLU;
+  constexpr bool kWeighted = EPI == EPI_SCATTER_WEIGHTED;
+  int* t_order = reinterpret_cast<int*>(lds + 128 * kPitch);           // [256]
+  float* t_w = reinterpret_cast<float*>(lds + 128 * kPitch + 1024);    // [256]
+  if constexpr (kScatter) {
+    const int t = static_cast<int>(threadIdx.x);
+    int o = 0;
+    float w = 1.f;
+    if (t < ti.rows) {
+      o = g.order[ti.row0 + t];
+      if (kWeighted) w = g.route_w[o];
+    }
+    __syncthreads();  // the ring is no longer read
+    if (t < kBM) {
+      t_order[t] = o;
+      if (kWeighted) t_w[t] = w;
+    }
+  }
   f32x4_t sc0[kFrags], sc1[kFrags];
 #pragma unroll
   for (int n = 0; n < kFrags; ++n) {
@@ -138,8 +160,7 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * pass + mm;
       const int rl = (wm + 4 * mm) * 16 + (lane & 15);  // row within the pass
-      float w = 1.f;
-      if (EPI == EPI_SCATTER_WEIGHTED && pass * 128 + rl < ti.rows) w = g.route_w[g.order[ti.row0 + pass * 128 + rl]];
+      const float w = kWeighted && !OUT_F32 ? t_w[pass * 128 + rl] : 1.f;
       unsigned char* dst = lds + rl * kPitch + colw * kEsz;
 #pragma unroll
       for (int n = 0; n < kFrags; ++n) {
@@ -165,9 +186,10 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
       const int r = pass * 128 + rl;
       const int64_t col = n0 + ch * (16 / kEsz);
       if (r >= ti.rows || col >= N) continue;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + rl * kPitch + ch * 16);
-      const int p = ti.row0 + r;
-      const int64_t row = EPI == EPI_SWIGLU ? static_cast<int64_t>(p) : static_cast<int64_t>(g.order[p]);
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + rl * kPitch + ch * 16);
+      if constexpr (kWeighted && OUT_F32)
+        v = __builtin_bit_cast(u32x4_t, __builtin_bit_cast(f32x4_t, v) * t_w[r]);
+      const int64_t row = kScatter ? static_cast<int64_t>(t_order[r]) : static_cast<int64_t>(ti.row0 + r);
       unsigned char* out = static_cast<unsigned char*>(g.out) +
                            ((OUT_F32 ? split * g.split_stride : 0) + row * g.ldo + col) * kEsz;
       *reinterpret_cast<u32x4_t*>(out) = v;
