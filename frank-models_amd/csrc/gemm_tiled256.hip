@@ -55,8 +55,6 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x
 // lgkmcnt 11:8; a field at its maximum does not wait).  Issued through the
 // builtin so the compiler's own wait insertion accounts for them.
 constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
-constexpr int kWaitVm6Lgkm0 = 0x0070 | 6;           // vmcnt(6) lgkmcnt(0)
-constexpr int kWaitVm12 = 0x0F70 | 12;              // vmcnt(12)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
 // vmcnt(vm) (0..63), with or without lgkmcnt(0).
 __host__ __device__ constexpr int wait_vm(int vm, bool lgkm0) {
@@ -380,94 +378,119 @@ __device__ __forceinline__ u32x4_t convert_frag(const u32x4_t q) {
   return f8x8_to_bf16x8(q[2 * H], q[2 * H + 1]);
 }
 
-// One 32-input half of an fp8 stage for a wave with NM active row groups,
-// as 8 chunks (weight fragment n = 0..7).  Chunk n converts fragment n+1's
-// half H from fp8 (fragment 0 before the first chunk), runs fragment n's NM
-// MFMAs, and between them issues this half's share of reads and loads:
-//   H = 0: A half 1 of the current stage (chunks 0..NM-1);
-//   H = 1: A half 0 and weight fragment n of the next stage (fragment n's
-//          old codes were converted a chunk earlier, so the read can reuse
-//          its registers), and the 6 loads that refill a buffer (chunks 0-5).
-// A scheduling fence closes each chunk, so the interleave does not depend on
-// the scheduler's global choices.
-template <int NM, int NSETS, int H>
-__device__ __forceinline__ void half_f8(const WaveCtx& c, f32x4_t (&acc)[8][4], const u32x4_t (&fa)[4],
-                                        u32x4_t (&fa_rd)[4], u32x4_t (&fq)[8], const unsigned char* a_rd,
-                                        const unsigned char* b_rd, int issue_kt, int issue_buf) {
-  u32x4_t cur{};
-  if constexpr (NM > 0) cur = convert_frag<H>(fq[0]);
+// This wave's 6 loads of fp8 stage kt (its share) into buffer buf.
+__device__ __forceinline__ void issue_share_f8(const WaveCtx& c, int kt, int buf) {
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    u32x4_t nxt = cur;
-    if constexpr (NM > 0) {
-      if (n < 7) nxt = convert_frag<H>(fq[n + 1]);
-      acc[n][0] = mfma16(cur, fa[0], acc[n][0]);
-      if (n < NM) fa_rd[n] = read_a_frag(c, a_rd, n);
-      if (H == 1) fq[n] = read_b_frag<NSETS>(c, b_rd, n);
+  for (int d = 0; d < 6; ++d) issue_one_f8(c, kt, buf, d);
+}
+
+// A fragments of both 32-input halves and the 8 raw fp8 weight fragments of
+// the stage in buffer buf.
+template <int NM, int NSETS>
+__device__ __forceinline__ void read_stage_f8(const WaveCtx& c, int buf, u32x4_t (&fa)[2][4], u32x4_t (&fq)[8]) {
+  const unsigned char* st = c.lds + buf * kStageF8;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int m = 0; m < NM; ++m) fa[h][m] = read_a_frag(c, st + h * kAStage, m);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) fq[n] = read_b_frag<NSETS>(c, st + 2 * kAStage, n);
+}
+
+// The 64 MFMAs of one fp8 stage, half by half; weight fragment n+1's codes
+// are converted to bf16 while fragment n's MFMAs run.
+template <int NM>
+__device__ __forceinline__ void multiply_f8(f32x4_t (&acc)[8][4], const u32x4_t (&fa)[2][4], const u32x4_t (&fq)[8]) {
+  if constexpr (NM > 0) {
+    u32x4_t cur = convert_frag<0>(fq[0]);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const u32x4_t nxt = n < 7 ? convert_frag<0>(fq[n + 1]) : convert_frag<1>(fq[0]);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(cur, fa[0][m], acc[n][m]);
+      cur = nxt;
     }
-    if (NM > 1) acc[n][1] = mfma16(cur, fa[1], acc[n][1]);
-    if (H == 1 && n < 6) issue_one_f8(c, issue_kt, issue_buf, n);
-    if (NM > 2) acc[n][2] = mfma16(cur, fa[2], acc[n][2]);
-    if (NM > 3) acc[n][3] = mfma16(cur, fa[3], acc[n][3]);
-    if constexpr (NM == 4) {
-      if (n < 7) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (n < 4 && H == 1)
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      else if (n < 4 || H == 1)
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (H == 1 && n < 6) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const u32x4_t nxt = n < 7 ? convert_frag<1>(fq[n + 1]) : cur;
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(cur, fa[1][m], acc[n][m]);
+      cur = nxt;
     }
-    __builtin_amdgcn_sched_barrier(0);
-    cur = nxt;
   }
 }
 
-// K loop for fp8 weights.  Per stage kt (buffer kt % 3), two halves with a
-// barrier each:
-//   half 0: multiply half 0 while reading A half 1 of stage kt; wait until
-//           this wave's reads are done and stage kt+1 has landed (only stage
-//           kt+2's 6 loads outstanding), barrier.
-//   half 1: multiply half 1 while reading stage kt+1's A half 0 and weight
-//           fragments and refilling buffer kt % 3 with stage kt+3 (every
-//           wave's reads of it finished before the half-0 barrier); wait for
-//           the reads, barrier.
-// Stage kt+3 then has a stage and a half to land.  The tail re-reads the
-// last stage into idle buffers, keeping the wait counts constant.
-template <int NM, int NSETS>
+// K loop for fp8 weights: the bf16 loop's ping-pong between wave groups G0
+// (waves 0-3) and G1 (waves 4-7), one 64-input stage per slot, a 3-deep ring
+// (R = kStagesF8), and each wave loading its own share (6 loads) of a stage.
+//   Slot 2k:   G0 multiplies stage k; G1 reads stage k and loads stage k+2.
+//   Slot 2k+1: G1 multiplies stage k; G0 reads stage k+1 and loads stage k+3.
+// Every memory slot ends with lgkmcnt(0) and vmcnt(6): only the share just
+// issued may be in flight, so G1 has stage k+1 and G0 stage k+2 complete,
+// each ahead of the barrier before its first reader.  The buffer a load
+// refills held stage k-1 (G1, last read in slot 2k-2) or stage k (G0, last
+// read in slot 2k); the other buffers hold stages being read or still
+// landing.  Loads past the last stage are not issued (those slots wait for
+// everything instead); the prologue re-reads the last stage into buffers
+// that are never read when K has fewer stages than the ring.
+template <int NM, int NSETS, int G>
 __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
+  constexpr int R = kStagesF8;
   const int KT = c.KT;
+  u32x4_t fa[2][4], fq[8];
 #pragma unroll
-  for (int s = 0; s < kStagesF8; ++s)
-#pragma unroll
-    for (int d = 0; d < 6; ++d) issue_one_f8(c, s < KT ? s : KT - 1, s, d);
-  __builtin_amdgcn_s_waitcnt(kWaitVm12);  // stage 0 landed
+  for (int s = 0; s < (G == 0 ? R : R - 1); ++s) issue_share_f8(c, s < KT ? s : KT - 1, s);
+  __builtin_amdgcn_s_waitcnt(wait_vm(6 * (G == 0 ? R - 1 : R - 2), false));
   asm volatile("s_barrier" ::: "memory");
-  u32x4_t fa0[4], fa1[4], fq[8];
-  if constexpr (NM > 0) {
-#pragma unroll
-    for (int m = 0; m < NM; ++m) fa0[m] = read_a_frag(c, c.lds, m);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) fq[n] = read_b_frag<NSETS>(c, c.lds + 2 * kAStage, n);
+  if constexpr (G == 0) {
+    if constexpr (NM > 0) read_stage_f8<NM, NSETS>(c, 0, fa, fq);
+    __builtin_amdgcn_s_waitcnt(wait_vm(6 * (R - 2), true));
   }
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  int buf = 0;
+  asm volatile("s_barrier" ::: "memory");
+
+  int rd = G == 0 ? 1 : 0;      // buffer of the stage this group reads next
+  int wr = G == 0 ? 0 : R - 1;  // buffer its next load refills
   for (int kt = 0; kt < KT; ++kt) {
-    const int next = buf == kStagesF8 - 1 ? 0 : buf + 1;
-    const unsigned char* cur_st = c.lds + buf * kStageF8;
-    const unsigned char* next_st = c.lds + next * kStageF8;
-    half_f8<NM, NSETS, 0>(c, acc, fa0, fa1, fq, cur_st + kAStage, nullptr, 0, 0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    half_f8<NM, NSETS, 1>(c, acc, fa1, fa0, fq, next_st, next_st + 2 * kAStage, kt + 3 < KT ? kt + 3 : KT - 1,
-                          buf);
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    buf = next;
+    if constexpr (G == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
+      multiply_f8<NM>(acc, fa, fq);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NM > 0)
+        if (kt + 1 < KT) read_stage_f8<NM, NSETS>(c, rd, fa, fq);
+      if (kt + R < KT) {
+        issue_share_f8(c, kt + R, wr);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_vm(6 * (R - 2), true));
+      } else {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_vm(0, true));
+      }
+      asm volatile("s_barrier" ::: "memory");
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NM > 0) read_stage_f8<NM, NSETS>(c, rd, fa, fq);
+      if (kt + R - 1 < KT) {
+        issue_share_f8(c, kt + R - 1, wr);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_vm(6 * (R - 2), true));
+      } else {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_vm(0, true));
+      }
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
+      multiply_f8<NM>(acc, fa, fq);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
+    }
+    rd = rd + 1 == R ? 0 : rd + 1;
+    wr = wr + 1 == R ? 0 : wr + 1;
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
@@ -547,12 +570,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   const int groups = (ti.rows + 15) >> 4;
   const int nm = groups > wm ? min(4, (groups - wm + 3) >> 2) : 0;
   if constexpr (F8) {
-    switch (nm) {
-      case 4: k_loop_f8<4, NSETS>(c, acc); break;
-      case 3: k_loop_f8<3, NSETS>(c, acc); break;
-      case 2: k_loop_f8<2, NSETS>(c, acc); break;
-      case 1: k_loop_f8<1, NSETS>(c, acc); break;
-      default: k_loop_f8<0, NSETS>(c, acc); break;
+    if (wave < 4) {
+      switch (nm) {
+        case 4: k_loop_f8<4, NSETS, 0>(c, acc); break;
+        case 3: k_loop_f8<3, NSETS, 0>(c, acc); break;
+        case 2: k_loop_f8<2, NSETS, 0>(c, acc); break;
+        case 1: k_loop_f8<1, NSETS, 0>(c, acc); break;
+        default: k_loop_f8<0, NSETS, 0>(c, acc); break;
+      }
+    } else {
+      switch (nm) {
+        case 4: k_loop_f8<4, NSETS, 1>(c, acc); break;
+        case 3: k_loop_f8<3, NSETS, 1>(c, acc); break;
+        case 2: k_loop_f8<2, NSETS, 1>(c, acc); break;
+        case 1: k_loop_f8<1, NSETS, 1>(c, acc); break;
+        default: k_loop_f8<0, NSETS, 1>(c, acc); break;
+      }
     }
   } else {
     if (wave < 4) {  // the two ping-pong groups run mirrored loops
