@@ -30,6 +30,13 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(bf16_t, b);
 }
 
+// s_waitcnt immediate for vmcnt(vm) (0..63), with or without lgkmcnt(0)
+// (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8; a
+// field at its maximum does not wait).
+__host__ __device__ constexpr int wait_vm(int vm, bool lgkm0) {
+  return (vm & 15) | ((vm >> 4) << 14) | 0x70 | (lgkm0 ? 0 : 0xF00);
+}
+
 // gate * silu(up) = g * u / (1 + exp(-u)) (components/activation/swiglu.mlir:37-47)
 // for the MFMA kernels, whose SwiGLU output is stored as bf16: the hardware
 // reciprocal (1 ulp) stands in for an IEEE division, far below bf16's

@@ -56,10 +56,6 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x
 // builtin so the compiler's own wait insertion accounts for them.
 constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
-// vmcnt(vm) (0..63), with or without lgkmcnt(0).
-__host__ __device__ constexpr int wait_vm(int vm, bool lgkm0) {
-  return (vm & 15) | ((vm >> 4) << 14) | 0x70 | (lgkm0 ? 0 : 0xF00);
-}
 
 __host__ __device__ __forceinline__ int split_boundary(int kblocks, int ksplit, int s) {
   return s >= ksplit ? kblocks : (s * kblocks / ksplit) & ~1;

@@ -7,8 +7,8 @@
 // renormalisation); oracles/moe.py:86-105.
 //
 // One block handles kTok = 16 tokens.  Logits for those tokens land in LDS,
-// then each wave runs softmax + top-k for 4 of the tokens with the expert
-// axis spread over its 64 lanes.
+// then softmax + top-k runs four tokens per wave (16 lanes each, DPP row
+// reductions) for k <= 16, or one token per wave over its 64 lanes.
 #include "common.h"
 #include "launch.h"
 
@@ -20,80 +20,186 @@ constexpr int kThreads = 256;
 constexpr int kMaxExpert = 256;    // lanes hold up to 4 experts each
 constexpr int kMfmaMaxExpert = 128;
 
-// Softmax + top-k + optional renormalisation of kTok tokens whose logits
-// are in lds_logits[kTok][ld].
-// The block's n_waves waves take tokens wave, wave + n_waves, ...
-__device__ void softmax_topk(const float* lds_logits, int ld, int tok0, int n_tokens,
-                             int n_expert, int k, bool normalize, int* ids, float* weights,
-                             int n_waves) {
+// Softmax + top-k + optional renormalisation of token t, whose logits are
+// lg[0 .. n_expert), by one wave with the expert axis spread over its lanes.
+__device__ void softmax_topk_token(const float* lg, int t, int n_tokens, int n_expert, int k, bool normalize,
+                                   int* ids, float* weights) {
   const int lane = threadIdx.x & (kWave - 1);
+  float p[4];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + i * kWave;
+    p[i] = e < n_expert ? lg[e] : -INFINITY;
+    m = fmaxf(m, p[i]);
+  }
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + i * kWave;
+    p[i] = e < n_expert ? expf(p[i] - m) : 0.f;
+    s += p[i];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + i * kWave;
+    p[i] = e < n_expert ? p[i] / s : -1.f;  // -1 marks "not selectable"
+  }
+  // Lane `slot` keeps the slot's expert and probability.
+  float my_w = 0.f;
+  int my_id = 0;
+  for (int slot = 0; slot < k; ++slot) {
+    // lane-local best: larger value, then lower index (i ascending -> e ascending)
+    float bv = -1.f;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (p[i] > bv) {
+        bv = p[i];
+        bi = lane + i * kWave;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, kWave);
+      const int oi = __shfl_xor(bi, o, kWave);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + i * kWave == bi) p[i] = -1.f;
+    if (lane == slot) {
+      my_w = bv;
+      my_id = bi;
+    }
+  }
+  if (normalize) {
+    // Sum in slot order (the linalg reduction of moe_ffn_block.mlir:97-107).
+    float wsum = 0.f;
+    for (int slot = 0; slot < k; ++slot) wsum += __shfl(my_w, slot, kWave);
+    my_w = my_w / wsum;
+  }
+  if (lane < k) {
+    ids[static_cast<int64_t>(lane) * n_tokens + t] = my_id;
+    weights[static_cast<int64_t>(lane) * n_tokens + t] = my_w;
+  }
+}
+
+// Row rotation within 16-lane DPP rows (row_ror:N), for reductions over a
+// row without going through LDS.
+template <int N>
+__device__ __forceinline__ int ror16(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xF, 0xF, false);
+}
+template <int N>
+__device__ __forceinline__ float ror16(float v) {
+  return __builtin_bit_cast(float, ror16<N>(__builtin_bit_cast(int, v)));
+}
+
+// Softmax + top-k (k <= 16, n_expert <= 256) of four tokens at once, one per
+// 16-lane row: row g takes token t0 + g, whose logits are lg[g * ld + e];
+// lane j of the row holds experts j, j + 16, ...  Reductions over the row
+// use DPP rotations.  The selection runs on the logits (the softmax is
+// monotonic with one denominator per token, so the order and exact ties
+// are those of the probabilities): larger first, lower expert index on
+// ties.  Each token's denominator is the one its lane 0 summed.
+__device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int n_expert, int k, bool normalize,
+                              int* ids, float* weights) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int g = lane >> 4, j = lane & 15;
+  const int t = t0 + g;
+  const float* row = lg + g * ld;
+  float v[16];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = j + 16 * i;
+    v[i] = e < n_expert ? row[e] : -INFINITY;
+    m = fmaxf(m, v[i]);
+  }
+  m = fmaxf(m, ror16<8>(m));
+  m = fmaxf(m, ror16<4>(m));
+  m = fmaxf(m, ror16<2>(m));
+  m = fmaxf(m, ror16<1>(m));
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (j + 16 * i < n_expert) s += expf(v[i] - m);
+  s += ror16<8>(s);
+  s += ror16<4>(s);
+  s += ror16<2>(s);
+  s += ror16<1>(s);
+  s = __shfl(s, lane & ~15, kWave);
+  float my_l = -INFINITY;
+  int my_id = 0;
+  for (int slot = 0; slot < k; ++slot) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (j + 16 * i < n_expert && v[i] > bv) {  // i ascending: ties keep the lower expert
+        bv = v[i];
+        bi = j + 16 * i;
+      }
+    }
+#define FMOE_TOPK_STEP(N)                                   \
+    {                                                       \
+      const float ov = ror16<N>(bv);                        \
+      const int oi = ror16<N>(bi);                          \
+      if (ov > bv || (ov == bv && oi < bi)) {               \
+        bv = ov;                                            \
+        bi = oi;                                            \
+      }                                                     \
+    }
+    FMOE_TOPK_STEP(8)
+    FMOE_TOPK_STEP(4)
+    FMOE_TOPK_STEP(2)
+    FMOE_TOPK_STEP(1)
+#undef FMOE_TOPK_STEP
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (j + 16 * i == bi) v[i] = -INFINITY;
+    if (j == slot) {
+      my_l = bv;
+      my_id = bi;
+    }
+  }
+  float my_w = expf(my_l - m) / s;
+  if (normalize) {
+    // Sum in slot order (the linalg reduction of moe_ffn_block.mlir:97-107).
+    float wsum = 0.f;
+    for (int slot = 0; slot < k; ++slot) wsum += __shfl(my_w, (lane & ~15) + slot, kWave);
+    my_w = my_w / wsum;
+  }
+  if (j < k && t < n_tokens) {
+    ids[static_cast<int64_t>(j) * n_tokens + t] = my_id;
+    weights[static_cast<int64_t>(j) * n_tokens + t] = my_w;
+  }
+}
+
+// Softmax + top-k of the kTok tokens from tok0 whose logits are in
+// lds_logits[kTok][ld]; the block's n_waves waves take tokens wave,
+// wave + n_waves, ...
+__device__ void softmax_topk(const float* lds_logits, int ld, int tok0, int n_tokens, int n_expert, int k,
+                             bool normalize, int* ids, float* weights, int n_waves) {
   const int wave = threadIdx.x / kWave;
+  if (k <= 16) {
+    // four tokens per wave, 16 lanes each
+    for (int q = wave; q < kTok / 4; q += n_waves) {
+      if (tok0 + 4 * q >= n_tokens) break;
+      softmax_topk4(lds_logits + 4 * q * ld, ld, tok0 + 4 * q, n_tokens, n_expert, k, normalize, ids, weights);
+    }
+    return;
+  }
   for (int tt = wave; tt < kTok; tt += n_waves) {
     const int t = tok0 + tt;
     if (t >= n_tokens) break;
-    float p[4];
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + i * kWave;
-      p[i] = e < n_expert ? lds_logits[tt * ld + e] : -INFINITY;
-      m = fmaxf(m, p[i]);
-    }
-    m = wave_max(m);
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + i * kWave;
-      p[i] = e < n_expert ? expf(p[i] - m) : 0.f;
-      s += p[i];
-    }
-    s = wave_sum(s);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + i * kWave;
-      p[i] = e < n_expert ? p[i] / s : -1.f;  // -1 marks "not selectable"
-    }
-    // Lane `slot` keeps the slot's expert and probability.
-    float my_w = 0.f;
-    int my_id = 0;
-    for (int slot = 0; slot < k; ++slot) {
-      // lane-local best: larger value, then lower index (i ascending -> e ascending)
-      float bv = -1.f;
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (p[i] > bv) {
-          bv = p[i];
-          bi = lane + i * kWave;
-        }
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, kWave);
-        const int oi = __shfl_xor(bi, o, kWave);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (lane + i * kWave == bi) p[i] = -1.f;
-      if (lane == slot) {
-        my_w = bv;
-        my_id = bi;
-      }
-    }
-    if (normalize) {
-      // Sum in slot order (the linalg reduction of moe_ffn_block.mlir:97-107).
-      float wsum = 0.f;
-      for (int slot = 0; slot < k; ++slot) wsum += __shfl(my_w, slot, kWave);
-      my_w = my_w / wsum;
-    }
-    if (lane < k) {
-      ids[static_cast<int64_t>(lane) * n_tokens + t] = my_id;
-      weights[static_cast<int64_t>(lane) * n_tokens + t] = my_w;
-    }
+    softmax_topk_token(lds_logits + tt * ld, t, n_tokens, n_expert, k, normalize, ids, weights);
   }
 }
 

@@ -111,10 +111,12 @@ def test_router_configs(fm, wl, cfg_name, T):
         _router_check(fm, x, wr, cfg.n_expert_used, cfg.normalize)
 
 
-# Large batches with 33..128 experts and uneven expert counts (33, 40, 80
-# leave MFMA columns partly unused).
+# Large batches with 33..256 experts and uneven expert counts (33, 40, 80,
+# 200 leave MFMA columns partly unused; above 128 experts the SIMT kernel
+# runs).  k <= 16 takes the four-tokens-per-wave top-k.
 @pytest.mark.parametrize("E,k,H,T", [(128, 8, 2048, 8192), (64, 6, 2048, 512), (80, 4, 256, 300),
-                                     (40, 2, 128, 256), (33, 1, 64, 1000)])
+                                     (40, 2, 128, 256), (33, 1, 64, 1000), (256, 8, 512, 512),
+                                     (200, 6, 320, 700), (160, 4, 192, 256), (128, 8, 2048, 255)])
 def test_router_wide(fm, wl, E, k, H, T):
     cfg = wl.Config("R", H, 64, E, k, (T,), "bf16", "bf16", True, 1e-4, seed=E)
     x, wr, _ = wl.router_inputs(cfg, T)
