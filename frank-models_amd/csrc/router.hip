@@ -101,23 +101,25 @@ __device__ __forceinline__ float ror16(float v) {
   return __builtin_bit_cast(float, ror16<N>(__builtin_bit_cast(int, v)));
 }
 
-// Softmax + top-k (k <= 16, n_expert <= 256) of four tokens at once, one per
-// 16-lane row: row g takes token t0 + g, whose logits are lg[g * ld + e];
-// lane j of the row holds experts j, j + 16, ...  Reductions over the row
+// Softmax + top-k (k <= 16, n_expert <= 16 NV <= 256) of four tokens at
+// once, one per 16-lane row: row g takes token t0 + g, whose logits are
+// lg[g * ld + e]; lane j of the row holds experts j, j + 16, ... (NV each:
+// each is a few VALU instructions per slot, at 4 cycles each for a wave).  Reductions over the row
 // use DPP rotations.  The selection runs on the logits (the softmax is
 // monotonic with one denominator per token, so the order and exact ties
 // are those of the probabilities): larger first, lower expert index on
 // ties.  Each token's denominator is the one its lane 0 summed.
+template <int NV>
 __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int n_expert, int k, bool normalize,
                               int* ids, float* weights) {
   const int lane = threadIdx.x & (kWave - 1);
   const int g = lane >> 4, j = lane & 15;
   const int t = t0 + g;
   const float* row = lg + g * ld;
-  float v[16];
+  float v[NV];
   float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < NV; ++i) {
     const int e = j + 16 * i;
     v[i] = e < n_expert ? row[e] : -INFINITY;
     m = fmaxf(m, v[i]);
@@ -128,7 +130,7 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
   m = fmaxf(m, ror16<1>(m));
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
+  for (int i = 0; i < NV; ++i)
     if (j + 16 * i < n_expert) s += expf(v[i] - m);
   s += ror16<8>(s);
   s += ror16<4>(s);
@@ -141,7 +143,7 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < NV; ++i) {
       if (j + 16 * i < n_expert && v[i] > bv) {  // i ascending: ties keep the lower expert
         bv = v[i];
         bi = j + 16 * i;
@@ -162,7 +164,7 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
     FMOE_TOPK_STEP(1)
 #undef FMOE_TOPK_STEP
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < NV; ++i)
       if (j + 16 * i == bi) v[i] = -INFINITY;
     if (j == slot) {
       my_l = bv;
@@ -185,6 +187,8 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
 // Softmax + top-k of the kTok tokens from tok0 whose logits are in
 // lds_logits[kTok][ld]; the block's n_waves waves take tokens wave,
 // wave + n_waves, ...
+// NV bounds the experts per lane of the four-token path (n_expert <= 16 NV).
+template <int NV>
 __device__ void softmax_topk(const float* lds_logits, int ld, int tok0, int n_tokens, int n_expert, int k,
                              bool normalize, int* ids, float* weights, int n_waves) {
   const int wave = threadIdx.x / kWave;
@@ -192,7 +196,7 @@ __device__ void softmax_topk(const float* lds_logits, int ld, int tok0, int n_to
     // four tokens per wave, 16 lanes each
     for (int q = wave; q < kTok / 4; q += n_waves) {
       if (tok0 + 4 * q >= n_tokens) break;
-      softmax_topk4(lds_logits + 4 * q * ld, ld, tok0 + 4 * q, n_tokens, n_expert, k, normalize, ids, weights);
+      softmax_topk4<NV>(lds_logits + 4 * q * ld, ld, tok0 + 4 * q, n_tokens, n_expert, k, normalize, ids, weights);
     }
     return;
   }
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void router_simt_kernel(
     lds[tt * ld + e] = acc;
   }
   __syncthreads();
-  softmax_topk(lds, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights, kThreads / kWave);
+  softmax_topk<kMaxExpert / 16>(lds, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights, kThreads / kWave);
 }
 
 // MFMA logits for bf16 inputs, n_embd % 32 == 0, n_expert <= 128.
@@ -315,7 +319,8 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
     logits[tt * ld + e] = v;
   }
   __syncthreads();
-  softmax_topk(logits, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights, kMfmaWaves);
+  softmax_topk<kMfmaMaxExpert / 16>(logits, ld, tok0, n_tokens, n_expert, k, normalize != 0, ids, weights,
+                                    kMfmaWaves);
 }
 
 }  // namespace
