@@ -232,6 +232,8 @@ struct BlockLayout {
   size_t ids, weights;
   PermuteLayout perm;
   size_t h, y, total;
+  size_t rpart;          // decode router's split logits (0 bytes when the shape takes the general router)
+  size_t rpart_bytes;
   int h_dtype, y_dtype;
   int y_parts;           // fp32 partial buffers reserved for a K-split down GEMM
   int64_t y_part_elems;  // elements per partial
@@ -268,6 +270,10 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   off += align_up(static_cast<size_t>(n) * 4);
   L.perm = permute_layout(n, E, off);
   off = L.perm.total;
+  L.rpart = off;
+  L.rpart_bytes = router_decode_scratch_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
+                                              static_cast<int>(k), act);
+  off += align_up(L.rpart_bytes);
   L.h_dtype = act;
   L.h = off;
   off += align_up(static_cast<size_t>(n) * F * dtype_bytes(L.h_dtype));
@@ -387,14 +393,22 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   void* h = at<char>(workspace, L.h);
   void* y = at<char>(workspace, L.y);
 
-  // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128).
-  {
+  // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128),
+  // then the slot-major assignments grouped by expert (replaces the gather,
+  // mul_mat_id.mlir:50-61).  Decode-sized batches run both as two launches.
+  const bool decode_router = L.rpart_bytes > 0 && reinterpret_cast<uintptr_t>(c.input) % 16 == 0 &&
+                             reinterpret_cast<uintptr_t>(c.w_router) % 16 == 0;
+  if (decode_router) {
     ScopedTimer t(FMOE_TIMER_ROUTER, s);
-    FMOE_HIP(launch_router(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
-                           static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype, ids, rw, s));
-  }
-  // Group the slot-major assignments by expert (replaces the gather, mul_mat_id.mlir:50-61).
-  {
+    FMOE_HIP(launch_router_decode(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
+                                  static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype,
+                                  at<float>(workspace, L.rpart), ids, rw, order, offsets, err, s));
+  } else {
+    {
+      ScopedTimer t(FMOE_TIMER_ROUTER, s);
+      FMOE_HIP(launch_router(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
+                             static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype, ids, rw, s));
+    }
     ScopedTimer t(FMOE_TIMER_PERMUTE, s);
     FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err,
                             at<int>(workspace, L.perm.scratch), s));

@@ -37,6 +37,16 @@ __host__ __device__ constexpr int wait_vm(int vm, bool lgkm0) {
   return (vm & 15) | ((vm >> 4) << 14) | 0x70 | (lgkm0 ? 0 : 0xF00);
 }
 
+// Block barrier that orders LDS accesses only: unlike __syncthreads it does
+// not wait for the wave's outstanding global stores.  For blocks whose
+// threads exchange data through LDS alone (global memory written before the
+// barrier is not read by another thread of the block after it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // gate * silu(up) = g * u / (1 + exp(-u)) (components/activation/swiglu.mlir:37-47)
 // for the MFMA kernels, whose SwiGLU output is stored as bf16: the hardware
 // reciprocal (1 ulp) stands in for an IEEE division, far below bf16's

@@ -110,6 +110,18 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
                          int n_expert, int k, bool normalize, int dtype, int* ids,
                          float* weights, hipStream_t stream);
 
+// Decode-sized batches (bf16, n_tokens <= kDecodeMaxTokens, n_expert <= 256,
+// k <= 16): router logits split over many blocks into `part`
+// (router_decode_scratch_bytes, 0 when the shape does not qualify), then one
+// block runs softmax + top-k and the permutation (ids, weights, order,
+// offsets, err_count as launch_router + launch_permute write them).
+// hipErrorNotSupported when the inputs do not qualify.
+constexpr int kDecodeMaxTokens = 64;
+size_t router_decode_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k, int dtype);
+hipError_t launch_router_decode(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k,
+                                bool normalize, int dtype, float* part, int* ids, float* weights, int* order,
+                                int* offsets, int* err_count, hipStream_t stream);
+
 // Batches above kPermuteChunk assignments run chunked, with a histogram
 // scratch of permute_scratch_bytes() (0 for smaller batches).
 constexpr int kPermuteChunk = 2048;

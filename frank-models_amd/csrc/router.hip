@@ -11,6 +11,7 @@
 // reductions) for k <= 16, or one token per wave over its 64 lanes.
 #include "common.h"
 #include "launch.h"
+#include "permute_block.h"
 
 namespace fmoe {
 namespace {
@@ -111,7 +112,7 @@ __device__ __forceinline__ float ror16(float v) {
 // ties.  Each token's denominator is the one its lane 0 summed.
 template <int NV>
 __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int n_expert, int k, bool normalize,
-                              int* ids, float* weights) {
+                              int* ids, float* weights, int* ids_copy = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   const int g = lane >> 4, j = lane & 15;
   const int t = t0 + g;
@@ -181,6 +182,7 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
   if (j < k && t < n_tokens) {
     ids[static_cast<int64_t>(j) * n_tokens + t] = my_id;
     weights[static_cast<int64_t>(j) * n_tokens + t] = my_w;
+    if (ids_copy) ids_copy[j * n_tokens + t] = my_id;
   }
 }
 
@@ -323,6 +325,132 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
                                     kMfmaWaves);
 }
 
+// ---- Decode-sized batches (T <= kDecodeMaxTokens, bf16, k <= 16,
+// n_expert <= 256): the logits are split over many blocks instead of
+// streaming the whole router matrix through one CU, and one block finishes
+// the softmax, top-k and the token -> expert permutation.
+//
+// router_split_logits_kernel: block (token group of 16, expert chunk of 16,
+// column split of kSplitCols hidden columns); 4 waves take 128 columns each
+// (4 trips of 32, all loaded before the first MFMA) and are summed in wave
+// order.  part[(split * T + t) * E + e] holds the split's partial logit.
+constexpr int kSplitCols = 512;
+constexpr int kSplitWaves = 4;
+
+__device__ __forceinline__ u32x4_t ld16(const bf16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+__global__ __launch_bounds__(kSplitWaves * kWave) void router_split_logits_kernel(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, int n_tokens, int n_embd, int n_expert,
+    float* __restrict__ part) {
+  __shared__ f32x4_t red[kSplitWaves][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row = lane & 15, kofs = (lane >> 4) * 8;
+  const int t = min(static_cast<int>(blockIdx.x) * 16 + row, n_tokens - 1);   // rows past the end repeat
+  const int e = min(static_cast<int>(blockIdx.y) * 16 + row, n_expert - 1);   // the last token / expert
+  const bf16_t* xr = x + static_cast<int64_t>(t) * n_embd + kofs;
+  const bf16_t* wrow = wr + static_cast<int64_t>(e) * n_embd + kofs;
+  const int h0 = static_cast<int>(blockIdx.z) * kSplitCols + wave * 128;
+  const u32x4_t zero{0u, 0u, 0u, 0u};
+  u32x4_t a[4], b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = h0 + 32 * j;
+    a[j] = h < n_embd ? ld16(xr + h) : zero;
+    b[j] = h < n_embd ? ld16(wrow + h) : zero;
+  }
+  f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[j]), __builtin_bit_cast(bf16x8_t, b[j]),
+                                                  acc, 0, 0, 0);
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    f32x4_t v = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kSplitWaves; ++w) v += red[w][lane];
+    // D[token][expert]: lane holds expert (lane & 15), tokens 4*(lane>>4)+i.
+    const int ee = static_cast<int>(blockIdx.y) * 16 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tt = static_cast<int>(blockIdx.x) * 16 + (lane >> 4) * 4 + i;
+      if (tt < n_tokens && ee < n_expert)
+        part[(static_cast<int64_t>(blockIdx.z) * n_tokens + tt) * n_expert + ee] = v[i];
+    }
+  }
+}
+
+// One block: logits = the splits' partials summed in split order, softmax +
+// top-k four tokens per wave (n_expert <= 16 NV), then the permutation of the
+// k * T slot-major ids, read back from an LDS copy.  The partials of kSumU
+// logits x kSumS splits are loaded before any is added, so a thread waits
+// for memory once per group rather than once per partial.
+constexpr int kSumU = 4, kSumS = 8;
+
+size_t topk_permute_lds_bytes(int n_tokens, int n_expert, int k) {
+  return (static_cast<size_t>((n_tokens + 3) / 4 * 4) * (n_expert + 1) + static_cast<size_t>(k) * n_tokens) * 4;
+}
+
+template <int NV>
+__global__ __launch_bounds__(perm::kThreads) void router_topk_permute_kernel(
+    const float* __restrict__ part, int n_split, int n_tokens, int n_expert, int k, int normalize,
+    int* __restrict__ ids, float* __restrict__ weights, int* __restrict__ order, int* __restrict__ offsets,
+    int* __restrict__ err_count) {
+  extern __shared__ float lg[];  // [roundup(T, 4)][n_expert + 1] logits, then k * T ids
+  const int ld = n_expert + 1;
+  int* ids_lds = reinterpret_cast<int*>(lg + (n_tokens + 3) / 4 * 4 * ld);
+  const int n = n_tokens * n_expert;
+  for (int i0 = threadIdx.x; i0 < n; i0 += kSumU * perm::kThreads) {
+    float acc[kSumU];
+#pragma unroll
+    for (int u = 0; u < kSumU; ++u) acc[u] = 0.f;
+    for (int s0 = 0; s0 < n_split; s0 += kSumS) {
+      float pv[kSumU][kSumS];
+#pragma unroll
+      for (int u = 0; u < kSumU; ++u)
+#pragma unroll
+        for (int q = 0; q < kSumS; ++q) {
+          const int idx = i0 + u * perm::kThreads;
+          pv[u][q] = idx < n && s0 + q < n_split ? part[static_cast<int64_t>(s0 + q) * n + idx] : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < kSumU; ++u)
+#pragma unroll
+        for (int q = 0; q < kSumS; ++q)
+          if (s0 + q < n_split) acc[u] += pv[u][q];
+    }
+#pragma unroll
+    for (int u = 0; u < kSumU; ++u) {
+      const int idx = i0 + u * perm::kThreads;
+      if (idx < n) {
+        const int t = idx / n_expert;
+        lg[t * ld + idx - t * n_expert] = acc[u];
+      }
+    }
+  }
+  lds_barrier();
+  const int wave = threadIdx.x / kWave;
+  for (int q = wave; 4 * q < n_tokens; q += perm::kWaves)
+    softmax_topk4<NV>(lg + 4 * q * ld, ld, 4 * q, n_tokens, n_expert, k, normalize != 0, ids, weights, ids_lds);
+  lds_barrier();
+  perm::permute_block(ids_lds, k * n_tokens, n_expert, order, offsets, err_count);
+}
+
+template <int NV>
+hipError_t launch_topk_permute(const float* part, int n_split, int n_tokens, int n_expert, int k, bool normalize,
+                               int* ids, float* weights, int* order, int* offsets, int* err, hipStream_t stream) {
+  const size_t lds = topk_permute_lds_bytes(n_tokens, n_expert, k);
+  // Up to 64 x 257 logits and 1024 ids, a little over the 64 KiB default.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(router_topk_permute_kernel<NV>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(topk_permute_lds_bytes(kDecodeMaxTokens, 256, 16)));
+  (void)attr;
+  hipLaunchKernelGGL((router_topk_permute_kernel<NV>), dim3(1), dim3(perm::kThreads), lds, stream, part, n_split,
+                     n_tokens, n_expert, k, normalize ? 1 : 0, ids, weights, order, offsets, err);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert,
@@ -359,6 +487,38 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
     }
   }
   return hipGetLastError();
+}
+
+}  // namespace fmoe
+
+namespace fmoe {
+
+size_t router_decode_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k, int dtype) {
+  if (dtype != DT_BF16 || n_tokens <= 0 || n_tokens > kDecodeMaxTokens || n_embd % 32 || n_expert <= 0 ||
+      n_expert > 256 || k <= 0 || k > 16 || k > n_expert)
+    return 0;
+  const int n_split = (n_embd + kSplitCols - 1) / kSplitCols;
+  return static_cast<size_t>(n_split) * n_tokens * n_expert * sizeof(float);
+}
+
+hipError_t launch_router_decode(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k,
+                                bool normalize, int dtype, float* part, int* ids, float* weights, int* order,
+                                int* offsets, int* err_count, hipStream_t stream) {
+  if (!part || router_decode_scratch_bytes(n_tokens, n_embd, n_expert, k, dtype) == 0 ||
+      reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(wr) % 16)
+    return hipErrorNotSupported;
+  const int n_split = (n_embd + kSplitCols - 1) / kSplitCols;
+  hipLaunchKernelGGL(router_split_logits_kernel, dim3((n_tokens + 15) / 16, (n_expert + 15) / 16, n_split),
+                     dim3(kSplitWaves * kWave), 0, stream, static_cast<const bf16_t*>(x),
+                     static_cast<const bf16_t*>(wr), n_tokens, n_embd, n_expert, part);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int nv = (n_expert + 15) / 16;
+  if (nv <= 1) return launch_topk_permute<1>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
+  if (nv <= 2) return launch_topk_permute<2>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
+  if (nv <= 4) return launch_topk_permute<4>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
+  if (nv <= 8) return launch_topk_permute<8>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
+  return launch_topk_permute<16>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
 }
 
 }  // namespace fmoe

@@ -125,6 +125,24 @@ def test_unaligned_shapes_bf16(fm, wl, gemm_path, H, F, T):
 
 
 # ------------------------------------------------------------------ full-size configurations
+# Decode-sized batches (bf16, T <= 64, n_expert <= 256, k <= 16, H % 32 == 0)
+# take the split-logits router whose last block also permutes; these shapes
+# cover its edges: one and several column splits, expert counts that are not
+# a multiple of 16, k = 16, T = 64 and a token count not a multiple of 4.
+@pytest.mark.parametrize("name,H,F,T,E,k", [
+    ("C4", 512, 128, 1, 256, 16), ("C3", 1056, 128, 33, 160, 6), ("C4", 96, 64, 64, 256, 8),
+    ("C2", 2080, 128, 5, 8, 2), ("C3", 256, 64, 64, 40, 16), ("C4", 4096, 128, 3, 250, 7),
+])
+def test_decode_router_shapes(fm, wl, name, H, F, T, E, k):
+    # probabilities of 160+ experts sit closer together: a smaller margin
+    cfg = _scaled(wl, name, H, F, n_expert=E, n_expert_used=k, margin=1e-4 if E < 160 else 1e-5)
+    case = Case(fm, wl, cfg, T)
+    out = case.run()
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
+
+
 @pytest.mark.parametrize("name,T", [("C2", 16), ("C4", 1), ("C4", 4), ("C4", 16), ("C4", 64), ("C3", 64),
                                     ("C5", 16)])
 def test_full_size_decode(fm, wl, name, T):
