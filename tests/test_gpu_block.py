@@ -95,6 +95,8 @@ def test_c1_toy_fp32(fm, wl, gemm_path):
 SMALL = [
     ("C2", 256, 512, 16), ("C2", 256, 512, 300), ("C3", 128, 256, 64), ("C3", 128, 192, 700),
     ("C4", 256, 384, 1), ("C4", 256, 384, 64), ("C5", 256, 512, 16), ("C5", 256, 512, 300),
+    # short input axes of the down projection: several column tiles per streaming block
+    ("C3", 224, 96, 40), ("C5", 320, 128, 24),
 ]
 
 

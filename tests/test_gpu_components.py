@@ -61,19 +61,22 @@ def _router_check(fm, x, wr, k, norm, rtol_w=1e-5):
     np.testing.assert_allclose(w, rw, rtol=rtol_w, atol=1e-7)
 
 
-@pytest.mark.parametrize("path", ["tiled", "tiled_large", "auto"])
-@pytest.mark.parametrize("n_out,n_in,k,T", [(304, 512, 2, 300), (256, 256, 4, 700)])
+@pytest.mark.parametrize("path", ["tiled", "tiled_large", "stream", "auto"])
+@pytest.mark.parametrize("n_out,n_in,k,T", [(304, 512, 2, 300), (256, 256, 4, 700), (208, 96, 2, 40),
+                                            (208, 96, 2, 5)])
 def test_mul_mat_id_bf16_paths(fm, path, n_out, n_in, k, T):
     """bf16 mul_mat_id (plain scatter epilogue, bf16 output) on each MFMA
     path vs the oracle on the same bf16 values: rtol 2e-2 of the output's RMS.
     300 and 700 tokens over 8 experts give partial row tiles and (n_out 304)
-    a partial column tile."""
+    a partial column tile; n_out 208 (13 blocks of 16 rows) with a 96-input
+    axis leaves the streaming kernel's last block of column tiles part-full."""
     ll = fm.lowlevel
     rng = np.random.default_rng(n_out + T)
     w = torch.from_numpy((rng.standard_normal((n_out, n_in, 8)) * 0.05).astype(np.float32)).bfloat16()
     x = torch.from_numpy(rng.standard_normal((n_in, k, T)).astype(np.float32)).bfloat16()
     ids = np.stack([rng.permutation(8)[:k] for _ in range(T)], axis=1).astype(np.int32)
-    code = {"tiled": ll.PATH_TILED, "tiled_large": ll.PATH_TILED_LARGE, "auto": ll.PATH_AUTO}[path]
+    code = {"tiled": ll.PATH_TILED, "tiled_large": ll.PATH_TILED_LARGE, "stream": ll.PATH_STREAM,
+            "auto": ll.PATH_AUTO}[path]
     ll.check(ll.lib().fmoe_set_gemm_path(code))
     try:
         out = fm.mul_mat_id(w.cuda(), x.cuda(), torch.from_numpy(ids).cuda())
