@@ -16,6 +16,14 @@ Public API (same signatures as the reference's components/oracles):
 and per-layer loading of GGUF-named MoE parameters (``load_moe_layers``,
 ``save_packed`` / ``load_packed``, ``quantize_fp8``; see ``params``),
 
+the decode step's attention half (the component after the MoE block on
+the decode path): ``attention_block_decode(input, positions, k_cached,
+v_cached, wq, wk, wv, wo, bq, bk, bv, bo, use_bias, n_head, n_head_kv,
+n_embd, rope_freq_base, rope_freq_scale)``, the paged KV cache
+(``kvcache_gather``, ``kvcache_scatter_decode``, ``kvcache_scatter_prefill``)
+and ``AttentionBlockDecode`` (packed weights; ``.paged`` reads the paged
+cache in place),
+
 plus ``router``, ``permute``, ``pack_expert_weights``,
 ``quantize_expert_weights``, ``QuantizedExpertWeights``,
 ``PackedExpertWeights`` and ``MoEFFNBlock`` (packed weights + reusable
@@ -45,6 +53,15 @@ from .api import (  # noqa: F401
     rms_norm,
     router,
     swiglu,
+)
+from .attention import (  # noqa: F401
+    AttentionBlockDecode,
+    PackedLinearWeights,
+    attention_block_decode,
+    kvcache_gather,
+    kvcache_scatter_decode,
+    kvcache_scatter_prefill,
+    pack_linear_weights,
 )
 from . import _lib as lowlevel  # noqa: F401
 from . import params  # noqa: F401

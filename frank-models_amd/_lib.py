@@ -108,6 +108,34 @@ SIGNATURES = {
         [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
          ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
     ),
+    # decode attention half
+    "fmoe_kvcache_gather": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                 _vp, _vp],
+    ),
+    "fmoe_kvcache_scatter_decode": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_i64, _vp],
+    ),
+    "fmoe_kvcache_scatter_prefill": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64,
+                 _vp, _vp],
+    ),
+    "fmoe_pack_linear_weight": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _vp, _vp, _vp]),
+    "fmoe_attention_block_decode_workspace_bytes": (_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "fmoe_attention_block_decode": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, ctypes.c_float, _c_int, _vp, _vp, _vp, _vp, _sz,
+         _vp],
+    ),
+    "fmoe_attention_decode_paged_workspace_bytes": (_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "fmoe_attention_decode_paged": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp,
+         _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, ctypes.c_float, _c_int, _vp, _vp, _vp, _vp, _sz,
+         _vp],
+    ),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,568 @@
+// The decode step's attention half: paged KV cache copies, the projection
+// epilogue (bias + RoPE), and grouped-query attention of one new token per
+// sequence against the paged cache.
+//
+// Paged cache (components/kvcache/kvcache.mlir, oracles/kvcache.py:51-185):
+// a pool [n_blocks, block_size, n_head_kv, head_dim]; sequence b's position
+// j lives in physical block block_tables[b, j / block_size] at row
+// j % block_size.  The reference gathers max_context_len positions per
+// sequence (zero rows at and past context_lens[b]), appends the new K/V and
+// runs attention_gqa without a mask (attention_block_decode.mlir:202-216,
+// attention_gqa.mlir:120-137).  The attention kernels here read the pool in
+// place instead of gathering: the zero rows' contribution is exact in closed
+// form (score 0, value 0), so they are counted, not read.
+//
+// Attention is split over the context: one block per (split of kSplitLen
+// positions, KV head, sequence) computes, for the G query heads sharing the
+// KV head, the split's max score, sum of exp and unnormalised output; a
+// combine kernel merges the splits in order with the zero rows and the new
+// token.
+#include "common.h"
+#include "launch.h"
+
+namespace fmoe {
+namespace {
+
+constexpr int kCopyThreads = 256;
+
+// ------------------------------------------------------------------ cache copies
+// Rows are copied as 32-bit words (a row is n_head_kv * head_dim elements,
+// head_dim even, so a bf16 row is a whole number of words).
+
+__global__ __launch_bounds__(kCopyThreads) void kv_gather_kernel(const uint32_t* __restrict__ cache, int64_t n_blocks,
+                                                                 int block_size, int row_words,
+                                                                 const int* __restrict__ tables, int max_blocks,
+                                                                 const int* __restrict__ ctx_lens, int max_ctx,
+                                                                 uint32_t* __restrict__ out) {
+  const int j = blockIdx.x, b = blockIdx.y;
+  const int n = min(max(ctx_lens[b], 0), max_ctx);
+  const uint32_t* src = nullptr;
+  if (j < n) {
+    const int lb = j / block_size;
+    const int pb = lb < max_blocks ? tables[static_cast<int64_t>(b) * max_blocks + lb] : -1;
+    if (pb >= 0 && pb < n_blocks) src = cache + (static_cast<int64_t>(pb) * block_size + j % block_size) * row_words;
+  }
+  uint32_t* dst = out + (static_cast<int64_t>(b) * max_ctx + j) * row_words;
+  for (int w = threadIdx.x; w < row_words; w += kCopyThreads) dst[w] = src ? src[w] : 0u;
+}
+
+// One row per sequence; when several sequences name the same slot the last
+// one wins, as in the reference's sequential loop (oracles/kvcache.py:134-139).
+__global__ __launch_bounds__(kCopyThreads) void kv_scatter_decode_kernel(uint32_t* __restrict__ cache, int64_t n_blocks,
+                                                                         int block_size, int row_words,
+                                                                         const uint32_t* __restrict__ vals,
+                                                                         const int* __restrict__ block_idx,
+                                                                         const int* __restrict__ pos_idx, int batch) {
+  const int b = blockIdx.x;
+  const int bi = block_idx[b], p = pos_idx[b];
+  bool later = false;
+  for (int b2 = b + 1 + static_cast<int>(threadIdx.x); b2 < batch; b2 += kCopyThreads)
+    later |= block_idx[b2] == bi && pos_idx[b2] == p;
+  if (__syncthreads_or(later)) return;
+  if (bi < 0 || bi >= n_blocks || p < 0 || p >= block_size) return;
+  uint32_t* dst = cache + (static_cast<int64_t>(bi) * block_size + p) * row_words;
+  const uint32_t* src = vals + static_cast<int64_t>(b) * row_words;
+  for (int w = threadIdx.x; w < row_words; w += kCopyThreads) dst[w] = src[w];
+}
+
+__global__ __launch_bounds__(kCopyThreads) void kv_scatter_prefill_kernel(
+    uint32_t* __restrict__ cache, int64_t n_blocks, int block_size, int row_words, const uint32_t* __restrict__ vals,
+    int seq_len, const int* __restrict__ tables, int max_blocks, const int* __restrict__ start) {
+  const int s = blockIdx.x, b = blockIdx.y;
+  const int64_t p = static_cast<int64_t>(start[b]) + s;
+  if (p < 0) return;
+  const int64_t lb = p / block_size;
+  if (lb >= max_blocks) return;
+  const int pb = tables[static_cast<int64_t>(b) * max_blocks + lb];
+  if (pb < 0 || pb >= n_blocks) return;
+  uint32_t* dst = cache + (static_cast<int64_t>(pb) * block_size + p % block_size) * row_words;
+  const uint32_t* src = vals + (static_cast<int64_t>(b) * seq_len + s) * row_words;
+  for (int w = threadIdx.x; w < row_words; w += kCopyThreads) dst[w] = src[w];
+}
+
+// ------------------------------------------------------------------ small helpers
+__global__ void iota_kernel(int* __restrict__ v, int n, int* __restrict__ pair, int pair0, int pair1) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) v[i] = i;
+  if (i == 0 && pair) {
+    pair[0] = pair0;
+    pair[1] = pair1;
+  }
+}
+
+__global__ void fill_int_kernel(int* __restrict__ v, int n, int value) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) v[i] = value;
+}
+
+__device__ __forceinline__ float load_act(const void* p, int dt, int64_t i) {
+  return dt == DT_F32 ? static_cast<const float*>(p)[i] : bf16_to_f32(static_cast<const bf16_t*>(p)[i]);
+}
+
+__device__ __forceinline__ void store_act(void* p, int dt, int64_t i, float v) {
+  if (dt == DT_F32)
+    static_cast<float*>(p)[i] = v;
+  else
+    static_cast<bf16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// qkv [B, nq + 2 nkv] fp32 GEMM output -> + bias, RoPE on the q and k parts
+// (pairs (2i, 2i+1), angle pos * freq_scale / freq_base^(2i/D), in double
+// precision like the reference oracle), q_rot fp32 [B, nq], k_new / v_new
+// [B, nkv] in act dtype (rope.mlir:38-104, oracles/position.py:6-50).
+__global__ __launch_bounds__(256) void qkv_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ bq,
+                                                       const float* __restrict__ bk, const float* __restrict__ bv,
+                                                       const int64_t* __restrict__ positions, int nq, int nkv, int D,
+                                                       double freq_base, double freq_scale, float* __restrict__ q_rot,
+                                                       void* __restrict__ k_new, void* __restrict__ v_new, int act) {
+  const int b = blockIdx.x;
+  const int width = nq + 2 * nkv;
+  const float* row = qkv + static_cast<int64_t>(b) * width;
+  const double pos = static_cast<double>(positions[b]);
+  const int pairs = (nq + nkv) / 2;
+  for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
+    const int col = 2 * i;
+    const bool is_q = col < nq;
+    const int c = is_q ? col : col - nq;
+    const float* bias = is_q ? bq : bk;
+    float x0 = row[col], x1 = row[col + 1];
+    if (bias) {
+      x0 += bias[c];
+      x1 += bias[c + 1];
+    }
+    const int pi = (c % D) / 2;
+    const double freq = freq_scale / pow(freq_base, static_cast<double>(2 * pi) / D);
+    double sn, cs;
+    sincos(pos * freq, &sn, &cs);
+    const float cf = static_cast<float>(cs), sf = static_cast<float>(sn);
+    const float y0 = x0 * cf - x1 * sf;
+    const float y1 = x0 * sf + x1 * cf;
+    if (is_q) {
+      q_rot[static_cast<int64_t>(b) * nq + c] = y0;
+      q_rot[static_cast<int64_t>(b) * nq + c + 1] = y1;
+    } else {
+      store_act(k_new, act, static_cast<int64_t>(b) * nkv + c, y0);
+      store_act(k_new, act, static_cast<int64_t>(b) * nkv + c + 1, y1);
+    }
+  }
+  for (int c = threadIdx.x; c < nkv; c += blockDim.x) {
+    float v = row[nq + nkv + c];
+    if (bv) v += bv[c];
+    store_act(v_new, act, static_cast<int64_t>(b) * nkv + c, v);
+  }
+}
+
+// out[b, n] = y[b, n] (+ bias[n]) in act dtype.
+__global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict__ y, const float* __restrict__ bias,
+                                                        void* __restrict__ out, int64_t rows, int n, int act) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * n) return;
+  float v = y[i];
+  if (bias) v += bias[i % n];
+  store_act(out, act, i, v);
+}
+
+// ------------------------------------------------------------------ split attention
+template <typename T, int CW>
+__device__ __forceinline__ void load_chunk(const T* p, float (&v)[CW]);
+
+template <>
+__device__ __forceinline__ void load_chunk<float, 2>(const float* p, float (&v)[2]) {
+  const float2 x = *reinterpret_cast<const float2*>(p);
+  v[0] = x.x, v[1] = x.y;
+}
+template <>
+__device__ __forceinline__ void load_chunk<float, 4>(const float* p, float (&v)[4]) {
+  const float4 x = *reinterpret_cast<const float4*>(p);
+  v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+}
+__device__ __forceinline__ void unpack2(uint32_t w, float* v) {
+  v[0] = __uint_as_float(w << 16);
+  v[1] = __uint_as_float(w & 0xFFFF0000u);
+}
+template <>
+__device__ __forceinline__ void load_chunk<bf16_t, 2>(const bf16_t* p, float (&v)[2]) {
+  unpack2(*reinterpret_cast<const uint32_t*>(p), v);
+}
+template <>
+__device__ __forceinline__ void load_chunk<bf16_t, 4>(const bf16_t* p, float (&v)[4]) {
+  const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
+  unpack2(x[0], v);
+  unpack2(x[1], v + 2);
+}
+template <>
+__device__ __forceinline__ void load_chunk<bf16_t, 8>(const bf16_t* p, float (&v)[8]) {
+  const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
+  unpack2(x[0], v);
+  unpack2(x[1], v + 2);
+  unpack2(x[2], v + 4);
+  unpack2(x[3], v + 6);
+}
+__device__ __forceinline__ float load_one(const float* p) { return *p; }
+__device__ __forceinline__ float load_one(const bf16_t* p) { return bf16_to_f32(*p); }
+
+struct AttnArgs {
+  const float* q;         // [B, n_head * D] fp32, RoPE applied
+  const void* k_pool;     // [n_blocks, block_size, n_head_kv, D]
+  const void* v_pool;
+  const int* tables;      // [B, max_blocks] (this layer)
+  const int* ctx_lens;    // [B] (this layer)
+  int max_blocks;
+  int max_ctx;
+  int64_t n_blocks;
+  int block_size;
+  int n_head, n_head_kv;
+  int n_split;
+  float scale;
+  float* part;            // [B, n_head, n_split, D + 2]: o[D], m, l
+};
+
+constexpr int kSplitLen = 256;
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / kWave;
+
+// Block (split s, KV head, sequence b).  Scores: 8 lanes per position, each
+// lane holding DL of the D = 8 DL dimensions in chunks of CW elements, so
+// the 8 lanes of a position read each 128 B span of the row together; the
+// G query heads of the KV head are scored from one read of K.  Probabilities
+// stay in LDS; P.V: a wave takes a quarter of the split's positions, lanes
+// spread over the row (PP rows at once when D < 64).
+template <typename T, int DL, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
+  constexpr int D = 8 * DL;
+  constexpr int CW = (sizeof(T) == 4 ? 4 : 8) < DL ? (sizeof(T) == 4 ? 4 : 8) : DL;  // elements per 16 B (or less)
+  constexpr int NC = DL / CW;
+  constexpr int VW = D >= kWave ? D / kWave : 1;       // P.V elements per lane per row
+  constexpr int LPR = D / VW;                          // lanes per row in P.V
+  constexpr int PP = kWave / LPR;                      // rows per wave step in P.V
+  __shared__ float sc[G][kSplitLen];
+  __shared__ int rows[kSplitLen];
+  __shared__ float red[kAttnWaves][G][D];
+  __shared__ float stat[G][2];
+
+  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int n_b = min(max(a.ctx_lens[b], 0), a.max_ctx);
+  const int j0 = s * kSplitLen;
+  const int len = min(kSplitLen, n_b - j0);  // block-uniform; <= 0: no cached position here
+  float* part = a.part + (static_cast<int64_t>(b) * a.n_head + kvh * G) * a.n_split * (D + 2);
+  if (len <= 0) {
+    for (int i = tid; i < G * (D + 2); i += kAttnThreads) {
+      const int g = i / (D + 2), k = i - g * (D + 2);
+      part[(static_cast<int64_t>(g) * a.n_split + s) * (D + 2) + k] = k == D ? -INFINITY : 0.f;
+    }
+    return;
+  }
+  const int64_t row_elems = static_cast<int64_t>(a.n_head_kv) * D;
+  for (int t = tid; t < kSplitLen; t += kAttnThreads) {
+    int r = -2;  // -2: past the split's positions; -1: table entry out of range (a zero row)
+    if (t < len) {
+      const int j = j0 + t;
+      const int lb = j / a.block_size;
+      const int pb = lb < a.max_blocks ? a.tables[static_cast<int64_t>(b) * a.max_blocks + lb] : -1;
+      r = (pb >= 0 && pb < a.n_blocks) ? pb * a.block_size + j % a.block_size : -1;
+    }
+    rows[t] = r;
+  }
+  const T* kp = static_cast<const T*>(a.k_pool) + static_cast<int64_t>(kvh) * D;
+  const T* vp = static_cast<const T*>(a.v_pool) + static_cast<int64_t>(kvh) * D;
+  const int pi = lane >> 3, sub = lane & 7;
+  float q[G][DL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < CW; ++e)
+        q[g][c * CW + e] =
+            a.q[(static_cast<int64_t>(b) * a.n_head + kvh * G + g) * D + c * 8 * CW + sub * CW + e] * a.scale;
+  __syncthreads();
+
+  // ---- scores: 32 positions per block step, two steps' rows in flight
+  constexpr int kStep = kAttnWaves * 8;
+  for (int t0 = 0; t0 < len; t0 += 2 * kStep) {
+    float kv[2][DL];
+    int rr[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + u * kStep + wave * 8 + pi;
+      rr[u] = t < kSplitLen ? rows[t] : -2;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float v[CW];
+        if (rr[u] >= 0) {
+          load_chunk<T, CW>(kp + rr[u] * row_elems + c * 8 * CW + sub * CW, v);
+        } else {
+#pragma unroll
+          for (int e = 0; e < CW; ++e) v[e] = 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < CW; ++e) kv[u][c * CW + e] = v[e];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + u * kStep + wave * 8 + pi;
+      float dot[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < DL; ++i) acc = fmaf(q[g][i], kv[u][i], acc);
+        acc += __shfl_xor(acc, 1, kWave);
+        acc += __shfl_xor(acc, 2, kWave);
+        acc += __shfl_xor(acc, 4, kWave);
+        dot[g] = acc;
+      }
+      if (t < kSplitLen) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (sub == (g & 7)) sc[g][t] = rr[u] == -2 ? -INFINITY : dot[g];  // a zero row scores 0
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- per-head max and sum of exp over the split's len positions (only
+  // those scores were written); probabilities in place
+  for (int g = wave; g < G; g += kAttnWaves) {
+    float m = -INFINITY;
+    for (int t = lane; t < len; t += kWave) m = fmaxf(m, sc[g][t]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int t = lane; t < len; t += kWave) {
+      const float p = __expf(sc[g][t] - m);
+      sc[g][t] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      stat[g][0] = m;
+      stat[g][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- P.V over this wave's quarter of the positions
+  const int pr = lane / LPR, dl = lane - pr * LPR;
+  float acc[G][VW];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) acc[g][e] = 0.f;
+  constexpr int kQuarter = kSplitLen / kAttnWaves;
+  constexpr int kUnroll = 8;
+  const int tq0 = wave * kQuarter;
+  const int tq1 = min(tq0 + kQuarter, len);
+  for (int t0 = tq0; t0 < tq1; t0 += kUnroll * PP) {
+    float vv[kUnroll][VW];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int t = t0 + u * PP + pr;
+      const int r = t < tq1 ? rows[t] : -2;
+#pragma unroll
+      for (int e = 0; e < VW; ++e) vv[u][e] = r >= 0 ? load_one(vp + r * row_elems + dl * VW + e) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int t = t0 + u * PP + pr;
+      if (t < tq1) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float p = sc[g][t];
+#pragma unroll
+          for (int e = 0; e < VW; ++e) acc[g][e] = fmaf(p, vv[u][e], acc[g][e]);
+        }
+      }
+    }
+  }
+  // rows handled by different lane groups of the wave, then the waves in order
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, kWave);
+  if (pr == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) red[wave][g][dl * VW + e] = acc[g][e];
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += kAttnThreads) {
+    const int g = i / D, d = i - g * D;
+    float o = red[0][g][d];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) o += red[w][g][d];
+    float* pg = part + (static_cast<int64_t>(g) * a.n_split + s) * (D + 2);
+    pg[d] = o;
+    if (d == 0) {
+      pg[D] = stat[g][0];
+      pg[D + 1] = stat[g][1];
+    }
+  }
+}
+
+// One wave per (query head, sequence): merges the splits in order with the
+// zero rows of the gather (max_ctx - min(ctx_len, max_ctx) keys of score 0
+// and value 0) and the new token, whose K/V (RoPE applied) are k_new/v_new.
+__global__ __launch_bounds__(kWave) void attn_combine_kernel(AttnArgs a, int D, const void* __restrict__ k_new,
+                                                             const void* __restrict__ v_new, int act,
+                                                             void* __restrict__ out) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int kvh = h / (a.n_head / a.n_head_kv);
+  const int n_b = min(max(a.ctx_lens[b], 0), a.max_ctx);
+  const int n_zero = a.max_ctx - n_b;
+  const int n_used = (n_b + kSplitLen - 1) / kSplitLen;
+  const float* qh = a.q + (static_cast<int64_t>(b) * a.n_head + h) * D;
+  const int64_t kv0 = (static_cast<int64_t>(b) * a.n_head_kv + kvh) * D;
+  float dot = 0.f;
+  for (int d = lane; d < D; d += kWave) dot = fmaf(qh[d] * a.scale, load_act(k_new, act, kv0 + d), dot);
+  const float s_new = wave_sum(dot);
+  const float* part = a.part + (static_cast<int64_t>(b) * a.n_head + h) * a.n_split * (D + 2);
+  float M = s_new;
+  if (n_zero > 0) M = fmaxf(M, 0.f);
+  for (int s = 0; s < n_used; ++s) M = fmaxf(M, part[static_cast<int64_t>(s) * (D + 2) + D]);
+  const float w_new = __expf(s_new - M);
+  float l = w_new + (n_zero > 0 ? static_cast<float>(n_zero) * __expf(-M) : 0.f);
+  for (int s = 0; s < n_used; ++s) {
+    const float* ps = part + static_cast<int64_t>(s) * (D + 2);
+    l += ps[D + 1] * __expf(ps[D] - M);
+  }
+  const float inv = 1.f / l;
+  for (int d = lane; d < D; d += kWave) {
+    float o = w_new * load_act(v_new, act, kv0 + d);
+    for (int s = 0; s < n_used; ++s) {
+      const float* ps = part + static_cast<int64_t>(s) * (D + 2);
+      o = fmaf(ps[d], __expf(ps[D] - M), o);
+    }
+    store_act(out, act, (static_cast<int64_t>(b) * a.n_head + h) * D + d, o * inv);
+  }
+}
+
+template <typename T, int DL>
+hipError_t launch_split_g(const AttnArgs& a, int G, int B, hipStream_t s) {
+  const dim3 grid(a.n_split, a.n_head_kv, B);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<T, DL, 1>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<T, DL, 2>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<T, DL, 4>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attn_split_kernel<T, DL, 8>), grid, dim3(kAttnThreads), 0, s, a); break;
+    default: return hipErrorNotSupported;
+  }
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_split_d(const AttnArgs& a, int D, int G, int B, hipStream_t s) {
+  switch (D) {
+    case 16: return launch_split_g<T, 2>(a, G, B, s);
+    case 32: return launch_split_g<T, 4>(a, G, B, s);
+    case 64: return launch_split_g<T, 8>(a, G, B, s);
+    case 128: return launch_split_g<T, 16>(a, G, B, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+}  // namespace
+
+bool attn_decode_supported(int head_dim, int group) {
+  return (head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128) &&
+         (group == 1 || group == 2 || group == 4 || group == 8);
+}
+
+int attn_decode_splits(int max_ctx) { return (max_ctx + kSplitLen - 1) / kSplitLen; }
+
+hipError_t launch_attn_decode(const float* q_rot, const void* k_pool, const void* v_pool, int64_t n_blocks,
+                              int block_size, const int* tables, int max_blocks, const int* ctx_lens, int max_ctx,
+                              const void* k_new, const void* v_new, int batch, int n_head, int n_head_kv,
+                              int head_dim, int dtype, float scale, float* part, void* out, hipStream_t s) {
+  if (!attn_decode_supported(head_dim, n_head / n_head_kv) || n_head % n_head_kv) return hipErrorNotSupported;
+  if (batch == 0) return hipSuccess;
+  AttnArgs a;
+  a.q = q_rot;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.tables = tables;
+  a.ctx_lens = ctx_lens;
+  a.max_blocks = max_blocks;
+  a.max_ctx = max_ctx;
+  a.n_blocks = n_blocks;
+  a.block_size = block_size;
+  a.n_head = n_head;
+  a.n_head_kv = n_head_kv;
+  a.n_split = attn_decode_splits(max_ctx);
+  a.scale = scale;
+  a.part = part;
+  const int G = n_head / n_head_kv;
+  if (a.n_split > 0) {
+    const hipError_t e = dtype == DT_F32 ? launch_split_d<float>(a, head_dim, G, batch, s)
+                                         : launch_split_d<bf16_t>(a, head_dim, G, batch, s);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head, batch), dim3(kWave), 0, s, a, head_dim, k_new, v_new, dtype,
+                     out);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv_rope(const float* qkv, const float* bq, const float* bk, const float* bv,
+                           const int64_t* positions, int batch, int nq, int nkv, int head_dim, double freq_base,
+                           double freq_scale, float* q_rot, void* k_new, void* v_new, int act, hipStream_t s) {
+  if (batch == 0) return hipSuccess;
+  hipLaunchKernelGGL(qkv_rope_kernel, dim3(batch), dim3(256), 0, s, qkv, bq, bk, bv, positions, nq, nkv, head_dim,
+                     freq_base, freq_scale, q_rot, k_new, v_new, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_bias_cast(const float* y, const float* bias, void* out, int64_t rows, int n, int act,
+                            hipStream_t s) {
+  const int64_t total = rows * n;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(bias_cast_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, y, bias, out,
+                     rows, n, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_iota(int* v, int n, int* pair, int pair0, int pair1, hipStream_t s) {
+  const int blocks = n > 0 ? (n + 255) / 256 : 1;
+  hipLaunchKernelGGL(iota_kernel, dim3(blocks), dim3(256), 0, s, v, n, pair, pair0, pair1);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_int(int* v, int n, int value, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_int_kernel, dim3((n + 255) / 256), dim3(256), 0, s, v, n, value);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_gather(const void* cache, int64_t n_blocks, int block_size, int row_bytes, const int* tables,
+                            int max_blocks, const int* ctx_lens, int max_ctx, int batch, void* out, hipStream_t s) {
+  if (batch == 0 || max_ctx == 0 || row_bytes == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_gather_kernel, dim3(max_ctx, batch), dim3(kCopyThreads), 0, s,
+                     static_cast<const uint32_t*>(cache), n_blocks, block_size, row_bytes / 4, tables, max_blocks,
+                     ctx_lens, max_ctx, static_cast<uint32_t*>(out));
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_scatter_decode(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
+                                    const int* block_idx, const int* pos_idx, int batch, hipStream_t s) {
+  if (batch == 0 || row_bytes == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch), dim3(kCopyThreads), 0, s, static_cast<uint32_t*>(cache),
+                     n_blocks, block_size, row_bytes / 4, static_cast<const uint32_t*>(vals), block_idx, pos_idx,
+                     batch);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_scatter_prefill(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
+                                     int seq_len, const int* tables, int max_blocks, const int* start, int batch,
+                                     hipStream_t s) {
+  if (batch == 0 || seq_len == 0 || row_bytes == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_scatter_prefill_kernel, dim3(seq_len, batch), dim3(kCopyThreads), 0, s,
+                     static_cast<uint32_t*>(cache), n_blocks, block_size, row_bytes / 4,
+                     static_cast<const uint32_t*>(vals), seq_len, tables, max_blocks, start);
+  return hipGetLastError();
+}
+
+}  // namespace fmoe

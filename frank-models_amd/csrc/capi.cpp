@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -485,6 +486,152 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   return ok();
 }
 
+// ------------------------------------------------------------ attention half
+// Shapes shared by the attention entry points.
+struct AttnShape {
+  int64_t B, n_head, n_head_kv, n_embd, n_embd_kv, D;
+};
+
+int validate_attn_shape(const AttnShape& a, int act_dtype, int w_dtype) {
+  if (!act_dtype_ok(act_dtype)) return fail(FMOE_ERR_DTYPE, "activation dtype %d", act_dtype);
+  if (!w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", w_dtype);
+  if (act_dtype == FMOE_F32 && w_dtype != FMOE_F32) return fail(FMOE_ERR_DTYPE, "f32 activations need f32 weights");
+  FMOE_TRY(check_dims("batch", a.B, 0, 65535));
+  FMOE_TRY(check_dims("n_head", a.n_head, 1, 65535));
+  FMOE_TRY(check_dims("n_head_kv", a.n_head_kv, 1, a.n_head));
+  FMOE_TRY(check_dims("n_embd", a.n_embd, 1, kMaxDim));
+  FMOE_TRY(check_dims("n_embd_kv", a.n_embd_kv, 1, kMaxDim));
+  if (a.n_head % a.n_head_kv) return fail(FMOE_ERR_SHAPE, "n_head %% n_head_kv != 0");
+  if (a.n_embd % a.n_head || a.n_embd_kv % a.n_head_kv || a.n_embd / a.n_head != a.n_embd_kv / a.n_head_kv)
+    return fail(FMOE_ERR_SHAPE, "head_dim must be n_embd / n_head = n_embd_kv / n_head_kv");
+  if (!attn_decode_supported(static_cast<int>(a.D), static_cast<int>(a.n_head / a.n_head_kv)))
+    return fail(FMOE_ERR_SHAPE, "head_dim %lld with %lld query heads per KV head is not supported "
+                "(head_dim 16/32/64/128, group 1/2/4/8)", static_cast<long long>(a.D),
+                static_cast<long long>(a.n_head / a.n_head_kv));
+  if (a.n_embd + 2 * a.n_embd_kv > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_embd + 2 n_embd_kv too large");
+  return FMOE_OK;
+}
+
+struct AttnLayout {
+  size_t order, offsets, tables, lens, qkv, q_rot, k_new, v_new, part, attn, y, total;
+};
+
+AttnLayout attn_layout(const AttnShape& a, int64_t max_ctx, int act) {
+  AttnLayout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at_ = off;
+    off += align_up(bytes);
+    return at_;
+  };
+  const size_t ab = dtype_bytes(act);
+  L.order = take(static_cast<size_t>(a.B) * 4);
+  L.offsets = take(2 * 4);
+  L.tables = take(static_cast<size_t>(a.B) * 4);
+  L.lens = take(static_cast<size_t>(a.B) * 4);
+  L.qkv = take(static_cast<size_t>(a.B) * (a.n_embd + 2 * a.n_embd_kv) * 4);
+  L.q_rot = take(static_cast<size_t>(a.B) * a.n_embd * 4);
+  L.k_new = take(static_cast<size_t>(a.B) * a.n_embd_kv * ab);
+  L.v_new = take(static_cast<size_t>(a.B) * a.n_embd_kv * ab);
+  L.part = take(static_cast<size_t>(a.B) * a.n_head * attn_decode_splits(static_cast<int>(max_ctx)) * (a.D + 2) * 4);
+  L.attn = take(static_cast<size_t>(a.B) * a.n_embd * ab);
+  L.y = take(static_cast<size_t>(a.B) * a.n_embd * 4);
+  L.total = off;
+  return L;
+}
+
+// out[B, N] (out_dtype) = x[B, K] @ W for a one-expert packed weight
+// [N, K]; order/offsets hold the identity grouping of the B rows.
+int run_linear(const void* x, int64_t K, const void* packed, const float* scales, int w_dtype, int64_t N, void* out,
+               int out_dtype, int B, int act, const int* order, const int* offsets, hipStream_t s) {
+  GroupedGemmArgs g;
+  g.a = x;
+  g.lda = K;
+  g.a_mode = A_DIRECT;
+  g.order = order;
+  g.offsets = offsets;
+  g.n_tokens = B;
+  g.n_assign = B;
+  g.n_expert = 1;
+  g.w0 = packed;
+  g.s0 = w_dtype == FMOE_F8E4M3FN ? scales : nullptr;
+  g.N = N;
+  g.K = K;
+  g.out = out;
+  g.ldo = N;
+  g.epi = EPI_SCATTER;
+  g.act_dtype = act;
+  g.w_dtype = w_dtype;
+  g.w_format = packed_format(N, K, w_dtype);
+  g.out_dtype = out_dtype;
+  g.max_rows_per_expert = B;
+  // Decode batches read each weight once in the streaming kernel.
+  if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && gemm_stream_supported(g)) {
+    FMOE_HIP(launch_gemm_stream(g, s));
+    g_last_path = FMOE_PATH_STREAM;
+    return FMOE_OK;
+  }
+  return run_grouped_gemm(g, s);
+}
+
+struct AttnWeights {
+  const void* wqkv;
+  const float* wqkv_scales;
+  const void* wo;
+  const float* wo_scales;
+  int w_dtype;
+  const float *bq, *bk, *bv, *bo;
+  int use_bias;
+  float freq_base, freq_scale;
+};
+
+// Projections, RoPE, attention over the pools and the output projection
+// (attention_block_decode.mlir:96-233).  k_new / v_new: [B, n_embd_kv] in
+// act dtype (RoPE applied to k_new).
+int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, const int64_t* positions,
+                  const void* k_pool, const void* v_pool, int64_t n_blocks, int block_size, const int* tables,
+                  int max_blocks, const int* lens, int max_ctx, int act, void* out, void* k_new, void* v_new,
+                  void* workspace, const AttnLayout& L, hipStream_t s) {
+  const int B = static_cast<int>(a.B);
+  const int nq = static_cast<int>(a.n_embd), nkv = static_cast<int>(a.n_embd_kv);
+  int* order = at<int>(workspace, L.order);
+  int* offsets = at<int>(workspace, L.offsets);
+  FMOE_HIP(launch_iota(order, B, offsets, 0, B, s));
+  float* qkv = at<float>(workspace, L.qkv);
+  float* q_rot = at<float>(workspace, L.q_rot);
+  FMOE_TRY(run_linear(input, a.n_embd, w.wqkv, w.wqkv_scales, w.w_dtype, nq + 2 * nkv, qkv, FMOE_F32, B, act, order,
+                      offsets, s));
+  const bool bias = w.use_bias != 0;
+  FMOE_HIP(launch_qkv_rope(qkv, bias ? w.bq : nullptr, bias ? w.bk : nullptr, bias ? w.bv : nullptr, positions, B, nq,
+                           nkv, static_cast<int>(a.D), w.freq_base, w.freq_scale, q_rot, k_new, v_new, act, s));
+  void* attn = at<char>(workspace, L.attn);
+  const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(a.D)));
+  FMOE_HIP(launch_attn_decode(q_rot, k_pool, v_pool, n_blocks, block_size, tables, max_blocks, lens, max_ctx, k_new,
+                              v_new, B, static_cast<int>(a.n_head), static_cast<int>(a.n_head_kv),
+                              static_cast<int>(a.D), act, scale, at<float>(workspace, L.part), attn, s));
+  float* y = at<float>(workspace, L.y);
+  FMOE_TRY(run_linear(attn, a.n_embd, w.wo, w.wo_scales, w.w_dtype, nq, y, FMOE_F32, B, act, order, offsets, s));
+  FMOE_HIP(launch_bias_cast(y, bias ? w.bo : nullptr, out, B, nq, act, s));
+  return FMOE_OK;
+}
+
+int check_attn_weights(const AttnWeights& w) {
+  if (!w.wqkv || !w.wo) return fail(FMOE_ERR_INVALID_ARGUMENT, "null weight");
+  if (w.w_dtype == FMOE_F8E4M3FN && (!w.wqkv_scales || !w.wo_scales))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
+  if (w.use_bias != 0 && w.use_bias != 1) return fail(FMOE_ERR_INVALID_ARGUMENT, "use_bias must be 0 or 1");
+  if (w.use_bias && (!w.bq || !w.bk || !w.bv || !w.bo)) return fail(FMOE_ERR_INVALID_ARGUMENT, "null bias");
+  return FMOE_OK;
+}
+
+int check_pool(const char* what, int64_t n_blocks, int64_t block_size, const AttnShape& a) {
+  FMOE_TRY(check_dims(what, n_blocks, 1, kMaxDim));
+  FMOE_TRY(check_dims("block_size", block_size, 1, kMaxDim));
+  if (n_blocks * block_size > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_blocks * block_size exceeds 2^31-1");
+  (void)a;
+  return FMOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -806,6 +953,207 @@ int fmoe_moe_ffn_block_routing(void* workspace, int64_t n_tokens, int64_t n_expe
   if (weights) *weights = at<float>(workspace, L.weights);
   if (order) *order = at<int32_t>(workspace, L.perm.order);
   if (offsets) *offsets = at<int32_t>(workspace, L.perm.offsets);
+  return ok();
+}
+
+// ------------------------------------------------------------ paged KV cache
+static int kv_common(const void* cache, int dtype, int64_t n_blocks, int64_t block_size, int64_t n_head_kv,
+                     int64_t head_dim, int* row_bytes) {
+  if (!act_dtype_ok(dtype)) return fail(FMOE_ERR_DTYPE, "cache dtype %d", dtype);
+  FMOE_TRY(check_dims("n_blocks", n_blocks, 1, kMaxDim));
+  FMOE_TRY(check_dims("block_size", block_size, 1, kMaxDim));
+  FMOE_TRY(check_dims("n_head_kv", n_head_kv, 1, 65535));
+  FMOE_TRY(check_dims("head_dim", head_dim, 2, 65535));
+  if (head_dim % 2) return fail(FMOE_ERR_SHAPE, "head_dim must be even");
+  const int64_t rb = n_head_kv * head_dim * dtype_bytes(dtype);
+  if (rb > (1 << 30)) return fail(FMOE_ERR_SHAPE, "row too large");
+  if (!cache) return fail(FMOE_ERR_INVALID_ARGUMENT, "null cache");
+  if (reinterpret_cast<uintptr_t>(cache) % 4) return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned cache");
+  *row_bytes = static_cast<int>(rb);
+  return FMOE_OK;
+}
+
+int fmoe_kvcache_gather(const void* cache, int dtype, int64_t n_blocks, int64_t block_size, int64_t n_head_kv,
+                        int64_t head_dim, int64_t layer, const int32_t* block_tables, const int32_t* context_lens,
+                        int64_t n_layers, int64_t batch, int64_t max_blocks_per_seq, int64_t max_context_len,
+                        void* out, void* stream) {
+  int rb = 0;
+  FMOE_TRY(kv_common(cache, dtype, n_blocks, block_size, n_head_kv, head_dim, &rb));
+  FMOE_TRY(check_dims("n_layers", n_layers, 1, kMaxDim));
+  FMOE_TRY(check_dims("layer", layer, 0, n_layers - 1));
+  FMOE_TRY(check_dims("batch", batch, 0, 65535));
+  FMOE_TRY(check_dims("max_blocks_per_seq", max_blocks_per_seq, 1, kMaxDim));
+  FMOE_TRY(check_dims("max_context_len", max_context_len, 0, kMaxDim));
+  if (batch == 0 || max_context_len == 0) return ok();
+  if (!block_tables || !context_lens || !out) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (reinterpret_cast<uintptr_t>(out) % 4) return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned out");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_kv_gather(cache, n_blocks, static_cast<int>(block_size), rb,
+                            block_tables + layer * batch * max_blocks_per_seq, static_cast<int>(max_blocks_per_seq),
+                            context_lens + layer * batch, static_cast<int>(max_context_len), static_cast<int>(batch),
+                            out, static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int fmoe_kvcache_scatter_decode(void* cache, int dtype, int64_t n_blocks, int64_t block_size, int64_t n_head_kv,
+                                int64_t head_dim, const void* new_vals, const int32_t* block_indices,
+                                const int32_t* pos_in_blocks, int64_t batch, void* stream) {
+  int rb = 0;
+  FMOE_TRY(kv_common(cache, dtype, n_blocks, block_size, n_head_kv, head_dim, &rb));
+  FMOE_TRY(check_dims("batch", batch, 0, kMaxDim));
+  if (batch == 0) return ok();
+  if (!new_vals || !block_indices || !pos_in_blocks) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (reinterpret_cast<uintptr_t>(new_vals) % 4) return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned new_vals");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_kv_scatter_decode(cache, n_blocks, static_cast<int>(block_size), rb, new_vals, block_indices,
+                                    pos_in_blocks, static_cast<int>(batch), static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+int fmoe_kvcache_scatter_prefill(void* cache, int dtype, int64_t n_blocks, int64_t block_size, int64_t n_head_kv,
+                                 int64_t head_dim, int64_t layer, const void* new_vals, int64_t seq_len,
+                                 const int32_t* block_tables, int64_t n_layers, int64_t batch,
+                                 int64_t max_blocks_per_seq, const int32_t* start_positions, void* stream) {
+  int rb = 0;
+  FMOE_TRY(kv_common(cache, dtype, n_blocks, block_size, n_head_kv, head_dim, &rb));
+  FMOE_TRY(check_dims("n_layers", n_layers, 1, kMaxDim));
+  FMOE_TRY(check_dims("layer", layer, 0, n_layers - 1));
+  FMOE_TRY(check_dims("batch", batch, 0, 65535));
+  FMOE_TRY(check_dims("seq_len", seq_len, 0, kMaxDim));
+  FMOE_TRY(check_dims("max_blocks_per_seq", max_blocks_per_seq, 1, kMaxDim));
+  if (batch == 0 || seq_len == 0) return ok();
+  if (!new_vals || !block_tables || !start_positions) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (reinterpret_cast<uintptr_t>(new_vals) % 4) return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned new_vals");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_kv_scatter_prefill(cache, n_blocks, static_cast<int>(block_size), rb, new_vals,
+                                     static_cast<int>(seq_len), block_tables + layer * batch * max_blocks_per_seq,
+                                     static_cast<int>(max_blocks_per_seq), start_positions, static_cast<int>(batch),
+                                     static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+// ------------------------------------------------------------ dense linear weights
+int fmoe_pack_linear_weight(const void* src, int src_dtype, int64_t n_in, int64_t n_out, int64_t row_offset,
+                            int64_t n_out_total, int dst_dtype, void* dst, float* dst_scales, void* stream) {
+  if (src_dtype != FMOE_F32 && src_dtype != FMOE_BF16) return fail(FMOE_ERR_DTYPE, "source dtype %d", src_dtype);
+  if (!w_dtype_ok(dst_dtype)) return fail(FMOE_ERR_DTYPE, "packed dtype %d", dst_dtype);
+  FMOE_TRY(check_dims("n_in", n_in, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_out_total", n_out_total, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_out", n_out, 0, n_out_total));
+  FMOE_TRY(check_dims("row_offset", row_offset, 0, n_out_total - n_out));
+  if (n_out == 0 || n_in == 0) return ok();
+  if (!src || !dst) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (dst_dtype == FMOE_F8E4M3FN && !dst_scales) return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 needs dst_scales");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_pack_linear(src, src_dtype, static_cast<int>(n_in), static_cast<int>(n_out),
+                              static_cast<int>(row_offset), static_cast<int>(n_out_total), dst_dtype, dst, dst_scales,
+                              static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
+// ------------------------------------------------------------ attention_block_decode
+size_t fmoe_attention_block_decode_workspace_bytes(int64_t batch, int64_t ctx_len, int64_t n_head, int64_t n_head_kv,
+                                                   int64_t n_embd, int64_t n_embd_kv, int act_dtype) {
+  if (!act_dtype_ok(act_dtype) || batch < 0 || ctx_len < 0 || ctx_len > kMaxDim || n_head < 1 || n_head_kv < 1 ||
+      n_embd < n_head || n_embd_kv < 0)
+    return 0;
+  const AttnShape a{batch, n_head, n_head_kv, n_embd, n_embd_kv, n_embd / n_head};
+  return attn_layout(a, ctx_len, act_dtype).total;
+}
+
+int fmoe_attention_block_decode(const void* input, const int64_t* positions, const void* k_cached,
+                                const void* v_cached, int64_t ctx_len, const void* packed_wqkv,
+                                const float* wqkv_scales, const void* packed_wo, const float* wo_scales, int w_dtype,
+                                const float* bq, const float* bk, const float* bv, const float* bo, int use_bias,
+                                int64_t batch, int64_t n_head, int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv,
+                                float rope_freq_base, float rope_freq_scale, int act_dtype, void* out, void* k_new,
+                                void* v_new, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_head < 1 || n_embd < 1) return fail(FMOE_ERR_SHAPE, "n_head and n_embd must be positive");
+  const AttnShape a{batch, n_head, n_head_kv, n_embd, n_embd_kv, n_embd / n_head};
+  FMOE_TRY(validate_attn_shape(a, act_dtype, w_dtype));
+  FMOE_TRY(check_dims("ctx_len", ctx_len, 0, kMaxDim));
+  const AttnWeights w{packed_wqkv, wqkv_scales, packed_wo, wo_scales, w_dtype, bq, bk, bv, bo, use_bias,
+                      rope_freq_base, rope_freq_scale};
+  FMOE_TRY(check_attn_weights(w));
+  if (batch == 0) return ok();
+  if (!input || !positions || !out || !k_new || !v_new || !workspace)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (ctx_len > 0 && (!k_cached || !v_cached)) return fail(FMOE_ERR_INVALID_ARGUMENT, "null cached K/V");
+  if (ctx_len > 0 && (reinterpret_cast<uintptr_t>(k_cached) % 16 || reinterpret_cast<uintptr_t>(v_cached) % 16))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "cached K/V must be 16-byte aligned");
+  if (batch * ctx_len > kMaxDim) return fail(FMOE_ERR_SHAPE, "batch * ctx_len exceeds 2^31-1");
+  if (!aligned_for(input, act_dtype) || !aligned_for(out, act_dtype) || !aligned_for(k_new, act_dtype) ||
+      !aligned_for(v_new, act_dtype))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  const AttnLayout L = attn_layout(a, ctx_len, act_dtype);
+  FMOE_TRY(check_workspace(workspace, workspace_bytes, L.total));
+  FMOE_TRY(ensure_device());
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // The gathered [B, ctx, Hkv, D] tensors are a pool of B blocks of ctx rows,
+  // sequence b owning block b in full.
+  int* tables = at<int>(workspace, L.tables);
+  int* lens = at<int>(workspace, L.lens);
+  FMOE_HIP(launch_iota(tables, static_cast<int>(batch), nullptr, 0, 0, s));
+  FMOE_HIP(launch_fill_int(lens, static_cast<int>(batch), static_cast<int>(ctx_len), s));
+  FMOE_TRY(run_attention(a, w, input, positions, k_cached, v_cached, batch, static_cast<int>(ctx_len), tables, 1, lens,
+                         static_cast<int>(ctx_len), act_dtype, out, k_new, v_new, workspace, L, s));
+  return ok();
+}
+
+size_t fmoe_attention_decode_paged_workspace_bytes(int64_t batch, int64_t max_context_len, int64_t n_head,
+                                                   int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv,
+                                                   int act_dtype) {
+  return fmoe_attention_block_decode_workspace_bytes(batch, max_context_len, n_head, n_head_kv, n_embd, n_embd_kv,
+                                                     act_dtype);
+}
+
+int fmoe_attention_decode_paged(const void* input, const int64_t* positions, void* k_cache, void* v_cache,
+                                int64_t n_blocks, int64_t block_size, int64_t layer, const int32_t* block_tables,
+                                const int32_t* context_lens, int64_t n_layers, int64_t max_blocks_per_seq,
+                                int64_t max_context_len, const int32_t* block_indices, const int32_t* pos_in_blocks,
+                                const void* packed_wqkv, const float* wqkv_scales, const void* packed_wo,
+                                const float* wo_scales, int w_dtype, const float* bq, const float* bk,
+                                const float* bv, const float* bo, int use_bias, int64_t batch, int64_t n_head,
+                                int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv, float rope_freq_base,
+                                float rope_freq_scale, int act_dtype, void* out, void* k_new, void* v_new,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_head < 1 || n_embd < 1) return fail(FMOE_ERR_SHAPE, "n_head and n_embd must be positive");
+  const AttnShape a{batch, n_head, n_head_kv, n_embd, n_embd_kv, n_embd / n_head};
+  FMOE_TRY(validate_attn_shape(a, act_dtype, w_dtype));
+  FMOE_TRY(check_pool("n_blocks", n_blocks, block_size, a));
+  FMOE_TRY(check_dims("n_layers", n_layers, 1, kMaxDim));
+  FMOE_TRY(check_dims("layer", layer, 0, n_layers - 1));
+  FMOE_TRY(check_dims("max_blocks_per_seq", max_blocks_per_seq, 1, kMaxDim));
+  FMOE_TRY(check_dims("max_context_len", max_context_len, 0, kMaxDim));
+  const AttnWeights w{packed_wqkv, wqkv_scales, packed_wo, wo_scales, w_dtype, bq, bk, bv, bo, use_bias,
+                      rope_freq_base, rope_freq_scale};
+  FMOE_TRY(check_attn_weights(w));
+  if (batch == 0) return ok();
+  if (!input || !positions || !k_cache || !v_cache || !block_tables || !context_lens || !block_indices ||
+      !pos_in_blocks || !out || !workspace)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (reinterpret_cast<uintptr_t>(k_cache) % 16 || reinterpret_cast<uintptr_t>(v_cache) % 16)
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "K/V pools must be 16-byte aligned");
+  if (!aligned_for(input, act_dtype) || !aligned_for(out, act_dtype) || (k_new && !aligned_for(k_new, act_dtype)) ||
+      (v_new && !aligned_for(v_new, act_dtype)))
+    return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  const AttnLayout L = attn_layout(a, max_context_len, act_dtype);
+  FMOE_TRY(check_workspace(workspace, workspace_bytes, L.total));
+  FMOE_TRY(ensure_device());
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* kn = k_new ? k_new : at<char>(workspace, L.k_new);
+  void* vn = v_new ? v_new : at<char>(workspace, L.v_new);
+  FMOE_TRY(run_attention(a, w, input, positions, k_cache, v_cache, n_blocks, static_cast<int>(block_size),
+                         block_tables + layer * batch * max_blocks_per_seq, static_cast<int>(max_blocks_per_seq),
+                         context_lens + layer * batch, static_cast<int>(max_context_len), act_dtype, out, kn, vn,
+                         workspace, L, s));
+  // scatter_decode after the attention has read the pools
+  // (transformer_layer_moe_decode.mlir:202-206).
+  const int rb = static_cast<int>(n_embd_kv * dtype_bytes(act_dtype));
+  FMOE_HIP(launch_kv_scatter_decode(k_cache, n_blocks, static_cast<int>(block_size), rb, kn, block_indices,
+                                    pos_in_blocks, static_cast<int>(batch), s));
+  FMOE_HIP(launch_kv_scatter_decode(v_cache, n_blocks, static_cast<int>(block_size), rb, vn, block_indices,
+                                    pos_in_blocks, static_cast<int>(batch), s));
   return ok();
 }
 

@@ -171,4 +171,44 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert,
                                     hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
+// Dense src [n_in, n_part] (x @ W layout; F32 or BF16) -> rows [row0,
+// row0 + n_part) of the one-expert packed weight [n_total, n_in] (pack.hip).
+hipError_t launch_pack_linear(const void* src, int src_dtype, int n_in, int n_part, int row0, int n_total,
+                              int dst_dtype, void* dst, float* dst_scales, hipStream_t stream);
+
+// ---- decode attention (attention.hip)
+// Paged pools [n_blocks, block_size, n_head_kv, head_dim]; rows are copied
+// as 32-bit words (row_bytes a multiple of 4).  Table entries outside the
+// pool read as zero rows (gather) or skip the write (scatters).
+hipError_t launch_kv_gather(const void* cache, int64_t n_blocks, int block_size, int row_bytes, const int* tables,
+                            int max_blocks, const int* ctx_lens, int max_ctx, int batch, void* out, hipStream_t s);
+hipError_t launch_kv_scatter_decode(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
+                                    const int* block_idx, const int* pos_idx, int batch, hipStream_t s);
+hipError_t launch_kv_scatter_prefill(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
+                                     int seq_len, const int* tables, int max_blocks, const int* start, int batch,
+                                     hipStream_t s);
+// v[i] = i for i < n; pair = {pair0, pair1} when non-null.
+hipError_t launch_iota(int* v, int n, int* pair, int pair0, int pair1, hipStream_t s);
+hipError_t launch_fill_int(int* v, int n, int value, hipStream_t s);
+// qkv [B, nq + 2 nkv] fp32 -> bias (optional), RoPE on q and k:
+// q_rot fp32 [B, nq], k_new / v_new [B, nkv] in act dtype.
+hipError_t launch_qkv_rope(const float* qkv, const float* bq, const float* bk, const float* bv,
+                           const int64_t* positions, int batch, int nq, int nkv, int head_dim, double freq_base,
+                           double freq_scale, float* q_rot, void* k_new, void* v_new, int act, hipStream_t s);
+// out[r, :] = y[r, :] (+ bias) in act dtype.
+hipError_t launch_bias_cast(const float* y, const float* bias, void* out, int64_t rows, int n, int act,
+                            hipStream_t s);
+// Head sizes and query-per-KV-head groups the attention kernels take.
+bool attn_decode_supported(int head_dim, int group);
+// Context splits of the attention (part holds batch * n_head * splits *
+// (head_dim + 2) floats).
+int attn_decode_splits(int max_ctx);
+// One new token per sequence against max_ctx positions of the paged pools
+// (zero rows at and past ctx_lens[b]) and its own k_new / v_new; out
+// [B, n_head * head_dim] in dtype (the pools' and k_new / v_new's dtype).
+hipError_t launch_attn_decode(const float* q_rot, const void* k_pool, const void* v_pool, int64_t n_blocks,
+                              int block_size, const int* tables, int max_blocks, const int* ctx_lens, int max_ctx,
+                              const void* k_new, const void* v_new, int batch, int n_head, int n_head_kv,
+                              int head_dim, int dtype, float scale, float* part, void* out, hipStream_t s);
+
 }  // namespace fmoe

@@ -80,7 +80,51 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__
   }
 }
 
+// Dense linear weight src [n_in, n_part] row-major (the reference's
+// `x @ W` operand, attention_block_decode.mlir:104-118) -> rows
+// [row0, row0 + n_part) of a one-expert packed [n_total, n_in] weight.  One
+// block per output row: a strided column read (one-time packing).
+__global__ __launch_bounds__(kThreads) void pack_linear_kernel(const void* __restrict__ src, int src_dt, int n_in,
+                                                               int n_part, int row0, int n_total, int dst_dt,
+                                                               void* __restrict__ dst, float* __restrict__ dst_scales) {
+  __shared__ float red[kThreads / kWave];
+  const int o = blockIdx.x;
+  const int og = row0 + o;
+  const int fmt = packed_format(n_total, n_in, dst_dt);
+  float scale = 1.f;
+  if (dst_dt == DT_F8) {
+    float m = 0.f;
+    for (int i = threadIdx.x; i < n_in; i += kThreads)
+      m = fmaxf(m, fabsf(load_src(src, src_dt, static_cast<int64_t>(i) * n_part + o)));
+    m = wave_max(m);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = m;
+    __syncthreads();
+    m = red[0];
+    for (int w = 1; w < kThreads / kWave; ++w) m = fmaxf(m, red[w]);
+    scale = m > 0.f ? m / 448.0f : 1.0f;
+    if (threadIdx.x == 0) dst_scales[og] = scale;
+  }
+  for (int i = threadIdx.x; i < n_in; i += kThreads) {
+    const float v = load_src(src, src_dt, static_cast<int64_t>(i) * n_part + o);
+    const int64_t d = packed_offset(fmt, dst_dt, 0, og, i, n_total, n_in);
+    if (dst_dt == DT_F8)
+      static_cast<f8_t*>(dst)[d] = static_cast<f8_t>(f32_to_e4m3fn(v / scale));
+    else if (dst_dt == DT_F32)
+      static_cast<float*>(dst)[d] = v;
+    else
+      static_cast<bf16_t*>(dst)[d] = f32_to_bf16(v);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_pack_linear(const void* src, int src_dtype, int n_in, int n_part, int row0, int n_total,
+                              int dst_dtype, void* dst, float* dst_scales, hipStream_t stream) {
+  if (n_part == 0 || n_in == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_linear_kernel, dim3(n_part), dim3(kThreads), 0, stream, src, src_dtype, n_in, n_part, row0,
+                     n_total, dst_dtype, dst, dst_scales);
+  return hipGetLastError();
+}
 
 hipError_t launch_pack(const void* src, int src_dtype, const float* src_scales, int n_out,
                        int n_in, int n_expert, int dst_dtype, void* dst, float* dst_scales,

@@ -239,6 +239,108 @@ int fmoe_moe_ffn_block_routing(void *workspace, int64_t n_tokens, int64_t n_expe
                                int act_dtype, int w_dtype, int32_t **ids,
                                float **weights, int32_t **order, int32_t **offsets);
 
+/* ---------------------------------------------------------------------- */
+/* The decode step's attention half (the next component after the MoE FFN
+ * block on the decode path, architectures/llm/transformer_layer_moe_decode.mlir:180-209).
+ *
+ * Paged KV cache.  Replaces @kvcache_components.gather / scatter_decode
+ * (components/kvcache/kvcache.mlir; oracles/kvcache.py:51-185) and the
+ * oracle-only scatter_prefill (oracles/kvcache.py:142-185).
+ *   cache: one pool [n_blocks, block_size, n_head_kv, head_dim] in dtype
+ *          (F32 or BF16), 4-byte aligned, updated in place by the scatters
+ *   block_tables [n_layers, batch, max_blocks_per_seq] int32,
+ *   context_lens [n_layers, batch] int32 (device)
+ *   gather out [batch, max_context_len, n_head_kv, head_dim]: rows at and past
+ *          min(context_lens[layer, b], max_context_len) are zero
+ *   scatter_decode: new_vals [batch, n_head_kv, head_dim] (cache dtype) to
+ *          (block_indices[b], pos_in_blocks[b]); when several b name one
+ *          slot the last b wins (the reference's sequential loop)
+ *   scatter_prefill: new_vals [batch, seq_len, n_head_kv, head_dim] to
+ *          positions start_positions[b] + s through the layer's block table.
+ * Table entries or indices outside the pool read as zero rows (gather) or
+ * skip the write (scatters): the reference would index out of bounds. */
+int fmoe_kvcache_gather(const void *cache, int dtype, int64_t n_blocks, int64_t block_size,
+                        int64_t n_head_kv, int64_t head_dim, int64_t layer,
+                        const int32_t *block_tables, const int32_t *context_lens,
+                        int64_t n_layers, int64_t batch, int64_t max_blocks_per_seq,
+                        int64_t max_context_len, void *out, void *stream);
+int fmoe_kvcache_scatter_decode(void *cache, int dtype, int64_t n_blocks, int64_t block_size,
+                                int64_t n_head_kv, int64_t head_dim, const void *new_vals,
+                                const int32_t *block_indices, const int32_t *pos_in_blocks,
+                                int64_t batch, void *stream);
+int fmoe_kvcache_scatter_prefill(void *cache, int dtype, int64_t n_blocks, int64_t block_size,
+                                 int64_t n_head_kv, int64_t head_dim, int64_t layer,
+                                 const void *new_vals, int64_t seq_len,
+                                 const int32_t *block_tables, int64_t n_layers, int64_t batch,
+                                 int64_t max_blocks_per_seq, const int32_t *start_positions,
+                                 void *stream);
+
+/* Dense projection weight in the reference's `x @ W` layout, src [n_in, n_out]
+ * row-major (F32 or BF16; attention_block_decode.mlir:104-118), packed into
+ * rows [row_offset, row_offset + n_out) of a one-expert packed weight
+ * [n_out_total, n_in] of fmoe_packed_weight_bytes(n_out_total, n_in, 1,
+ * dst_dtype) bytes (dst_scales [n_out_total] for F8E4M3FN, quantised per
+ * output channel as fmoe_pack_expert_weights does).  The attention entry
+ * points take wq | wk | wv packed as one [n_embd + 2 n_embd_kv, n_embd]
+ * weight (row offsets 0, n_embd, n_embd + n_embd_kv) and wo as [n_embd, n_embd]. */
+int fmoe_pack_linear_weight(const void *src, int src_dtype, int64_t n_in, int64_t n_out,
+                            int64_t row_offset, int64_t n_out_total, int dst_dtype, void *dst,
+                            float *dst_scales, void *stream);
+
+/* Decode attention block.  Replaces
+ * @attention_block_decode_components.attention_block_decode
+ * (components/attention/attention_block_decode.mlir:52-244; oracles/attention.py
+ * attention_block + attention_gqa:8-52; RoPE components/position/rope.mlir:22-110):
+ *   input [batch, n_embd], positions [batch] int64,
+ *   k_cached / v_cached [batch, ctx_len, n_head_kv, head_dim] (act dtype,
+ *   16-byte aligned), packed_wqkv / packed_wo (+ fp8 scales) as above,
+ *   biases bq [n_embd], bk, bv [n_embd_kv], bo [n_embd] float32 (read only
+ *   when use_bias = 1), head_dim = n_embd / n_head = n_embd_kv / n_head_kv
+ *   in {16, 32, 64, 128}, n_head / n_head_kv in {1, 2, 4, 8}.
+ *   out [batch, n_embd], k_new / v_new [batch, n_head_kv, head_dim] (RoPE
+ *   applied to k_new), all in act_dtype.
+ * The new token attends to the ctx_len cached positions and itself, scale
+ * 1/sqrt(head_dim), no mask (attention_gqa.mlir:120-137). */
+size_t fmoe_attention_block_decode_workspace_bytes(int64_t batch, int64_t ctx_len, int64_t n_head,
+                                                   int64_t n_head_kv, int64_t n_embd,
+                                                   int64_t n_embd_kv, int act_dtype);
+int fmoe_attention_block_decode(const void *input, const int64_t *positions,
+                                const void *k_cached, const void *v_cached, int64_t ctx_len,
+                                const void *packed_wqkv, const float *wqkv_scales,
+                                const void *packed_wo, const float *wo_scales, int w_dtype,
+                                const float *bq, const float *bk, const float *bv,
+                                const float *bo, int use_bias, int64_t batch, int64_t n_head,
+                                int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv,
+                                float rope_freq_base, float rope_freq_scale, int act_dtype,
+                                void *out, void *k_new, void *v_new, void *workspace,
+                                size_t workspace_bytes, void *stream);
+
+/* The decode layer's attention sequence on the paged cache: gather of
+ * max_context_len positions + attention_block_decode + scatter_decode of the
+ * new K/V (architectures/llm/transformer_layer_moe_decode.mlir:180-209), with
+ * the cache read in place instead of gathered.  Pools in act_dtype, 16-byte
+ * aligned; k_new / v_new may be null (the scatter still runs).  As in the
+ * reference, positions in [min(context_lens, max_context_len),
+ * max_context_len) enter the softmax as zero keys and values. */
+size_t fmoe_attention_decode_paged_workspace_bytes(int64_t batch, int64_t max_context_len,
+                                                   int64_t n_head, int64_t n_head_kv,
+                                                   int64_t n_embd, int64_t n_embd_kv,
+                                                   int act_dtype);
+int fmoe_attention_decode_paged(const void *input, const int64_t *positions, void *k_cache,
+                                void *v_cache, int64_t n_blocks, int64_t block_size,
+                                int64_t layer, const int32_t *block_tables,
+                                const int32_t *context_lens, int64_t n_layers,
+                                int64_t max_blocks_per_seq, int64_t max_context_len,
+                                const int32_t *block_indices, const int32_t *pos_in_blocks,
+                                const void *packed_wqkv, const float *wqkv_scales,
+                                const void *packed_wo, const float *wo_scales, int w_dtype,
+                                const float *bq, const float *bk, const float *bv,
+                                const float *bo, int use_bias, int64_t batch, int64_t n_head,
+                                int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv,
+                                float rope_freq_base, float rope_freq_scale, int act_dtype,
+                                void *out, void *k_new, void *v_new, void *workspace,
+                                size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
