@@ -23,6 +23,9 @@ The JSON line carries:
                         touched experts' weights + activations / time / 8 TB/s)
   cpu_baseline          the oracle's expert-grouped NumPy restatement (oracle/)
                         timed on this host on a bounded token sample
+  attention_decode      the decode step's attention half at Mixtral's attention
+                        shape (16 sequences x 4096 cached positions, paged
+                        bf16 KV): ms/step, per-phase times, KV-read GB/s
 """
 
 from __future__ import annotations
@@ -186,6 +189,70 @@ def all_configs(fm, wl, torch, args):
     return rows
 
 
+def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16):
+    """The decode step's attention half at Mixtral-8x7B's attention shape
+    (n_embd 4096, 32 query heads, 8 KV heads, head_dim 128), bf16: one new
+    token per sequence for `batch` sequences, each with `ctx` cached
+    positions in a paged pool (block_size rows per block, blocks shuffled),
+    through AttentionBlockDecode.paged (projections, RoPE, attention read
+    in place, output projection, scatter of the new K/V)."""
+    n_embd, H, Hkv = 4096, 32, 8
+    D = n_embd // H
+    nkv = Hkv * D
+    g = torch.Generator(device="cuda").manual_seed(7)
+    bf = torch.bfloat16
+    rnd = lambda *s, scale=1.0: (torch.randn(*s, generator=g, device="cuda") * scale).to(bf)
+    per_seq = (ctx + 1 + block_size - 1) // block_size
+    n_blocks = batch * per_seq
+    kp = rnd(n_blocks, block_size, Hkv, D)
+    vp = rnd(n_blocks, block_size, Hkv, D)
+    perm = torch.randperm(n_blocks, generator=g, device="cuda").to(torch.int32)
+    tables = perm.view(1, batch, per_seq).contiguous()
+    lens = torch.full((1, batch), ctx, dtype=torch.int32, device="cuda")
+    bi = tables[0, :, ctx // block_size].contiguous()
+    pi = torch.full((batch,), ctx % block_size, dtype=torch.int32, device="cuda")
+    s = n_embd ** -0.5
+    blk = fm.AttentionBlockDecode(rnd(n_embd, n_embd, scale=s), rnd(n_embd, nkv, scale=s), rnd(n_embd, nkv, scale=s),
+                                  rnd(n_embd, n_embd, scale=s), n_head=H, n_head_kv=Hkv, n_embd=n_embd, act_dtype=bf)
+    x = rnd(batch, n_embd)
+    pos = torch.full((batch,), ctx, dtype=torch.int64, device="cuda")
+
+    def step():
+        blk.paged(x, pos, kp, vp, 0, tables, lens, ctx, bi, pi)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    ll = fm.lowlevel
+    ll.timing_read()
+    ll.timing_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kern = {k: v[0] / v[1] for k, v in ll.timing_read().items() if v[1]}
+    ll.timing_enable(False)
+    kv_bytes = 2.0 * batch * ctx * nkv * 2
+    qkv_bytes = n_embd * (n_embd + 2 * nkv) * 2.0
+    out_bytes = n_embd * n_embd * 2.0
+    res = {"workload": "Mixtral-8x7B attention (4096, 32 heads, 8 KV heads, head_dim 128), bf16, paged block 16",
+           "batch": batch, "context": ctx, "ms_per_step": ms, "tokens_per_s": batch / (ms * 1e-3),
+           "kernels_ms": kern, "kv_bytes": kv_bytes, "qkv_weight_bytes": qkv_bytes, "out_weight_bytes": out_bytes,
+           "step_hbm_frac": (kv_bytes + qkv_bytes + out_bytes) / (ms * 1e-3) / PEAK_HBM_BYTES}
+    if kern.get("attention"):
+        res["attention_GBps"] = kv_bytes / (kern["attention"] * 1e-3) / 1e9
+        res["attention_hbm_frac"] = res["attention_GBps"] * 1e9 / PEAK_HBM_BYTES
+    if kern.get("qkv"):
+        res["qkv_GBps"] = qkv_bytes / (kern["qkv"] * 1e-3) / 1e9
+    if kern.get("out_proj"):
+        res["out_proj_GBps"] = out_bytes / (kern["out_proj"] * 1e-3) / 1e9
+    return res
+
+
 def read_traffic(kernel_name):
     """HBM bytes per launch of `kernel_name` from a committed rocprofv3 PMC
     summary (profiles/pmc_<name>.json), or None."""
@@ -208,6 +275,11 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--attn-batch", type=int, default=16)
+    ap.add_argument("--attn-context", type=int, default=4096)
+    ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="time only the decode attention half (its own JSON line)")
     ap.add_argument("--all-configs", action="store_true",
                     help="also time C3/C4/C5 at every token count (table on stderr, 'configs' in the JSON)")
     args = ap.parse_args()
@@ -222,6 +294,13 @@ def main():
 
     fm = importlib.import_module("frank-models_amd")
     wl = importlib.import_module("frank-models_amd.workloads")
+    if args.attention_only:
+        att = attention_decode(fm, torch, args.attn_batch, args.attn_context, max(args.steps, 20), args.warmup)
+        log(f"attention decode {att['ms_per_step']:.3f} ms/step, kernels(ms) {att['kernels_ms']}")
+        print(json.dumps({"metric": "decode attention tokens/s (paged KV, Mixtral attention shape)",
+                          "value": att["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "dtype": "bf16",
+                          "data": "synthetic", "higher_is_better": True, "attention_decode": att}), flush=True)
+        return
     cfg = wl.CONFIGS["C2"]
     H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
 
@@ -275,6 +354,13 @@ def main():
             "kernels_ms": dec["kernels"],
         }
         log(f"decode {dec['ms']:.3f} ms/step, {result['decode']['hbm_frac']:.3f} of HBM peak")
+
+    if not args.no_attention:
+        log(f"attention decode: batch {args.attn_batch}, context {args.attn_context}")
+        result["attention_decode"] = attention_decode(fm, torch, args.attn_batch, args.attn_context,
+                                                      max(args.steps, 20), args.warmup)
+        log(f"attention decode {result['attention_decode']['ms_per_step']:.3f} ms/step, "
+            f"kernels(ms) {result['attention_decode']['kernels_ms']}")
 
     if args.all_configs:
         result["configs"] = all_configs(fm, wl, torch, args)

@@ -42,7 +42,7 @@ PATH_TILED_LARGE = 4
 
 
 # fmoe_timer
-TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id", "norm")
+TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id", "norm", "qkv", "attention", "out_proj")
 
 
 class FmoeError(RuntimeError):

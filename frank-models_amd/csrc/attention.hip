@@ -110,54 +110,65 @@ __device__ __forceinline__ void store_act(void* p, int dt, int64_t i, float v) {
 // (pairs (2i, 2i+1), angle pos * freq_scale / freq_base^(2i/D), in double
 // precision like the reference oracle), q_rot fp32 [B, nq], k_new / v_new
 // [B, nkv] in act dtype (rope.mlir:38-104, oracles/position.py:6-50).
-__global__ __launch_bounds__(256) void qkv_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ bq,
-                                                       const float* __restrict__ bk, const float* __restrict__ bv,
+__device__ __forceinline__ float split_sum(const float* p, int nsplit, int64_t stride) {
+  float v = p[0];
+  for (int k = 1; k < nsplit; ++k) v += p[k * stride];
+  return v;
+}
+
+__global__ __launch_bounds__(256) void qkv_rope_kernel(const float* __restrict__ qkv, int nsplit, int64_t split_stride,
+                                                       const float* __restrict__ bq, const float* __restrict__ bk,
+                                                       const float* __restrict__ bv,
                                                        const int64_t* __restrict__ positions, int nq, int nkv, int D,
                                                        double freq_base, double freq_scale, float* __restrict__ q_rot,
                                                        void* __restrict__ k_new, void* __restrict__ v_new, int act) {
+  // grid (batch, items / 256): an item is a RoPE pair of the q or k part or
+  // one element of the v part
   const int b = blockIdx.x;
+  const int i = blockIdx.y * blockDim.x + threadIdx.x;
+  const int pairs = (nq + nkv) / 2;
+  if (i >= pairs + nkv) return;
   const int width = nq + 2 * nkv;
   const float* row = qkv + static_cast<int64_t>(b) * width;
-  const double pos = static_cast<double>(positions[b]);
-  const int pairs = (nq + nkv) / 2;
-  for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
-    const int col = 2 * i;
-    const bool is_q = col < nq;
-    const int c = is_q ? col : col - nq;
-    const float* bias = is_q ? bq : bk;
-    float x0 = row[col], x1 = row[col + 1];
-    if (bias) {
-      x0 += bias[c];
-      x1 += bias[c + 1];
-    }
-    const int pi = (c % D) / 2;
-    const double freq = freq_scale / pow(freq_base, static_cast<double>(2 * pi) / D);
-    double sn, cs;
-    sincos(pos * freq, &sn, &cs);
-    const float cf = static_cast<float>(cs), sf = static_cast<float>(sn);
-    const float y0 = x0 * cf - x1 * sf;
-    const float y1 = x0 * sf + x1 * cf;
-    if (is_q) {
-      q_rot[static_cast<int64_t>(b) * nq + c] = y0;
-      q_rot[static_cast<int64_t>(b) * nq + c + 1] = y1;
-    } else {
-      store_act(k_new, act, static_cast<int64_t>(b) * nkv + c, y0);
-      store_act(k_new, act, static_cast<int64_t>(b) * nkv + c + 1, y1);
-    }
-  }
-  for (int c = threadIdx.x; c < nkv; c += blockDim.x) {
-    float v = row[nq + nkv + c];
+  if (i >= pairs) {
+    const int c = i - pairs;
+    float v = split_sum(row + nq + nkv + c, nsplit, split_stride);
     if (bv) v += bv[c];
     store_act(v_new, act, static_cast<int64_t>(b) * nkv + c, v);
+    return;
+  }
+  const int col = 2 * i;
+  const bool is_q = col < nq;
+  const int c = is_q ? col : col - nq;
+  const float* bias = is_q ? bq : bk;
+  float x0 = split_sum(row + col, nsplit, split_stride), x1 = split_sum(row + col + 1, nsplit, split_stride);
+  if (bias) {
+    x0 += bias[c];
+    x1 += bias[c + 1];
+  }
+  const int pi = (c % D) / 2;
+  const double freq = freq_scale / pow(freq_base, static_cast<double>(2 * pi) / D);
+  double sn, cs;
+  sincos(static_cast<double>(positions[b]) * freq, &sn, &cs);
+  const float cf = static_cast<float>(cs), sf = static_cast<float>(sn);
+  const float y0 = x0 * cf - x1 * sf;
+  const float y1 = x0 * sf + x1 * cf;
+  if (is_q) {
+    q_rot[static_cast<int64_t>(b) * nq + c] = y0;
+    q_rot[static_cast<int64_t>(b) * nq + c + 1] = y1;
+  } else {
+    store_act(k_new, act, static_cast<int64_t>(b) * nkv + c, y0);
+    store_act(k_new, act, static_cast<int64_t>(b) * nkv + c + 1, y1);
   }
 }
 
 // out[b, n] = y[b, n] (+ bias[n]) in act dtype.
-__global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict__ y, const float* __restrict__ bias,
-                                                        void* __restrict__ out, int64_t rows, int n, int act) {
+__global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict__ y, int nsplit, int64_t split_stride,
+                                                        const float* __restrict__ bias, void* __restrict__ out,
+                                                        int64_t rows, int n, int act) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= rows * n) return;
-  float v = y[i];
+  float v = split_sum(y + i, nsplit, split_stride);
   if (bias) v += bias[i % n];
   store_act(out, act, i, v);
 }
@@ -218,23 +229,33 @@ struct AttnArgs {
 };
 
 constexpr int kSplitLen = 256;
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 256;  // one thread per position of a split (rows[] fill)
+static_assert(kAttnThreads == kSplitLen, "the rows[] fill gives each thread one position");
 constexpr int kAttnWaves = kAttnThreads / kWave;
 
-// Block (split s, KV head, sequence b).  Scores: 8 lanes per position, each
-// lane holding DL of the D = 8 DL dimensions in chunks of CW elements, so
-// the 8 lanes of a position read each 128 B span of the row together; the
-// G query heads of the KV head are scored from one read of K.  Probabilities
-// stay in LDS; P.V: a wave takes a quarter of the split's positions, lanes
-// spread over the row (PP rows at once when D < 64).
+// Block (split s, KV head, sequence b); wave w owns the split's positions
+// [64 w, 64 w + 64) in both phases, so a wave's memory traffic is two
+// rounds of independent loads: all of its K rows, then (issued before the
+// block-wide softmax, so that their latency overlaps it) all of its V rows.
+// Scores: 8 lanes per position, each lane holding DL = D/8 dimensions in
+// 16-byte chunks spread so that the 8 lanes of a position read each 128 B
+// span of the row together; the G query heads of the KV head are scored
+// from one read of K.  P.V: LPR lanes per row, 16 bytes each.
 template <typename T, int DL, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
   constexpr int D = 8 * DL;
-  constexpr int CW = (sizeof(T) == 4 ? 4 : 8) < DL ? (sizeof(T) == 4 ? 4 : 8) : DL;  // elements per 16 B (or less)
-  constexpr int NC = DL / CW;
-  constexpr int VW = D >= kWave ? D / kWave : 1;       // P.V elements per lane per row
-  constexpr int LPR = D / VW;                          // lanes per row in P.V
-  constexpr int PP = kWave / LPR;                      // rows per wave step in P.V
+  constexpr int EPV = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
+  constexpr int CW = EPV < DL ? EPV : DL;                 // score chunk (elements)
+  constexpr int NC = DL / CW;                             // score chunks per lane per position
+  constexpr int kQ = kSplitLen / kAttnWaves;              // positions per wave
+  constexpr int kSteps = kQ / 8;                          // score steps of 8 positions
+  constexpr int SR = 16 / NC < kSteps ? 16 / NC : kSteps;  // steps per load round (<= 16 loads)
+  constexpr int VC = EPV;                                 // P.V elements per lane per row
+  constexpr int LPR = D / VC;                             // lanes per row
+  constexpr int PP = kWave / LPR;                         // rows per load instruction
+  constexpr int NV = kQ / PP;                             // V load instructions per wave
+  constexpr int VR = NV < 16 ? NV : 16;                   // per round
+  static_assert(kSteps % SR == 0 && NV % VR == 0, "rounds must tile the wave's positions");
   __shared__ float sc[G][kSplitLen];
   __shared__ int rows[kSplitLen];
   __shared__ float red[kAttnWaves][G][D];
@@ -254,8 +275,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
     return;
   }
   const int64_t row_elems = static_cast<int64_t>(a.n_head_kv) * D;
-  for (int t = tid; t < kSplitLen; t += kAttnThreads) {
-    int r = -2;  // -2: past the split's positions; -1: table entry out of range (a zero row)
+  {
+    const int t = tid;  // kAttnThreads == kSplitLen: one position per thread
+    int r = -2;         // -2: past the split's positions; -1: table entry outside the pool (a zero row)
     if (t < len) {
       const int j = j0 + t;
       const int lb = j / a.block_size;
@@ -277,50 +299,70 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
         q[g][c * CW + e] =
             a.q[(static_cast<int64_t>(b) * a.n_head + kvh * G + g) * D + c * 8 * CW + sub * CW + e] * a.scale;
   __syncthreads();
+  const int tw = wave * kQ;  // this wave's first position
 
-  // ---- scores: 32 positions per block step, two steps' rows in flight
-  constexpr int kStep = kAttnWaves * 8;
-  for (int t0 = 0; t0 < len; t0 += 2 * kStep) {
-    float kv[2][DL];
-    int rr[2];
+  // ---- scores, SR steps of 8 positions per round of loads; K stays in its
+  // storage format (CWW 32-bit words per chunk) until it is used
+  constexpr int CWW = CW * static_cast<int>(sizeof(T)) / 4;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int t = t0 + u * kStep + wave * 8 + pi;
-      rr[u] = t < kSplitLen ? rows[t] : -2;
+  for (int r0 = 0; r0 < kSteps; r0 += SR) {
+    uint32_t kr[SR][NC][CWW];
+    int rr[SR];
+#pragma unroll
+    for (int u = 0; u < SR; ++u) {
+      rr[u] = rows[tw + (r0 + u) * 8 + pi];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        float v[CW];
-        if (rr[u] >= 0) {
-          load_chunk<T, CW>(kp + rr[u] * row_elems + c * 8 * CW + sub * CW, v);
+        const T* src = kp + rr[u] * row_elems + c * 8 * CW + sub * CW;
+        if (CWW == 4) {
+          const u32x4_t w = rr[u] >= 0 ? *reinterpret_cast<const u32x4_t*>(src) : u32x4_t{0u, 0u, 0u, 0u};
+          kr[u][c][0] = w[0], kr[u][c][1 % CWW] = w[1], kr[u][c][2 % CWW] = w[2], kr[u][c][3 % CWW] = w[3];
+        } else if (CWW == 2) {
+          const u32x2_t w = rr[u] >= 0 ? *reinterpret_cast<const u32x2_t*>(src) : u32x2_t{0u, 0u};
+          kr[u][c][0] = w[0], kr[u][c][1 % CWW] = w[1];
         } else {
-#pragma unroll
-          for (int e = 0; e < CW; ++e) v[e] = 0.f;
+          kr[u][c][0] = rr[u] >= 0 ? *reinterpret_cast<const uint32_t*>(src) : 0u;
         }
-#pragma unroll
-        for (int e = 0; e < CW; ++e) kv[u][c * CW + e] = v[e];
       }
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int t = t0 + u * kStep + wave * 8 + pi;
-      float dot[G];
+    for (int u = 0; u < SR; ++u) {
+      const int t = tw + (r0 + u) * 8 + pi;
+      float kv[DL];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        if (sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < CW; ++e) kv[c * CW + e] = __uint_as_float(kr[u][c][e % CWW]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < CWW; ++e) unpack2(kr[u][c][e], kv + c * CW + 2 * e);
+        }
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) acc = fmaf(q[g][i], kv[u][i], acc);
+        for (int i = 0; i < DL; ++i) acc = fmaf(q[g][i], kv[i], acc);
         acc += __shfl_xor(acc, 1, kWave);
         acc += __shfl_xor(acc, 2, kWave);
         acc += __shfl_xor(acc, 4, kWave);
-        dot[g] = acc;
-      }
-      if (t < kSplitLen) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          if (sub == (g & 7)) sc[g][t] = rr[u] == -2 ? -INFINITY : dot[g];  // a zero row scores 0
+        if (sub == (g & 7)) sc[g][t] = rr[u] == -2 ? -INFINITY : acc;  // a zero row scores 0
       }
     }
   }
+
+  // ---- V rows of this wave, first round issued before the softmax
+  const int pr = lane / LPR, dl = lane - pr * LPR;
+  u32x4_t vraw[VR];
+  auto load_v = [&](int i0) {
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      const int r = rows[tw + (i0 + i) * PP + pr];
+      vraw[i] = r >= 0 ? *reinterpret_cast<const u32x4_t*>(vp + r * row_elems + dl * VC) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  load_v(0);
   __syncthreads();
 
   // ---- per-head max and sum of exp over the split's len positions (only
@@ -343,35 +385,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- P.V over this wave's quarter of the positions
-  const int pr = lane / LPR, dl = lane - pr * LPR;
-  float acc[G][VW];
+  // ---- P.V over this wave's positions
+  float acc[G][VC];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int e = 0; e < VW; ++e) acc[g][e] = 0.f;
-  constexpr int kQuarter = kSplitLen / kAttnWaves;
-  constexpr int kUnroll = 8;
-  const int tq0 = wave * kQuarter;
-  const int tq1 = min(tq0 + kQuarter, len);
-  for (int t0 = tq0; t0 < tq1; t0 += kUnroll * PP) {
-    float vv[kUnroll][VW];
+    for (int e = 0; e < VC; ++e) acc[g][e] = 0.f;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int t = t0 + u * PP + pr;
-      const int r = t < tq1 ? rows[t] : -2;
+  for (int i0 = 0; i0 < NV; i0 += VR) {
+    if (i0 > 0) load_v(i0);
 #pragma unroll
-      for (int e = 0; e < VW; ++e) vv[u][e] = r >= 0 ? load_one(vp + r * row_elems + dl * VW + e) : 0.f;
-    }
+    for (int i = 0; i < VR; ++i) {
+      const int t = tw + (i0 + i) * PP + pr;
+      if (t < len) {
+        float v[VC];
+        if (sizeof(T) == 4) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int t = t0 + u * PP + pr;
-      if (t < tq1) {
+          for (int e = 0; e < VC; ++e) v[e] = __uint_as_float(vraw[i][e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < VC / 2; ++e) unpack2(vraw[i][e], v + 2 * e);
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float p = sc[g][t];
 #pragma unroll
-          for (int e = 0; e < VW; ++e) acc[g][e] = fmaf(p, vv[u][e], acc[g][e]);
+          for (int e = 0; e < VC; ++e) acc[g][e] = fmaf(p, v[e], acc[g][e]);
         }
       }
     }
@@ -382,12 +421,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < VW; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, kWave);
+      for (int e = 0; e < VC; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, kWave);
   if (pr == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < VW; ++e) red[wave][g][dl * VW + e] = acc[g][e];
+      for (int e = 0; e < VC; ++e) red[wave][g][dl * VC + e] = acc[g][e];
   }
   __syncthreads();
   for (int i = tid; i < G * D; i += kAttnThreads) {
@@ -404,42 +443,72 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
   }
 }
 
-// One wave per (query head, sequence): merges the splits in order with the
+// One block per (query head, sequence) merges the context splits with the
 // zero rows of the gather (max_ctx - min(ctx_len, max_ctx) keys of score 0
 // and value 0) and the new token, whose K/V (RoPE applied) are k_new/v_new.
-__global__ __launch_bounds__(kWave) void attn_combine_kernel(AttnArgs a, int D, const void* __restrict__ k_new,
-                                                             const void* __restrict__ v_new, int act,
-                                                             void* __restrict__ out) {
+// Wave 0 reduces the per-split statistics with one split per lane and
+// leaves the split weights exp(m_s - M) in LDS; then thread d adds
+// dimension d over the splits, kCombineUnroll loads at a time.
+constexpr int kCombineThreads = 128;  // >= head_dim
+constexpr int kCombineChunk = 1024;   // splits whose weights are held in LDS at once
+constexpr int kCombineUnroll = 8;
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a, int D,
+                                                                       const void* __restrict__ k_new,
+                                                                       const void* __restrict__ v_new, int act,
+                                                                       void* __restrict__ out) {
+  __shared__ float wts[kCombineChunk];
+  __shared__ float stat[3];  // M, 1 / l, exp(s_new - M) / l
   const int h = blockIdx.x, b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int kvh = h / (a.n_head / a.n_head_kv);
   const int n_b = min(max(a.ctx_lens[b], 0), a.max_ctx);
   const int n_zero = a.max_ctx - n_b;
   const int n_used = (n_b + kSplitLen - 1) / kSplitLen;
   const float* qh = a.q + (static_cast<int64_t>(b) * a.n_head + h) * D;
   const int64_t kv0 = (static_cast<int64_t>(b) * a.n_head_kv + kvh) * D;
-  float dot = 0.f;
-  for (int d = lane; d < D; d += kWave) dot = fmaf(qh[d] * a.scale, load_act(k_new, act, kv0 + d), dot);
-  const float s_new = wave_sum(dot);
   const float* part = a.part + (static_cast<int64_t>(b) * a.n_head + h) * a.n_split * (D + 2);
-  float M = s_new;
-  if (n_zero > 0) M = fmaxf(M, 0.f);
-  for (int s = 0; s < n_used; ++s) M = fmaxf(M, part[static_cast<int64_t>(s) * (D + 2) + D]);
-  const float w_new = __expf(s_new - M);
-  float l = w_new + (n_zero > 0 ? static_cast<float>(n_zero) * __expf(-M) : 0.f);
-  for (int s = 0; s < n_used; ++s) {
-    const float* ps = part + static_cast<int64_t>(s) * (D + 2);
-    l += ps[D + 1] * __expf(ps[D] - M);
-  }
-  const float inv = 1.f / l;
-  for (int d = lane; d < D; d += kWave) {
-    float o = w_new * load_act(v_new, act, kv0 + d);
-    for (int s = 0; s < n_used; ++s) {
+  if (tid < kWave) {
+    float dot = 0.f;
+    for (int d = lane; d < D; d += kWave) dot = fmaf(qh[d] * a.scale, load_act(k_new, act, kv0 + d), dot);
+    const float s_new = wave_sum(dot);
+    float M = fmaxf(s_new, n_zero > 0 ? 0.f : -INFINITY);
+    for (int s = lane; s < n_used; s += kWave) M = fmaxf(M, part[static_cast<int64_t>(s) * (D + 2) + D]);
+    M = wave_max(M);
+    float l = 0.f;
+    for (int s = lane; s < n_used; s += kWave) {
       const float* ps = part + static_cast<int64_t>(s) * (D + 2);
-      o = fmaf(ps[d], __expf(ps[D] - M), o);
+      l = fmaf(ps[D + 1], __expf(ps[D] - M), l);
     }
-    store_act(out, act, (static_cast<int64_t>(b) * a.n_head + h) * D + d, o * inv);
+    l = wave_sum(l) + __expf(s_new - M) + (n_zero > 0 ? static_cast<float>(n_zero) * __expf(-M) : 0.f);
+    if (lane == 0) {
+      stat[0] = M;
+      stat[1] = 1.f / l;
+      stat[2] = __expf(s_new - M) / l;
+    }
   }
+  __syncthreads();
+  const float M = stat[0], inv = stat[1];
+  float o = tid < D ? stat[2] * load_act(v_new, act, kv0 + tid) : 0.f;
+  for (int c0 = 0; c0 < n_used; c0 += kCombineChunk) {
+    const int cn = min(kCombineChunk, n_used - c0);
+    __syncthreads();
+    for (int s = tid; s < cn; s += kCombineThreads)
+      wts[s] = __expf(part[static_cast<int64_t>(c0 + s) * (D + 2) + D] - M) * inv;
+    __syncthreads();
+    if (tid < D) {
+      for (int s0 = 0; s0 < cn; s0 += kCombineUnroll) {
+        float v[kCombineUnroll];
+#pragma unroll
+        for (int u = 0; u < kCombineUnroll; ++u)
+          v[u] = s0 + u < cn ? part[static_cast<int64_t>(c0 + s0 + u) * (D + 2) + tid] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kCombineUnroll; ++u)
+          if (s0 + u < cn) o = fmaf(v[u], wts[s0 + u], o);
+      }
+    }
+  }
+  if (tid < D) store_act(out, act, (static_cast<int64_t>(b) * a.n_head + h) * D + tid, o);
 }
 
 template <typename T, int DL>
@@ -502,26 +571,29 @@ hipError_t launch_attn_decode(const float* q_rot, const void* k_pool, const void
                                          : launch_split_d<bf16_t>(a, head_dim, G, batch, s);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head, batch), dim3(kWave), 0, s, a, head_dim, k_new, v_new, dtype,
-                     out);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head, batch), dim3(kCombineThreads), 0, s, a, head_dim, k_new, v_new,
+                     dtype, out);
   return hipGetLastError();
 }
 
-hipError_t launch_qkv_rope(const float* qkv, const float* bq, const float* bk, const float* bv,
-                           const int64_t* positions, int batch, int nq, int nkv, int head_dim, double freq_base,
-                           double freq_scale, float* q_rot, void* k_new, void* v_new, int act, hipStream_t s) {
+hipError_t launch_qkv_rope(const float* qkv, int nsplit, int64_t split_stride, const float* bq, const float* bk,
+                           const float* bv, const int64_t* positions, int batch, int nq, int nkv, int head_dim,
+                           double freq_base, double freq_scale, float* q_rot, void* k_new, void* v_new, int act,
+                           hipStream_t s) {
   if (batch == 0) return hipSuccess;
-  hipLaunchKernelGGL(qkv_rope_kernel, dim3(batch), dim3(256), 0, s, qkv, bq, bk, bv, positions, nq, nkv, head_dim,
-                     freq_base, freq_scale, q_rot, k_new, v_new, act);
+  const int items = (nq + nkv) / 2 + nkv;
+  hipLaunchKernelGGL(qkv_rope_kernel, dim3(batch, (items + 255) / 256), dim3(256), 0, s, qkv, nsplit, split_stride, bq,
+                     bk, bv, positions,
+                     nq, nkv, head_dim, freq_base, freq_scale, q_rot, k_new, v_new, act);
   return hipGetLastError();
 }
 
-hipError_t launch_bias_cast(const float* y, const float* bias, void* out, int64_t rows, int n, int act,
-                            hipStream_t s) {
+hipError_t launch_bias_cast(const float* y, int nsplit, int64_t split_stride, const float* bias, void* out,
+                            int64_t rows, int n, int act, hipStream_t s) {
   const int64_t total = rows * n;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(bias_cast_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, y, bias, out,
-                     rows, n, act);
+  hipLaunchKernelGGL(bias_cast_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, y, nsplit,
+                     split_stride, bias, out, rows, n, act);
   return hipGetLastError();
 }
 

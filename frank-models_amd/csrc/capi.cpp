@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -512,6 +513,9 @@ int validate_attn_shape(const AttnShape& a, int act_dtype, int w_dtype) {
   return FMOE_OK;
 }
 
+// K splits a decode projection may use (fp32 partials in the workspace).
+constexpr int kLinearMaxSplit = 8;
+
 struct AttnLayout {
   size_t order, offsets, tables, lens, qkv, q_rot, k_new, v_new, part, attn, y, total;
 };
@@ -529,21 +533,25 @@ AttnLayout attn_layout(const AttnShape& a, int64_t max_ctx, int act) {
   L.offsets = take(2 * 4);
   L.tables = take(static_cast<size_t>(a.B) * 4);
   L.lens = take(static_cast<size_t>(a.B) * 4);
-  L.qkv = take(static_cast<size_t>(a.B) * (a.n_embd + 2 * a.n_embd_kv) * 4);
+  L.qkv = take(static_cast<size_t>(a.B) * (a.n_embd + 2 * a.n_embd_kv) * 4 * kLinearMaxSplit);
   L.q_rot = take(static_cast<size_t>(a.B) * a.n_embd * 4);
   L.k_new = take(static_cast<size_t>(a.B) * a.n_embd_kv * ab);
   L.v_new = take(static_cast<size_t>(a.B) * a.n_embd_kv * ab);
   L.part = take(static_cast<size_t>(a.B) * a.n_head * attn_decode_splits(static_cast<int>(max_ctx)) * (a.D + 2) * 4);
   L.attn = take(static_cast<size_t>(a.B) * a.n_embd * ab);
-  L.y = take(static_cast<size_t>(a.B) * a.n_embd * 4);
+  L.y = take(static_cast<size_t>(a.B) * a.n_embd * 4 * kLinearMaxSplit);
   L.total = off;
   return L;
 }
 
-// out[B, N] (out_dtype) = x[B, K] @ W for a one-expert packed weight
-// [N, K]; order/offsets hold the identity grouping of the B rows.
-int run_linear(const void* x, int64_t K, const void* packed, const float* scales, int w_dtype, int64_t N, void* out,
-               int out_dtype, int B, int act, const int* order, const int* offsets, hipStream_t s) {
+// out[B, N] fp32 = x[B, K] @ W for a one-expert packed weight [N, K];
+// order/offsets hold the identity grouping of the B rows.  The streaming
+// kernel splits K so that the few column tiles of one weight still fill the
+// GPU: *nsplit partial sums, B * N floats apart, to be added in order.
+int run_linear(const void* x, int64_t K, const void* packed, const float* scales, int w_dtype, int64_t N, float* out,
+               int B, int act, const int* order, const int* offsets, hipStream_t s, int* nsplit) {
+  const int out_dtype = FMOE_F32;
+  *nsplit = 1;
   GroupedGemmArgs g;
   g.a = x;
   g.lda = K;
@@ -565,10 +573,19 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
   g.w_format = packed_format(N, K, w_dtype);
   g.out_dtype = out_dtype;
   g.max_rows_per_expert = B;
-  // Decode batches read each weight once in the streaming kernel.
+  // Decode batches read each weight once in the streaming kernel, with
+  // about 1024 blocks (4 per CU) and at least 4 input steps per wave.
   if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && gemm_stream_supported(g)) {
+    const int64_t tiles = (N + 15) / 16;
+    const int64_t steps = K / 32;
+    int64_t ks = (1024 + tiles - 1) / tiles;
+    ks = std::min<int64_t>(ks, std::max<int64_t>(1, steps / 16));
+    ks = std::max<int64_t>(1, std::min<int64_t>(ks, kLinearMaxSplit));
+    g.ksplit = static_cast<int>(ks);
+    g.split_stride = static_cast<int64_t>(B) * N;
     FMOE_HIP(launch_gemm_stream(g, s));
     g_last_path = FMOE_PATH_STREAM;
+    *nsplit = g.ksplit;
     return FMOE_OK;
   }
   return run_grouped_gemm(g, s);
@@ -599,19 +616,31 @@ int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, c
   FMOE_HIP(launch_iota(order, B, offsets, 0, B, s));
   float* qkv = at<float>(workspace, L.qkv);
   float* q_rot = at<float>(workspace, L.q_rot);
-  FMOE_TRY(run_linear(input, a.n_embd, w.wqkv, w.wqkv_scales, w.w_dtype, nq + 2 * nkv, qkv, FMOE_F32, B, act, order,
-                      offsets, s));
   const bool bias = w.use_bias != 0;
-  FMOE_HIP(launch_qkv_rope(qkv, bias ? w.bq : nullptr, bias ? w.bk : nullptr, bias ? w.bv : nullptr, positions, B, nq,
-                           nkv, static_cast<int>(a.D), w.freq_base, w.freq_scale, q_rot, k_new, v_new, act, s));
+  {
+    ScopedTimer t(FMOE_TIMER_QKV, s);
+    int ns = 1;
+    FMOE_TRY(run_linear(input, a.n_embd, w.wqkv, w.wqkv_scales, w.w_dtype, nq + 2 * nkv, qkv, B, act, order,
+                        offsets, s, &ns));
+    FMOE_HIP(launch_qkv_rope(qkv, ns, static_cast<int64_t>(B) * (nq + 2 * nkv), bias ? w.bq : nullptr,
+                             bias ? w.bk : nullptr, bias ? w.bv : nullptr, positions, B, nq, nkv,
+                             static_cast<int>(a.D), w.freq_base, w.freq_scale, q_rot, k_new, v_new, act, s));
+  }
   void* attn = at<char>(workspace, L.attn);
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(a.D)));
-  FMOE_HIP(launch_attn_decode(q_rot, k_pool, v_pool, n_blocks, block_size, tables, max_blocks, lens, max_ctx, k_new,
-                              v_new, B, static_cast<int>(a.n_head), static_cast<int>(a.n_head_kv),
-                              static_cast<int>(a.D), act, scale, at<float>(workspace, L.part), attn, s));
+  {
+    ScopedTimer t(FMOE_TIMER_ATTENTION, s);
+    FMOE_HIP(launch_attn_decode(q_rot, k_pool, v_pool, n_blocks, block_size, tables, max_blocks, lens, max_ctx, k_new,
+                                v_new, B, static_cast<int>(a.n_head), static_cast<int>(a.n_head_kv),
+                                static_cast<int>(a.D), act, scale, at<float>(workspace, L.part), attn, s));
+  }
   float* y = at<float>(workspace, L.y);
-  FMOE_TRY(run_linear(attn, a.n_embd, w.wo, w.wo_scales, w.w_dtype, nq, y, FMOE_F32, B, act, order, offsets, s));
-  FMOE_HIP(launch_bias_cast(y, bias ? w.bo : nullptr, out, B, nq, act, s));
+  {
+    ScopedTimer t(FMOE_TIMER_OUT_PROJ, s);
+    int ns = 1;
+    FMOE_TRY(run_linear(attn, a.n_embd, w.wo, w.wo_scales, w.w_dtype, nq, y, B, act, order, offsets, s, &ns));
+    FMOE_HIP(launch_bias_cast(y, ns, static_cast<int64_t>(B) * nq, bias ? w.bo : nullptr, out, B, nq, act, s));
+  }
   return FMOE_OK;
 }
 

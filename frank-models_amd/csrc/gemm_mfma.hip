@@ -323,11 +323,17 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   const int64_t kblocks = F8 ? K / 64 : K / 32;
   // This wave's share of the input axis, in 32-input steps (whole fp8
   // blocks of two steps for fp8 weights).
+  // With a K split (gridDim.y > 1, one-set fp32 scatter only) block row
+  // blockIdx.y takes its share first and writes partial sums split_stride
+  // elements apart.
   const int ksteps = static_cast<int>(K / 32);
   const int unit = F8 ? 2 : 1;
   const int units = ksteps / unit;
-  const int ks_begin = (wave * units / kStreamWaves) * unit;
-  const int ks_end = ((wave + 1) * units / kStreamWaves) * unit;
+  const int kz = blockIdx.y, nz = gridDim.y;
+  const int u0 = kz * units / nz, u1 = (kz + 1) * units / nz;
+  const int ks_begin = (u0 + wave * (u1 - u0) / kStreamWaves) * unit;
+  const int ks_end = (u0 + (wave + 1) * (u1 - u0) / kStreamWaves) * unit;
+  if (kz > 0) g.out = static_cast<float*>(g.out) + kz * g.split_stride;
   const unsigned char* wsrc[NSETS];
 #pragma unroll
   for (int s = 0; s < NSETS; ++s) {
@@ -476,6 +482,7 @@ hipError_t launch_tiled_t(const GroupedGemmArgs& g, hipStream_t s) {
 
 template <bool F8, int TILES>
 void launch_stream_tiles(const GroupedGemmArgs& g, hipStream_t s, dim3 grid, int col_tiles) {
+  grid.y = g.ksplit > 1 ? g.ksplit : 1;
   if (g.epi == EPI_SWIGLU)
     hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
   else if (g.epi == EPI_SCATTER_WEIGHTED)
@@ -507,7 +514,9 @@ bool gemm_tiled_supported(const GroupedGemmArgs& g) {
 }
 
 bool gemm_stream_supported(const GroupedGemmArgs& g) {
-  return mfma_common_ok(g) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0;
+  const bool split_ok = g.ksplit <= 1 || (g.epi == EPI_SCATTER && g.out_dtype == DT_F32 && g.split_stride > 0 &&
+                                          g.ksplit <= 64);
+  return mfma_common_ok(g) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0 && split_ok;
 }
 
 int resolve_tiled_variant(const GroupedGemmArgs& g, int variant) {

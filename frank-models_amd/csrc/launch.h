@@ -89,8 +89,9 @@ struct GroupedGemmArgs {
   int w_format = WF_ROWMAJOR;   // packed_format(N, K, w_dtype)
   int out_dtype = DT_F32;
   // Split of K over ksplit partial products written to out + s * split_stride
-  // (s < ksplit).  Only the 256-tile kernel splits; launchers report the
-  // split they used.
+  // (s < ksplit).  The 256-tile kernel splits on its own (launchers report
+  // the split they used); the streaming kernel splits when the caller sets
+  // ksplit (one weight set, fp32 scatter output).
   int ksplit = 1;
   int64_t split_stride = 0;
   // Upper bound on any expert's row count when the caller knows one (the
@@ -192,12 +193,14 @@ hipError_t launch_iota(int* v, int n, int* pair, int pair0, int pair1, hipStream
 hipError_t launch_fill_int(int* v, int n, int value, hipStream_t s);
 // qkv [B, nq + 2 nkv] fp32 -> bias (optional), RoPE on q and k:
 // q_rot fp32 [B, nq], k_new / v_new [B, nkv] in act dtype.
-hipError_t launch_qkv_rope(const float* qkv, const float* bq, const float* bk, const float* bv,
-                           const int64_t* positions, int batch, int nq, int nkv, int head_dim, double freq_base,
-                           double freq_scale, float* q_rot, void* k_new, void* v_new, int act, hipStream_t s);
-// out[r, :] = y[r, :] (+ bias) in act dtype.
-hipError_t launch_bias_cast(const float* y, const float* bias, void* out, int64_t rows, int n, int act,
-                            hipStream_t s);
+// qkv holds nsplit partial sums split_stride floats apart, added in order.
+hipError_t launch_qkv_rope(const float* qkv, int nsplit, int64_t split_stride, const float* bq, const float* bk,
+                           const float* bv, const int64_t* positions, int batch, int nq, int nkv, int head_dim,
+                           double freq_base, double freq_scale, float* q_rot, void* k_new, void* v_new, int act,
+                           hipStream_t s);
+// out[r, :] = sum of the nsplit partials y[r, :] (+ bias) in act dtype.
+hipError_t launch_bias_cast(const float* y, int nsplit, int64_t split_stride, const float* bias, void* out,
+                            int64_t rows, int n, int act, hipStream_t s);
 // Head sizes and query-per-KV-head groups the attention kernels take.
 bool attn_decode_supported(int head_dim, int group);
 // Context splits of the attention (part holds batch * n_head * splits *

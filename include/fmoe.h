@@ -99,7 +99,10 @@ typedef enum fmoe_timer {
   FMOE_TIMER_COMBINE = 4,
   FMOE_TIMER_MUL_MAT_ID = 5,
   FMOE_TIMER_NORM = 6,    /* ffn_norm RMSNorm of the sub-layer */
-  FMOE_TIMER_COUNT = 7
+  FMOE_TIMER_QKV = 7,     /* decode attention: Q/K/V projection + bias + RoPE */
+  FMOE_TIMER_ATTENTION = 8, /* decode attention: context splits + combine */
+  FMOE_TIMER_OUT_PROJ = 9,  /* decode attention: output projection + bias */
+  FMOE_TIMER_COUNT = 10
 } fmoe_timer;
 int fmoe_timing_enable(int on);
 int fmoe_timing_read(double *ms_out, int64_t *launches_out, int n);
