@@ -48,11 +48,18 @@ __global__ __launch_bounds__(kCopyThreads) void kv_gather_kernel(const uint32_t*
 
 // One row per sequence; when several sequences name the same slot the last
 // one wins, as in the reference's sequential loop (oracles/kvcache.py:134-139).
-__global__ __launch_bounds__(kCopyThreads) void kv_scatter_decode_kernel(uint32_t* __restrict__ cache, int64_t n_blocks,
+// blockIdx.y selects the pool (cache, vals) or (cache2, vals2).
+__global__ __launch_bounds__(kCopyThreads) void kv_scatter_decode_kernel(uint32_t* __restrict__ cache,
+                                                                         uint32_t* __restrict__ cache2, int64_t n_blocks,
                                                                          int block_size, int row_words,
                                                                          const uint32_t* __restrict__ vals,
+                                                                         const uint32_t* __restrict__ vals2,
                                                                          const int* __restrict__ block_idx,
                                                                          const int* __restrict__ pos_idx, int batch) {
+  if (blockIdx.y == 1) {
+    cache = cache2;
+    vals = vals2;
+  }
   const int b = blockIdx.x;
   const int bi = block_idx[b], p = pos_idx[b];
   bool later = false;
@@ -237,18 +244,21 @@ constexpr int kAttnWaves = kAttnThreads / kWave;
 // [64 w, 64 w + 64) in both phases, so a wave's memory traffic is two
 // rounds of independent loads: all of its K rows, then (issued before the
 // block-wide softmax, so that their latency overlaps it) all of its V rows.
-// Scores: 8 lanes per position, each lane holding DL = D/8 dimensions in
-// 16-byte chunks spread so that the 8 lanes of a position read each 128 B
-// span of the row together; the G query heads of the KV head are scored
-// from one read of K.  P.V: LPR lanes per row, 16 bytes each.
-template <typename T, int DL, int G>
+// Scores: LP lanes per position, each lane holding DL = D/LP dimensions in
+// chunks of up to 16 bytes spread so that the LP lanes of a position read
+// each span of the row together; the G query heads of the KV head are
+// scored from one read of K (query registers: G * DL per lane).  P.V: LPR
+// lanes per row, 16 bytes each.
+template <typename T, int D, int G, int LP>
 __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
-  constexpr int D = 8 * DL;
+  constexpr int DL = D / LP;
+  static_assert(G <= LP, "one lane per query head stores its score");
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
   constexpr int CW = EPV < DL ? EPV : DL;                 // score chunk (elements)
   constexpr int NC = DL / CW;                             // score chunks per lane per position
   constexpr int kQ = kSplitLen / kAttnWaves;              // positions per wave
-  constexpr int kSteps = kQ / 8;                          // score steps of 8 positions
+  constexpr int PPS = kWave / LP;                         // positions per score step
+  constexpr int kSteps = kQ / PPS;                        // score steps
   constexpr int SR = 16 / NC < kSteps ? 16 / NC : kSteps;  // steps per load round (<= 16 loads)
   constexpr int VC = EPV;                                 // P.V elements per lane per row
   constexpr int LPR = D / VC;                             // lanes per row
@@ -288,7 +298,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
   }
   const T* kp = static_cast<const T*>(a.k_pool) + static_cast<int64_t>(kvh) * D;
   const T* vp = static_cast<const T*>(a.v_pool) + static_cast<int64_t>(kvh) * D;
-  const int pi = lane >> 3, sub = lane & 7;
+  const int pi = lane / LP, sub = lane % LP;
   float q[G][DL];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -297,7 +307,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < CW; ++e)
         q[g][c * CW + e] =
-            a.q[(static_cast<int64_t>(b) * a.n_head + kvh * G + g) * D + c * 8 * CW + sub * CW + e] * a.scale;
+            a.q[(static_cast<int64_t>(b) * a.n_head + kvh * G + g) * D + c * LP * CW + sub * CW + e] * a.scale;
   __syncthreads();
   const int tw = wave * kQ;  // this wave's first position
 
@@ -310,10 +320,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
     int rr[SR];
 #pragma unroll
     for (int u = 0; u < SR; ++u) {
-      rr[u] = rows[tw + (r0 + u) * 8 + pi];
+      rr[u] = rows[tw + (r0 + u) * PPS + pi];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const T* src = kp + rr[u] * row_elems + c * 8 * CW + sub * CW;
+        const T* src = kp + rr[u] * row_elems + c * LP * CW + sub * CW;
         if (CWW == 4) {
           const u32x4_t w = rr[u] >= 0 ? *reinterpret_cast<const u32x4_t*>(src) : u32x4_t{0u, 0u, 0u, 0u};
           kr[u][c][0] = w[0], kr[u][c][1 % CWW] = w[1], kr[u][c][2 % CWW] = w[2], kr[u][c][3 % CWW] = w[3];
@@ -327,7 +337,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < SR; ++u) {
-      const int t = tw + (r0 + u) * 8 + pi;
+      const int t = tw + (r0 + u) * PPS + pi;
       float kv[DL];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -344,10 +354,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < DL; ++i) acc = fmaf(q[g][i], kv[i], acc);
-        acc += __shfl_xor(acc, 1, kWave);
-        acc += __shfl_xor(acc, 2, kWave);
-        acc += __shfl_xor(acc, 4, kWave);
-        if (sub == (g & 7)) sc[g][t] = rr[u] == -2 ? -INFINITY : acc;  // a zero row scores 0
+#pragma unroll
+        for (int o = 1; o < LP; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+        if (sub == g) sc[g][t] = rr[u] == -2 ? -INFINITY : acc;  // a zero row scores 0
       }
     }
   }
@@ -511,14 +520,21 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
   if (tid < D) store_act(out, act, (static_cast<int64_t>(b) * a.n_head + h) * D + tid, o);
 }
 
-template <typename T, int DL>
+// Lanes per position in the score phase.  For head_dim 128 (bf16, 4 query
+// heads per KV head) 8 lanes beat 16 (61.5 against 77.9 us at 16 x 4096
+// positions, 72.5 us with 16 lanes forced to 4 waves per SIMD), although
+// 16 lanes halve the query registers.
+constexpr int kLanesPerPos64 = 8;
+constexpr int kLanesPerPos128 = 8;
+
+template <typename T, int D, int LP>
 hipError_t launch_split_g(const AttnArgs& a, int G, int B, hipStream_t s) {
   const dim3 grid(a.n_split, a.n_head_kv, B);
   switch (G) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<T, DL, 1>), grid, dim3(kAttnThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<T, DL, 2>), grid, dim3(kAttnThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<T, DL, 4>), grid, dim3(kAttnThreads), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((attn_split_kernel<T, DL, 8>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<T, D, 1, LP>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<T, D, 2, LP>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<T, D, 4, LP>), grid, dim3(kAttnThreads), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attn_split_kernel<T, D, 8, LP>), grid, dim3(kAttnThreads), 0, s, a); break;
     default: return hipErrorNotSupported;
   }
   return hipGetLastError();
@@ -527,10 +543,10 @@ hipError_t launch_split_g(const AttnArgs& a, int G, int B, hipStream_t s) {
 template <typename T>
 hipError_t launch_split_d(const AttnArgs& a, int D, int G, int B, hipStream_t s) {
   switch (D) {
-    case 16: return launch_split_g<T, 2>(a, G, B, s);
-    case 32: return launch_split_g<T, 4>(a, G, B, s);
-    case 64: return launch_split_g<T, 8>(a, G, B, s);
-    case 128: return launch_split_g<T, 16>(a, G, B, s);
+    case 16: return launch_split_g<T, 16, 8>(a, G, B, s);
+    case 32: return launch_split_g<T, 32, 8>(a, G, B, s);
+    case 64: return launch_split_g<T, 64, kLanesPerPos64>(a, G, B, s);
+    case 128: return launch_split_g<T, 128, kLanesPerPos128>(a, G, B, s);
     default: return hipErrorNotSupported;
   }
 }
@@ -621,9 +637,20 @@ hipError_t launch_kv_gather(const void* cache, int64_t n_blocks, int block_size,
 hipError_t launch_kv_scatter_decode(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
                                     const int* block_idx, const int* pos_idx, int batch, hipStream_t s) {
   if (batch == 0 || row_bytes == 0) return hipSuccess;
-  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch), dim3(kCopyThreads), 0, s, static_cast<uint32_t*>(cache),
-                     n_blocks, block_size, row_bytes / 4, static_cast<const uint32_t*>(vals), block_idx, pos_idx,
-                     batch);
+  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch, 1), dim3(kCopyThreads), 0, s, static_cast<uint32_t*>(cache),
+                     nullptr, n_blocks, block_size, row_bytes / 4, static_cast<const uint32_t*>(vals), nullptr,
+                     block_idx, pos_idx, batch);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_scatter_decode2(void* k_cache, void* v_cache, int64_t n_blocks, int block_size, int row_bytes,
+                                     const void* k_vals, const void* v_vals, const int* block_idx, const int* pos_idx,
+                                     int batch, hipStream_t s) {
+  if (batch == 0 || row_bytes == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch, 2), dim3(kCopyThreads), 0, s,
+                     static_cast<uint32_t*>(k_cache), static_cast<uint32_t*>(v_cache), n_blocks, block_size,
+                     row_bytes / 4, static_cast<const uint32_t*>(k_vals), static_cast<const uint32_t*>(v_vals),
+                     block_idx, pos_idx, batch);
   return hipGetLastError();
 }
 

@@ -576,10 +576,11 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
   // Decode batches read each weight once in the streaming kernel, with
   // about 1024 blocks (4 per CU) and at least 4 input steps per wave.
   if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && gemm_stream_supported(g)) {
+    // Split K so that each wave streams one full trip of 8 steps (K / 32 /
+    // (4 waves * 8)) while the grid has fewer than ~2048 blocks.
     const int64_t tiles = (N + 15) / 16;
     const int64_t steps = K / 32;
-    int64_t ks = (1024 + tiles - 1) / tiles;
-    ks = std::min<int64_t>(ks, std::max<int64_t>(1, steps / 16));
+    int64_t ks = std::min<int64_t>(steps / 32, (2048 + tiles - 1) / tiles);
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, kLinearMaxSplit));
     g.ksplit = static_cast<int>(ks);
     g.split_stride = static_cast<int64_t>(B) * N;
@@ -1179,10 +1180,8 @@ int fmoe_attention_decode_paged(const void* input, const int64_t* positions, voi
   // scatter_decode after the attention has read the pools
   // (transformer_layer_moe_decode.mlir:202-206).
   const int rb = static_cast<int>(n_embd_kv * dtype_bytes(act_dtype));
-  FMOE_HIP(launch_kv_scatter_decode(k_cache, n_blocks, static_cast<int>(block_size), rb, kn, block_indices,
-                                    pos_in_blocks, static_cast<int>(batch), s));
-  FMOE_HIP(launch_kv_scatter_decode(v_cache, n_blocks, static_cast<int>(block_size), rb, vn, block_indices,
-                                    pos_in_blocks, static_cast<int>(batch), s));
+  FMOE_HIP(launch_kv_scatter_decode2(k_cache, v_cache, n_blocks, static_cast<int>(block_size), rb, kn, vn,
+                                     block_indices, pos_in_blocks, static_cast<int>(batch), s));
   return ok();
 }
 

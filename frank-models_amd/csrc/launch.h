@@ -185,6 +185,10 @@ hipError_t launch_kv_gather(const void* cache, int64_t n_blocks, int block_size,
                             int max_blocks, const int* ctx_lens, int max_ctx, int batch, void* out, hipStream_t s);
 hipError_t launch_kv_scatter_decode(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
                                     const int* block_idx, const int* pos_idx, int batch, hipStream_t s);
+// The same for the K and V pools in one launch.
+hipError_t launch_kv_scatter_decode2(void* k_cache, void* v_cache, int64_t n_blocks, int block_size, int row_bytes,
+                                     const void* k_vals, const void* v_vals, const int* block_idx, const int* pos_idx,
+                                     int batch, hipStream_t s);
 hipError_t launch_kv_scatter_prefill(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
                                      int seq_len, const int* tables, int max_blocks, const int* start, int batch,
                                      hipStream_t s);
