@@ -189,7 +189,7 @@ def all_configs(fm, wl, torch, args):
     return rows
 
 
-def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16):
+def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16, cpu_sample=0):
     """The decode step's attention half at Mixtral-8x7B's attention shape
     (n_embd 4096, 32 query heads, 8 KV heads, head_dim 128), bf16: one new
     token per sequence for `batch` sequences, each with `ctx` cached
@@ -250,7 +250,37 @@ def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16):
         res["qkv_GBps"] = qkv_bytes / (kern["qkv"] * 1e-3) / 1e9
     if kern.get("out_proj"):
         res["out_proj_GBps"] = out_bytes / (kern["out_proj"] * 1e-3) / 1e9
+    if cpu_sample:
+        res["cpu_baseline"] = attention_cpu_baseline(torch, blk, x, pos, kp, vp, tables, lens, ctx, bi, pi, cpu_sample)
     return res
+
+
+def attention_cpu_baseline(torch, blk, x, pos, kp, vp, tables, lens, ctx, bi, pi, sample):
+    """The oracle's gather + attention_block_decode + scatter (oracle/attention.py,
+    NumPy float32) on `sample` of the sequences, timed on this host."""
+    import numpy as np
+    from oracle import attention as oa
+
+    tb = tables[:, :sample].cpu().numpy()
+    needed = np.unique(tb)
+    remap = {int(b): i for i, b in enumerate(needed)}
+    tb = np.vectorize(remap.get)(tb).astype(np.int32)
+    kh = kp[torch.from_numpy(needed).cuda().long()].float().cpu().numpy()
+    vh = vp[torch.from_numpy(needed).cuda().long()].float().cpu().numpy()
+    ws = [torch.randn(s, device="cuda").mul(s[0] ** -0.5).float().cpu().numpy()
+          for s in ((4096, 4096), (4096, 1024), (4096, 1024), (4096, 4096))]
+    xs = x[:sample].float().cpu().numpy()
+    ps = pos[:sample].cpu().numpy()
+    bis = np.array([remap[int(b)] for b in bi[:sample].cpu().numpy()], np.int32)
+    t0 = time.perf_counter()
+    oa.attention_decode_paged(xs, ps, kh, vh, 0, tb, lens[:, :sample].cpu().numpy(), ctx, bis,
+                              pi[:sample].cpu().numpy(), *ws, None, None, None, None, False, 32, 8, 4096,
+                              dtype=np.float32)
+    dt = time.perf_counter() - t0
+    return {"value": sample / dt, "unit": "tokens/s", "cores": len(os.sched_getaffinity(0)), "kind": "port",
+            "sample": f"{sample} of the {x.shape[0]} sequences ({ctx} cached positions each), fp32 NumPy gather + "
+                      f"attention_block_decode + scatter (oracle/attention.py), one run ({dt:.2f}s), random weights "
+                      f"of the same shapes"}
 
 
 def read_traffic(kernel_name):
@@ -295,7 +325,8 @@ def main():
     fm = importlib.import_module("frank-models_amd")
     wl = importlib.import_module("frank-models_amd.workloads")
     if args.attention_only:
-        att = attention_decode(fm, torch, args.attn_batch, args.attn_context, max(args.steps, 20), args.warmup)
+        att = attention_decode(fm, torch, args.attn_batch, args.attn_context, max(args.steps, 20), args.warmup,
+                               cpu_sample=0 if args.no_cpu_baseline else 2)
         log(f"attention decode {att['ms_per_step']:.3f} ms/step, kernels(ms) {att['kernels_ms']}")
         print(json.dumps({"metric": "decode attention tokens/s (paged KV, Mixtral attention shape)",
                           "value": att["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "dtype": "bf16",
@@ -358,7 +389,8 @@ def main():
     if not args.no_attention:
         log(f"attention decode: batch {args.attn_batch}, context {args.attn_context}")
         result["attention_decode"] = attention_decode(fm, torch, args.attn_batch, args.attn_context,
-                                                      max(args.steps, 20), args.warmup)
+                                                      max(args.steps, 20), args.warmup,
+                                                      cpu_sample=0 if args.no_cpu_baseline else 2)
         log(f"attention decode {result['attention_decode']['ms_per_step']:.3f} ms/step, "
             f"kernels(ms) {result['attention_decode']['kernels_ms']}")
 

@@ -654,11 +654,11 @@ int check_attn_weights(const AttnWeights& w) {
   return FMOE_OK;
 }
 
-int check_pool(const char* what, int64_t n_blocks, int64_t block_size, const AttnShape& a) {
-  FMOE_TRY(check_dims(what, n_blocks, 1, kMaxDim));
+// Pools are addressed by a 32-bit row index (block * block_size + row).
+int check_pool(int64_t n_blocks, int64_t block_size) {
+  FMOE_TRY(check_dims("n_blocks", n_blocks, 1, kMaxDim));
   FMOE_TRY(check_dims("block_size", block_size, 1, kMaxDim));
   if (n_blocks * block_size > kMaxDim) return fail(FMOE_ERR_SHAPE, "n_blocks * block_size exceeds 2^31-1");
-  (void)a;
   return FMOE_OK;
 }
 
@@ -1150,7 +1150,7 @@ int fmoe_attention_decode_paged(const void* input, const int64_t* positions, voi
   if (n_head < 1 || n_embd < 1) return fail(FMOE_ERR_SHAPE, "n_head and n_embd must be positive");
   const AttnShape a{batch, n_head, n_head_kv, n_embd, n_embd_kv, n_embd / n_head};
   FMOE_TRY(validate_attn_shape(a, act_dtype, w_dtype));
-  FMOE_TRY(check_pool("n_blocks", n_blocks, block_size, a));
+  FMOE_TRY(check_pool(n_blocks, block_size));
   FMOE_TRY(check_dims("n_layers", n_layers, 1, kMaxDim));
   FMOE_TRY(check_dims("layer", layer, 0, n_layers - 1));
   FMOE_TRY(check_dims("max_blocks_per_seq", max_blocks_per_seq, 1, kMaxDim));
