@@ -66,6 +66,10 @@ from .attention import (  # noqa: F401
 from . import _lib as lowlevel  # noqa: F401
 from . import params  # noqa: F401
 from .params import (  # noqa: F401
+    ATTN_HPARAMS,
+    AttentionHParams,
+    AttentionLayer,
+    load_attention_layers,
     HPARAMS,
     MoEFFNLayer,
     MoEHParams,

@@ -28,6 +28,10 @@ kernels, so no packing or quantisation happens on the request path:
   holds the packed buffers themselves, so loading it is a copy.
 * ``quantize_fp8``: offline fp8 quantisation = load with ``weight_dtype="fp8"``
   and save the packed result.
+* ``load_attention_layers``: the decode attention half's tensors under the
+  same scheme (``blk.{i}.attn_norm.weight``, ``blk.{i}.attn_{q,k,v,output}.weight``
+  in the ``x @ W`` layout ``[n_in, n_out]``, optional ``.bias``;
+  tests/models/test_toy_llm.py:80-109), packed into ``AttentionBlockDecode``.
 """
 
 from __future__ import annotations
@@ -339,4 +343,92 @@ def quantize_fp8(params, hp: MoEHParams, path: Optional[Union[str, Path]] = None
     out = load_moe_layers(params, hp, act_dtype=act_dtype, weight_dtype="fp8", layers=layers)
     if path is not None:
         save_packed(out, path)
+    return out
+
+
+# ---------------------------------------------------------------- attention
+_ATTN_PROJ = ("attn_q", "attn_k", "attn_v", "attn_output")
+
+
+@dataclass(frozen=True)
+class AttentionHParams:
+    """The hyper-parameters of the decode attention half, under the names of
+    the reference's hparams accessors (models/llm/mixtral/hparams.mlir:26-80)."""
+
+    block_count: int
+    embedding_length: int  # n_embd
+    attention_head_count: int  # n_head
+    attention_head_count_kv: int  # n_head_kv
+    rope_freq_base: float
+    use_attention_bias: bool
+    layer_norm_rms_epsilon: float
+    rope_freq_scale: float = 1.0
+
+
+ATTN_HPARAMS = {
+    # models/llm/mixtral/hparams.mlir:26-80
+    "mixtral": AttentionHParams(32, 4096, 32, 8, 10000.0, False, 1e-5),
+    # models/llm/toy/hparams.mlir:27-81
+    "toy": AttentionHParams(2, 64, 4, 2, 10000.0, False, 1e-5),
+}
+
+
+def attention_shapes(hp: AttentionHParams) -> dict:
+    """``blk.{i}.attn_*`` shapes (tests/models/test_toy_llm.py:80-109): the
+    projections in the ``x @ W`` layout ``[n_in, n_out]``."""
+    H = hp.embedding_length
+    kv = hp.attention_head_count_kv * (H // hp.attention_head_count)
+    return {"attn_norm": (H,), "attn_q": (H, H), "attn_k": (H, kv), "attn_v": (H, kv), "attn_output": (H, H)}
+
+
+class AttentionLayer:
+    """One layer's attention half: ``attn_norm`` weight and an
+    ``AttentionBlockDecode`` with packed projections."""
+
+    def __init__(self, index: int, hp: AttentionHParams, norm_w: torch.Tensor, attn):
+        self.index = index
+        self.hp = hp
+        self.norm_w = norm_w
+        self.attn = attn
+
+
+def load_attention_layers(params, hp: AttentionHParams, act_dtype=torch.bfloat16, weight_dtype=None,
+                          layers: Optional[Iterable[int]] = None) -> list:
+    """Pack every requested layer's attention projections
+    (``blk.{i}.attn_{q,k,v,output}.weight``, biases ``.bias`` when
+    ``hp.use_attention_bias``, ``blk.{i}.attn_norm.weight``) for the decode
+    kernels.  ``weight_dtype``: "bf16", "f32" or "fp8"; default: the
+    activation dtype.  Shapes are checked before any device work."""
+    from .attention import AttentionBlockDecode
+
+    src = params if isinstance(params, ParamSource) else ParamSource(params)
+    if act_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"act_dtype must be torch.float32 or torch.bfloat16, got {act_dtype}")
+    shapes = attention_shapes(hp)
+    idx = list(range(hp.block_count) if layers is None else layers)
+    for i in idx:
+        for t, shape in shapes.items():
+            name = param_name(i, t)
+            if tuple(src.shape(name)) != tuple(shape):
+                raise ValueError(f"parameter {name!r} has shape {src.shape(name)}, expected {tuple(shape)}")
+        if hp.use_attention_bias:
+            for t in _ATTN_PROJ:
+                name = f"blk.{i}.{t}.bias"
+                want = (shapes[t][1],)
+                if tuple(src.shape(name)) != want:
+                    raise ValueError(f"parameter {name!r} has shape {src.shape(name)}, expected {want}")
+    dev = _device()
+    out = []
+    for i in idx:
+        # the packer converts fp32 sources to the weight dtype
+        w = [src.get(param_name(i, t)).to(dev, torch.float32) for t in _ATTN_PROJ]
+        b = [None] * 4
+        if hp.use_attention_bias:
+            b = [src.get(f"blk.{i}.{t}.bias").to(dev, torch.float32) for t in _ATTN_PROJ]
+        attn = AttentionBlockDecode(*w, *b, use_bias=hp.use_attention_bias, n_head=hp.attention_head_count,
+                                    n_head_kv=hp.attention_head_count_kv, n_embd=hp.embedding_length,
+                                    rope_freq_base=hp.rope_freq_base, rope_freq_scale=hp.rope_freq_scale,
+                                    act_dtype=act_dtype, weight_dtype=weight_dtype)
+        norm_w = src.get(param_name(i, "attn_norm")).to(dev, act_dtype).contiguous()
+        out.append(AttentionLayer(i, hp, norm_w, attn))
     return out

@@ -143,3 +143,46 @@ def test_safetensors_and_dict_sources_agree(fm, wl, tmp_path):
     b, _ = _run(fm.load_moe_layers(path, hp), inputs, "bf16")
     for x, y in zip(a, b):
         np.testing.assert_array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+# ------------------------------------------------------------------ attention tensors
+@pytest.mark.parametrize("act,bias", [("f32", False), ("f32", True), ("bf16", False)])
+def test_attention_layers_from_named_parameters(fm, act, bias):
+    """blk.{i}.attn_* tensors (tests/models/test_toy_llm.py:80-109 layout) load
+    into AttentionBlockDecode; each layer equals the oracle on its own tensors."""
+    from dataclasses import replace
+
+    from oracle import attention as oa
+    from helpers import assert_close_rms
+
+    hp = replace(fm.ATTN_HPARAMS["toy"], use_attention_bias=bias)
+    shapes = fm.params.attention_shapes(hp)
+    rng = np.random.default_rng(3 + bias)
+    params = {}
+    for i in range(hp.block_count):
+        for t, s in shapes.items():
+            params[f"blk.{i}.{t}.weight"] = (rng.standard_normal(s) * 0.2).astype(np.float32)
+        for t in ("attn_q", "attn_k", "attn_v", "attn_output"):
+            params[f"blk.{i}.{t}.bias"] = (rng.standard_normal(shapes[t][1]) * 0.1).astype(np.float32)
+    dt = torch.float32 if act == "f32" else torch.bfloat16
+    layers = fm.load_attention_layers(params, hp, act_dtype=dt)
+    assert [lay.index for lay in layers] == list(range(hp.block_count))
+    B, ctx, H, Hkv, n = 3, 20, hp.attention_head_count, hp.attention_head_count_kv, hp.embedding_length
+    D = n // H
+    rnd = (lambda a: a) if act == "f32" else nm.bf16_round
+    for lay in layers:
+        i = lay.index
+        w = {t: rnd(params[f"blk.{i}.{t}.weight"]) for t in ("attn_q", "attn_k", "attn_v", "attn_output")}
+        x = rnd(rng.standard_normal((B, n)).astype(np.float32))
+        kc = rnd(rng.standard_normal((B, ctx, Hkv, D)).astype(np.float32))
+        vc = rnd(rng.standard_normal((B, ctx, Hkv, D)).astype(np.float32))
+        pos = np.array([20, 5, 300], np.int64)
+        out, k_new, _ = lay.attn(torch.from_numpy(x).to("cuda", dt), torch.from_numpy(pos).cuda(),
+                                 torch.from_numpy(kc).to("cuda", dt), torch.from_numpy(vc).to("cuda", dt))
+        b = [params[f"blk.{i}.{t}.bias"] for t in ("attn_q", "attn_k", "attn_v", "attn_output")]
+        ref = oa.attention_block_decode(x, pos, kc, vc, w["attn_q"], w["attn_k"], w["attn_v"], w["attn_output"],
+                                        *b, bias, H, Hkv, n, hp.rope_freq_base, hp.rope_freq_scale)
+        rtol = 1e-4 if act == "f32" else 2e-2
+        assert_close_rms(out.float().cpu().numpy(), ref[0], rtol, what=f"layer {i}")
+        assert_close_rms(k_new.float().cpu().numpy(), ref[1], rtol, what=f"layer {i} k_new")
+        np.testing.assert_array_equal(lay.norm_w.float().cpu().numpy(), rnd(params[f"blk.{i}.attn_norm.weight"]))

@@ -66,3 +66,26 @@ def test_safetensors_source(fm, tmp_path):
         src.get("blk.0.attn_q.weight")
     with pytest.raises(ValueError, match="not an fmoe packed artifact"):
         fm.load_packed(path)
+
+
+# ------------------------------------------------------------------ attention tensors
+def test_attention_shapes_follow_the_toy_model(fm):
+    """tests/models/test_toy_llm.py:80-109: attn_q/attn_output [n_embd, n_embd],
+    attn_k/attn_v [n_embd, n_head_kv * head_dim]."""
+    hp = fm.ATTN_HPARAMS["toy"]
+    s = fm.params.attention_shapes(hp)
+    assert s == {"attn_norm": (64,), "attn_q": (64, 64), "attn_k": (64, 32), "attn_v": (64, 32),
+                 "attn_output": (64, 64)}
+    m = fm.ATTN_HPARAMS["mixtral"]
+    assert fm.params.attention_shapes(m)["attn_k"] == (4096, 1024)
+
+
+def test_attention_loader_checks_shapes_before_device_work(fm):
+    hp = fm.ATTN_HPARAMS["toy"]
+    params = {f"blk.0.{t}.weight": np.zeros(s, np.float32) for t, s in fm.params.attention_shapes(hp).items()}
+    params["blk.0.attn_k.weight"] = np.zeros((64, 16), np.float32)
+    with pytest.raises(ValueError, match="attn_k"):
+        fm.load_attention_layers(params, hp, layers=[0])
+    del params["blk.0.attn_k.weight"]
+    with pytest.raises(KeyError, match="attn_k"):
+        fm.load_attention_layers(params, hp, layers=[0])
