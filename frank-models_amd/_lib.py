@@ -129,6 +129,15 @@ SIGNATURES = {
          _vp],
     ),
     "fmoe_attention_decode_paged_workspace_bytes": (_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "fmoe_attention_sublayer_decode_paged_workspace_bytes": (
+        _sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "fmoe_attention_sublayer_decode_paged": (
+        _c_int,
+        [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp,
+         _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, ctypes.c_float, _c_int, _vp, _vp, _vp, _vp, _sz,
+         _vp],
+    ),
     "fmoe_attention_decode_paged": (
         _c_int,
         [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp,

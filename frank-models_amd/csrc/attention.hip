@@ -170,13 +170,20 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const float* __restrict__
 }
 
 // out[b, n] = y[b, n] (+ bias[n]) in act dtype.
+// out may alias residual (element-wise, same index).
 __global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict__ y, int nsplit, int64_t split_stride,
-                                                        const float* __restrict__ bias, void* __restrict__ out,
-                                                        int64_t rows, int n, int act) {
+                                                        const float* __restrict__ bias, const void* residual,
+                                                        void* out, int64_t rows, int n, int act) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= rows * n) return;
   float v = split_sum(y + i, nsplit, split_stride);
   if (bias) v += bias[i % n];
+  if (residual) {
+    // the reference rounds the attention output, then adds
+    // (transformer_layer_moe_decode.mlir:208-221)
+    if (act == DT_BF16) v = bf16_to_f32(f32_to_bf16(v));
+    v += load_act(residual, act, i);
+  }
   store_act(out, act, i, v);
 }
 
@@ -604,12 +611,12 @@ hipError_t launch_qkv_rope(const float* qkv, int nsplit, int64_t split_stride, c
   return hipGetLastError();
 }
 
-hipError_t launch_bias_cast(const float* y, int nsplit, int64_t split_stride, const float* bias, void* out,
-                            int64_t rows, int n, int act, hipStream_t s) {
+hipError_t launch_bias_cast(const float* y, int nsplit, int64_t split_stride, const float* bias, const void* residual,
+                            void* out, int64_t rows, int n, int act, hipStream_t s) {
   const int64_t total = rows * n;
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(bias_cast_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, y, nsplit,
-                     split_stride, bias, out, rows, n, act);
+                     split_stride, bias, residual, out, rows, n, act);
   return hipGetLastError();
 }
 

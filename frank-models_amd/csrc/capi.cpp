@@ -609,7 +609,7 @@ struct AttnWeights {
 int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, const int64_t* positions,
                   const void* k_pool, const void* v_pool, int64_t n_blocks, int block_size, const int* tables,
                   int max_blocks, const int* lens, int max_ctx, int act, void* out, void* k_new, void* v_new,
-                  void* workspace, const AttnLayout& L, hipStream_t s) {
+                  void* workspace, const AttnLayout& L, hipStream_t s, const void* residual = nullptr) {
   const int B = static_cast<int>(a.B);
   const int nq = static_cast<int>(a.n_embd), nkv = static_cast<int>(a.n_embd_kv);
   int* order = at<int>(workspace, L.order);
@@ -640,7 +640,8 @@ int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, c
     ScopedTimer t(FMOE_TIMER_OUT_PROJ, s);
     int ns = 1;
     FMOE_TRY(run_linear(attn, a.n_embd, w.wo, w.wo_scales, w.w_dtype, nq, y, B, act, order, offsets, s, &ns));
-    FMOE_HIP(launch_bias_cast(y, ns, static_cast<int64_t>(B) * nq, bias ? w.bo : nullptr, out, B, nq, act, s));
+    FMOE_HIP(launch_bias_cast(y, ns, static_cast<int64_t>(B) * nq, bias ? w.bo : nullptr, residual, out, B, nq, act,
+                              s));
   }
   return FMOE_OK;
 }
@@ -1137,6 +1138,18 @@ size_t fmoe_attention_decode_paged_workspace_bytes(int64_t batch, int64_t max_co
                                                      act_dtype);
 }
 
+static int attention_paged(const void* input, const void* residual, const void* norm_w, float rms_eps,
+                           const int64_t* positions, void* k_cache, void* v_cache, int64_t n_blocks,
+                           int64_t block_size, int64_t layer, const int32_t* block_tables,
+                           const int32_t* context_lens, int64_t n_layers, int64_t max_blocks_per_seq,
+                           int64_t max_context_len, const int32_t* block_indices, const int32_t* pos_in_blocks,
+                           const void* packed_wqkv, const float* wqkv_scales, const void* packed_wo,
+                           const float* wo_scales, int w_dtype, const float* bq, const float* bk, const float* bv,
+                           const float* bo, int use_bias, int64_t batch, int64_t n_head, int64_t n_head_kv,
+                           int64_t n_embd, int64_t n_embd_kv, float rope_freq_base, float rope_freq_scale,
+                           int act_dtype, void* out, void* k_new, void* v_new, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 int fmoe_attention_decode_paged(const void* input, const int64_t* positions, void* k_cache, void* v_cache,
                                 int64_t n_blocks, int64_t block_size, int64_t layer, const int32_t* block_tables,
                                 const int32_t* context_lens, int64_t n_layers, int64_t max_blocks_per_seq,
@@ -1147,6 +1160,60 @@ int fmoe_attention_decode_paged(const void* input, const int64_t* positions, voi
                                 int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv, float rope_freq_base,
                                 float rope_freq_scale, int act_dtype, void* out, void* k_new, void* v_new,
                                 void* workspace, size_t workspace_bytes, void* stream) {
+  return attention_paged(input, nullptr, nullptr, 0.f, positions, k_cache, v_cache, n_blocks, block_size, layer,
+                         block_tables, context_lens, n_layers, max_blocks_per_seq, max_context_len, block_indices,
+                         pos_in_blocks, packed_wqkv, wqkv_scales, packed_wo, wo_scales, w_dtype, bq, bk, bv, bo,
+                         use_bias, batch, n_head, n_head_kv, n_embd, n_embd_kv, rope_freq_base, rope_freq_scale,
+                         act_dtype, out, k_new, v_new, workspace, workspace_bytes, stream);
+}
+
+size_t fmoe_attention_sublayer_decode_paged_workspace_bytes(int64_t batch, int64_t max_context_len, int64_t n_head,
+                                                            int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv,
+                                                            int act_dtype) {
+  const size_t base = fmoe_attention_block_decode_workspace_bytes(batch, max_context_len, n_head, n_head_kv, n_embd,
+                                                                  n_embd_kv, act_dtype);
+  if (base == 0) return 0;
+  return base + align_up(static_cast<size_t>(batch) * n_embd * dtype_bytes(act_dtype));
+}
+
+int fmoe_attention_sublayer_decode_paged(const void* residual, const void* attn_norm_w, float rms_eps,
+                                         const int64_t* positions, void* k_cache, void* v_cache, int64_t n_blocks,
+                                         int64_t block_size, int64_t layer, const int32_t* block_tables,
+                                         const int32_t* context_lens, int64_t n_layers, int64_t max_blocks_per_seq,
+                                         int64_t max_context_len, const int32_t* block_indices,
+                                         const int32_t* pos_in_blocks, const void* packed_wqkv,
+                                         const float* wqkv_scales, const void* packed_wo, const float* wo_scales,
+                                         int w_dtype, const float* bq, const float* bk, const float* bv,
+                                         const float* bo, int use_bias, int64_t batch, int64_t n_head,
+                                         int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv, float rope_freq_base,
+                                         float rope_freq_scale, int act_dtype, void* out, void* k_new, void* v_new,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch > 0 && (!residual || !attn_norm_w)) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  if (batch > 0 && !aligned_for(attn_norm_w, act_dtype)) return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
+  return attention_paged(residual, residual, attn_norm_w, rms_eps, positions, k_cache, v_cache, n_blocks, block_size,
+                         layer, block_tables, context_lens, n_layers, max_blocks_per_seq, max_context_len,
+                         block_indices, pos_in_blocks, packed_wqkv, wqkv_scales, packed_wo, wo_scales, w_dtype, bq,
+                         bk, bv, bo, use_bias, batch, n_head, n_head_kv, n_embd, n_embd_kv, rope_freq_base,
+                         rope_freq_scale, act_dtype, out, k_new, v_new, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// Shared by the paged attention and the attention sub-layer: norm_w non-null
+// normalises `input` into the workspace first (attn_norm,
+// transformer_layer_moe_decode.mlir:174-177) and `residual` is added to the
+// output (:208-221).
+static int attention_paged(const void* input, const void* residual, const void* norm_w, float rms_eps,
+                           const int64_t* positions, void* k_cache, void* v_cache, int64_t n_blocks,
+                           int64_t block_size, int64_t layer, const int32_t* block_tables,
+                           const int32_t* context_lens, int64_t n_layers, int64_t max_blocks_per_seq,
+                           int64_t max_context_len, const int32_t* block_indices, const int32_t* pos_in_blocks,
+                           const void* packed_wqkv, const float* wqkv_scales, const void* packed_wo,
+                           const float* wo_scales, int w_dtype, const float* bq, const float* bk, const float* bv,
+                           const float* bo, int use_bias, int64_t batch, int64_t n_head, int64_t n_head_kv,
+                           int64_t n_embd, int64_t n_embd_kv, float rope_freq_base, float rope_freq_scale,
+                           int act_dtype, void* out, void* k_new, void* v_new, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   if (n_head < 1 || n_embd < 1) return fail(FMOE_ERR_SHAPE, "n_head and n_embd must be positive");
   const AttnShape a{batch, n_head, n_head_kv, n_embd, n_embd_kv, n_embd / n_head};
   FMOE_TRY(validate_attn_shape(a, act_dtype, w_dtype));
@@ -1168,15 +1235,25 @@ int fmoe_attention_decode_paged(const void* input, const int64_t* positions, voi
       (v_new && !aligned_for(v_new, act_dtype)))
     return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
   const AttnLayout L = attn_layout(a, max_context_len, act_dtype);
-  FMOE_TRY(check_workspace(workspace, workspace_bytes, L.total));
+  const size_t xn_off = L.total;
+  const size_t need = norm_w ? xn_off + align_up(static_cast<size_t>(batch) * n_embd * dtype_bytes(act_dtype))
+                             : L.total;
+  FMOE_TRY(check_workspace(workspace, workspace_bytes, need));
   FMOE_TRY(ensure_device());
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* kn = k_new ? k_new : at<char>(workspace, L.k_new);
   void* vn = v_new ? v_new : at<char>(workspace, L.v_new);
-  FMOE_TRY(run_attention(a, w, input, positions, k_cache, v_cache, n_blocks, static_cast<int>(block_size),
+  const void* x = input;
+  if (norm_w) {
+    void* xn = at<char>(workspace, xn_off);
+    ScopedTimer t(FMOE_TIMER_NORM, s);
+    FMOE_HIP(launch_rms_norm(input, norm_w, rms_eps, xn, batch, static_cast<int>(n_embd), act_dtype, s));
+    x = xn;
+  }
+  FMOE_TRY(run_attention(a, w, x, positions, k_cache, v_cache, n_blocks, static_cast<int>(block_size),
                          block_tables + layer * batch * max_blocks_per_seq, static_cast<int>(max_blocks_per_seq),
                          context_lens + layer * batch, static_cast<int>(max_context_len), act_dtype, out, kn, vn,
-                         workspace, L, s));
+                         workspace, L, s, residual));
   // scatter_decode after the attention has read the pools
   // (transformer_layer_moe_decode.mlir:202-206).
   const int rb = static_cast<int>(n_embd_kv * dtype_bytes(act_dtype));
@@ -1184,5 +1261,3 @@ int fmoe_attention_decode_paged(const void* input, const int64_t* positions, voi
                                      block_indices, pos_in_blocks, static_cast<int>(batch), s));
   return ok();
 }
-
-}  // extern "C"

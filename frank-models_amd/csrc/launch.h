@@ -202,9 +202,10 @@ hipError_t launch_qkv_rope(const float* qkv, int nsplit, int64_t split_stride, c
                            const float* bv, const int64_t* positions, int batch, int nq, int nkv, int head_dim,
                            double freq_base, double freq_scale, float* q_rot, void* k_new, void* v_new, int act,
                            hipStream_t s);
-// out[r, :] = sum of the nsplit partials y[r, :] (+ bias) in act dtype.
-hipError_t launch_bias_cast(const float* y, int nsplit, int64_t split_stride, const float* bias, void* out,
-                            int64_t rows, int n, int act, hipStream_t s);
+// out[r, :] = sum of the nsplit partials y[r, :] (+ bias) in act dtype,
+// then + residual[r, :] (optional; out may alias it).
+hipError_t launch_bias_cast(const float* y, int nsplit, int64_t split_stride, const float* bias, const void* residual,
+                            void* out, int64_t rows, int n, int act, hipStream_t s);
 // Head sizes and query-per-KV-head groups the attention kernels take.
 bool attn_decode_supported(int head_dim, int group);
 // Context splits of the attention (part holds batch * n_head * splits *

@@ -344,6 +344,34 @@ int fmoe_attention_decode_paged(const void *input, const int64_t *positions, voi
                                 void *out, void *k_new, void *v_new, void *workspace,
                                 size_t workspace_bytes, void *stream);
 
+/* The decode layer's attention sub-layer: out = residual +
+ * attention_decode_paged(rms_norm(residual, attn_norm_w, rms_eps), ...)
+ * (architectures/llm/transformer_layer_moe_decode.mlir:174-221: attn_norm,
+ * gather, attention_block_decode, scatter_decode, residual add), the
+ * attention-half counterpart of fmoe_moe_ffn_sublayer.  The attention output
+ * is rounded to act_dtype before the add, as the reference adds two tensors.
+ * out may alias residual.  Arguments otherwise as fmoe_attention_decode_paged. */
+size_t fmoe_attention_sublayer_decode_paged_workspace_bytes(int64_t batch, int64_t max_context_len,
+                                                            int64_t n_head, int64_t n_head_kv,
+                                                            int64_t n_embd, int64_t n_embd_kv,
+                                                            int act_dtype);
+int fmoe_attention_sublayer_decode_paged(const void *residual, const void *attn_norm_w,
+                                         float rms_eps, const int64_t *positions, void *k_cache,
+                                         void *v_cache, int64_t n_blocks, int64_t block_size,
+                                         int64_t layer, const int32_t *block_tables,
+                                         const int32_t *context_lens, int64_t n_layers,
+                                         int64_t max_blocks_per_seq, int64_t max_context_len,
+                                         const int32_t *block_indices,
+                                         const int32_t *pos_in_blocks, const void *packed_wqkv,
+                                         const float *wqkv_scales, const void *packed_wo,
+                                         const float *wo_scales, int w_dtype, const float *bq,
+                                         const float *bk, const float *bv, const float *bo,
+                                         int use_bias, int64_t batch, int64_t n_head,
+                                         int64_t n_head_kv, int64_t n_embd, int64_t n_embd_kv,
+                                         float rope_freq_base, float rope_freq_scale,
+                                         int act_dtype, void *out, void *k_new, void *v_new,
+                                         void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,9 @@ INFRASTRUCTURE ONLY (see the package docstring for who may import it).
   ``scatter_decode`` of the new K/V.  Because gather zero-fills and the
   attention has no mask, each position in ``[min(ctx_len, max_ctx),
   max_ctx)`` enters the softmax as a key of zeros (score 0, value 0).
+* ``attention_sublayer_decode_paged``: attn_norm RMSNorm (layer.rms_norm),
+  the paged decode above, residual add
+  (transformer_layer_moe_decode.mlir:174-221).
 """
 
 from __future__ import annotations
@@ -130,3 +133,20 @@ def attention_decode_paged(x, positions, k_cache, v_cache, layer, block_tables, 
     kc2 = kv_scatter_decode(k_cache, k_new.astype(k_cache.dtype), block_indices, pos_in_blocks)
     vc2 = kv_scatter_decode(v_cache, v_new.astype(v_cache.dtype), block_indices, pos_in_blocks)
     return out, k_new, v_new, kc2, vc2
+
+
+def attention_sublayer_decode_paged(residual, attn_norm_w, rms_eps, positions, k_cache, v_cache, layer,
+                                    block_tables, context_lens, max_context_len, block_indices, pos_in_blocks, wq, wk,
+                                    wv, wo, bq, bk, bv, bo, use_bias, n_head, n_head_kv, n_embd,
+                                    freq_base=10000.0, freq_scale=1.0, dtype=np.float64):
+    """The decode layer's attention sub-layer (transformer_layer_moe_decode.mlir:174-221):
+    attn_norm RMSNorm, the paged attention, residual add.  Returns
+    ``(out, k_new, v_new, k_cache', v_cache')``."""
+    from .layer import rms_norm
+
+    xn = rms_norm(residual, attn_norm_w, rms_eps, dtype=dtype)
+    out, k_new, v_new, kc, vc = attention_decode_paged(xn, positions, k_cache, v_cache, layer, block_tables,
+                                                       context_lens, max_context_len, block_indices, pos_in_blocks,
+                                                       wq, wk, wv, wo, bq, bk, bv, bo, use_bias, n_head, n_head_kv,
+                                                       n_embd, freq_base, freq_scale, dtype)
+    return np.asarray(residual, dtype) + out, k_new, v_new, kc, vc

@@ -264,3 +264,48 @@ def test_paged_equals_gather_then_block(fm):
     torch.cuda.synchronize()
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
     assert_close_rms(_host(o2), _host(o1), 1e-5)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_attention_sublayer_decode_paged(fm, dt):
+    """attn_norm + paged attention + residual add in one call; in place
+    (out=residual) equals out of place bit for bit."""
+    rng = np.random.default_rng(31)
+    tdt = DT[dt]
+    B, n_embd, H, Hkv, bs, n_blocks, max_ctx = 3, 256, 8, 2, 16, 40, 100
+    D = n_embd // H
+    tables = rng.permutation(n_blocks)[: B * 8].reshape(1, B, 8).astype(np.int32)
+    lens = np.array([[100, 37, 64]], np.int32)
+    kp = _round(rng.standard_normal((n_blocks, bs, Hkv, D)), tdt)
+    vp = _round(rng.standard_normal((n_blocks, bs, Hkv, D)), tdt)
+    bi = np.array([tables[0, b, 7] for b in range(B)], np.int32)
+    pi = np.array([15, 15, 15], np.int32)
+    w, b, hw = _weights(rng, n_embd, Hkv * D, tdt)
+    res = _round(rng.standard_normal((B, n_embd)), tdt)
+    nw = _round(rng.standard_normal(n_embd) * 0.5 + 1.0, tdt)
+    pos = np.array([100, 37, 64], np.int64)
+    blk = fm.AttentionBlockDecode(*(_dev(w[k], tdt) for k in ("wq", "wk", "wv", "wo")),
+                                  *(torch.from_numpy(b[k]).cuda() for k in ("bq", "bk", "bv", "bo")),
+                                  use_bias=True, n_head=H, n_head_kv=Hkv, n_embd=n_embd, act_dtype=tdt)
+    kd, vd = _dev(kp, tdt), _dev(vp, tdt)
+    r = _dev(res, tdt)
+    out, k_new, _ = blk.paged_sublayer(r, _dev(nw, tdt), 1e-5, torch.from_numpy(pos).cuda(), kd, vd, 0, tables,
+                                       lens, max_ctx, bi, pi)
+    torch.cuda.synchronize()
+    ref = oa.attention_sublayer_decode_paged(res, nw, 1e-5, pos, kp, vp, 0, tables, lens, max_ctx, bi, pi, hw["wq"],
+                                             hw["wk"], hw["wv"], hw["wo"], b["bq"], b["bk"], b["bv"], b["bo"], True, H,
+                                             Hkv, n_embd)
+    rtol = 1e-4 if dt == "f32" else 2e-2
+    assert_close_rms(_host(out), ref[0], rtol, what=f"sub-layer {dt}")
+    if dt == "f32":
+        # the attention part on its own (a bf16 sum's rounding is relative to
+        # the residual, so this is checked in fp32 only)
+        assert_close_rms(_host(out) - res, ref[0] - res, rtol, what="sub-layer attention part")
+    # in place on the same pools (pools restored first: the call wrote the new K/V)
+    kd2, vd2 = _dev(kp, tdt), _dev(vp, tdt)
+    r2 = _dev(res, tdt)
+    out2, _, _ = blk.paged_sublayer(r2, _dev(nw, tdt), 1e-5, torch.from_numpy(pos).cuda(), kd2, vd2, 0, tables, lens,
+                                    max_ctx, bi, pi, out=r2)
+    torch.cuda.synchronize()
+    assert out2.data_ptr() == r2.data_ptr()
+    assert torch.equal(out2, out)

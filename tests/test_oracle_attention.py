@@ -233,3 +233,23 @@ def test_paged_decode_is_gather_block_scatter_with_zero_rows():
     untouched = np.ones(6 * bs, bool).reshape(6, bs)
     untouched[5, 2] = untouched[3, 3] = False
     np.testing.assert_array_equal(kc2[untouched], kp[untouched])
+
+
+def test_attention_sublayer_is_norm_then_paged_then_residual():
+    from oracle import layer as ol
+
+    rng = np.random.default_rng(10)
+    n_embd, H, Hkv, bs = 16, 4, 2, 4
+    D = n_embd // H
+    a = _block_inputs(rng, 2, 0, n_embd, H, Hkv, bias=False)
+    kp, vp = _pool(rng, 6, bs, Hkv, D), _pool(rng, 6, bs, Hkv, D)
+    tables = np.array([[[2, 5, 0], [1, 3, 4]]], np.int32)
+    lens = np.array([[6, 3]], np.int32)
+    nw = rng.standard_normal(n_embd)
+    args = (a["positions"], kp, vp, 0, tables, lens, 7, np.array([5, 3]), np.array([2, 3]), a["wq"], a["wk"],
+            a["wv"], a["wo"], None, None, None, None, False, H, Hkv, n_embd)
+    got = oa.attention_sublayer_decode_paged(a["x"], nw, 1e-5, *args)
+    xn = ol.rms_norm(a["x"], nw, 1e-5)
+    want = oa.attention_decode_paged(xn, *args)
+    np.testing.assert_allclose(got[0], a["x"] + want[0], rtol=1e-14)
+    np.testing.assert_array_equal(got[3], want[3])
