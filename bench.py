@@ -25,7 +25,9 @@ The JSON line carries:
                         timed on this host on a bounded token sample
   attention_decode      the decode step's attention half at Mixtral's attention
                         shape (16 sequences x 4096 cached positions, paged
-                        bf16 KV): ms/step, per-phase times, KV-read GB/s
+                        bf16 KV): ms/step, per-phase times, KV-read GB/s;
+                        decode_layer: that attention sub-layer followed by the
+                        C2 MoE sub-layer on the same 16 tokens
 """
 
 from __future__ import annotations
@@ -189,7 +191,7 @@ def all_configs(fm, wl, torch, args):
     return rows
 
 
-def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16, cpu_sample=0):
+def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16, cpu_sample=0, moe=None):
     """The decode step's attention half at Mixtral-8x7B's attention shape
     (n_embd 4096, 32 query heads, 8 KV heads, head_dim 128), bf16: one new
     token per sequence for `batch` sequences, each with `ctx` cached
@@ -250,6 +252,31 @@ def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16, cpu_sa
         res["qkv_GBps"] = qkv_bytes / (kern["qkv"] * 1e-3) / 1e9
     if kern.get("out_proj"):
         res["out_proj_GBps"] = out_bytes / (kern["out_proj"] * 1e-3) / 1e9
+    if moe is not None:
+        # One whole decode layer body (transformer_layer_moe_decode.mlir:174-255):
+        # the attention sub-layer then the MoE sub-layer, both in place on the
+        # residual stream of the same `batch` tokens.
+        wr, packed, cfg = moe
+        moe_blk = fm.MoEFFNBlock(wr, *packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                                 cfg.normalize, act_dtype=bf)
+        resid = rnd(batch, n_embd)
+        nw = torch.ones(n_embd, dtype=bf, device="cuda")
+
+        def layer():
+            blk.paged_sublayer(resid, nw, 1e-5, pos, kp, vp, 0, tables, lens, ctx, bi, pi, out=resid)
+            moe_blk.sublayer(resid, nw, 1e-5, out=resid)
+
+        for _ in range(warmup):
+            layer()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            layer()
+        torch.cuda.synchronize()
+        lms = (time.perf_counter() - t0) / steps * 1e3
+        res["decode_layer"] = {"ms_per_step": lms, "tokens_per_s": batch / (lms * 1e-3),
+                               "what": f"attention sub-layer ({batch} sequences x {ctx} positions) + MoE "
+                                       f"sub-layer ({cfg.name}, {batch} tokens), in place on one residual stream"}
     if cpu_sample:
         res["cpu_baseline"] = attention_cpu_baseline(torch, blk, x, pos, kp, vp, tables, lens, ctx, bi, pi, cpu_sample)
     return res
@@ -388,9 +415,11 @@ def main():
 
     if not args.no_attention:
         log(f"attention decode: batch {args.attn_batch}, context {args.attn_context}")
+        wr = torch.from_numpy(pre["wr_np"]).to("cuda", torch.bfloat16)
         result["attention_decode"] = attention_decode(fm, torch, args.attn_batch, args.attn_context,
                                                       max(args.steps, 20), args.warmup,
-                                                      cpu_sample=0 if args.no_cpu_baseline else 2)
+                                                      cpu_sample=0 if args.no_cpu_baseline else 2,
+                                                      moe=(wr, pre["weights"][1], cfg))
         log(f"attention decode {result['attention_decode']['ms_per_step']:.3f} ms/step, "
             f"kernels(ms) {result['attention_decode']['kernels_ms']}")
 
