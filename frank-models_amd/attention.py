@@ -177,10 +177,12 @@ class AttentionBlockDecode:
         self.head_dim = self.n_embd // self.n_head
         self._ws = None
 
-    def _get_ws(self, batch, ctx):
-        nbytes = L.lib().fmoe_attention_block_decode_workspace_bytes(batch, ctx, self.n_head, self.n_head_kv,
-                                                                     self.n_embd, self.n_embd_kv, self.act)
-        if self._ws is None or self._ws.numel() < nbytes or self._ws.device != torch.device("cuda", torch.cuda.current_device()):
+    def _get_ws(self, batch, ctx, sublayer=False):
+        fn = ("fmoe_attention_sublayer_decode_paged_workspace_bytes" if sublayer
+              else "fmoe_attention_block_decode_workspace_bytes")
+        nbytes = getattr(L.lib(), fn)(batch, ctx, self.n_head, self.n_head_kv, self.n_embd, self.n_embd_kv, self.act)
+        dev = torch.device("cuda", torch.cuda.current_device())
+        if self._ws is None or self._ws.numel() < nbytes or self._ws.device != dev:
             self._ws = _workspace(nbytes)
         return self._ws
 
@@ -218,14 +220,9 @@ class AttentionBlockDecode:
                _ptr(out), _ptr(k_new), _ptr(v_new), _ptr(ws), ws.numel(), _stream())
         return out, k_new, v_new
 
-    def paged(self, x, positions, k_cache, v_cache, layer, block_tables, context_lens, max_context_len,
-              block_indices, pos_in_blocks):
-        """Attention of one new token per sequence over the paged pools
-        ``[n_blocks, block_size, n_head_kv, head_dim]`` (updated in place with
-        the new K/V) -> ``(out, k_new, v_new)``."""
-        x, pos = self._x(x, positions)
-        B = int(x.shape[0])
-        dt = x.dtype
+    def _paged_args(self, B, dt, k_cache, v_cache, block_tables, context_lens, block_indices, pos_in_blocks):
+        """Checks the pools and paging metadata of a paged call; returns the
+        device int32 tensors (tables, lens, block indices, positions in block)."""
         for name, p in (("k_cache", k_cache), ("v_cache", v_cache)):
             if not isinstance(p, torch.Tensor) or p.dtype != dt or p.device.type != "cuda" or not p.is_contiguous():
                 raise TypeError(f"{name} must be a contiguous {dt} device tensor")
@@ -239,18 +236,34 @@ class AttentionBlockDecode:
             raise ValueError("block_tables [n_layers, batch, max_blocks] and context_lens [n_layers, batch] expected")
         if int(bi.numel()) != B or int(pi.numel()) != B:
             raise ValueError("block_indices and pos_in_blocks must be [batch]")
-        n_blocks, bs = int(k_cache.shape[0]), int(k_cache.shape[1])
+        return bt, cl, bi, pi
+
+    def _paging(self, k_cache, v_cache, layer, bt, cl, max_context_len, bi, pi):
+        """The C ABI's pool and paging arguments, from k_cache to pos_in_blocks."""
+        return (_ptr(k_cache), _ptr(v_cache), int(k_cache.shape[0]), int(k_cache.shape[1]), int(layer), _ptr(bt),
+                _ptr(cl), int(bt.shape[0]), int(bt.shape[2]), int(max_context_len), _ptr(bi), _ptr(pi))
+
+    def _tail(self, B, out, k_new, v_new, ws):
+        return (B, self.n_head, self.n_head_kv, self.n_embd, self.n_embd_kv, self.freq_base, self.freq_scale,
+                self.act, _ptr(out), _ptr(k_new), _ptr(v_new), _ptr(ws), ws.numel(), _stream())
+
+    def paged(self, x, positions, k_cache, v_cache, layer, block_tables, context_lens, max_context_len,
+              block_indices, pos_in_blocks):
+        """Attention of one new token per sequence over the paged pools
+        ``[n_blocks, block_size, n_head_kv, head_dim]`` (updated in place with
+        the new K/V) -> ``(out, k_new, v_new)``."""
+        x, pos = self._x(x, positions)
+        B, dt = int(x.shape[0]), x.dtype
+        bt, cl, bi, pi = self._paged_args(B, dt, k_cache, v_cache, block_tables, context_lens, block_indices,
+                                          pos_in_blocks)
         out = torch.empty((B, self.n_embd), dtype=dt, device=x.device)
         k_new = torch.empty((B, self.n_head_kv, self.head_dim), dtype=dt, device=x.device)
         v_new = torch.empty_like(k_new)
         ws = self._get_ws(B, int(max_context_len))
-        L.call("fmoe_attention_decode_paged", _ptr(x), _ptr(pos), _ptr(k_cache), _ptr(v_cache), n_blocks, bs,
-               int(layer), _ptr(bt), _ptr(cl), int(bt.shape[0]), int(bt.shape[2]), int(max_context_len), _ptr(bi),
-               _ptr(pi), *self._weights(), B, self.n_head, self.n_head_kv, self.n_embd, self.n_embd_kv,
-               self.freq_base, self.freq_scale, self.act, _ptr(out), _ptr(k_new), _ptr(v_new), _ptr(ws), ws.numel(),
-               _stream())
+        L.call("fmoe_attention_decode_paged", _ptr(x), _ptr(pos),
+               *self._paging(k_cache, v_cache, layer, bt, cl, max_context_len, bi, pi), *self._weights(),
+               *self._tail(B, out, k_new, v_new, ws))
         return out, k_new, v_new
-
 
     def paged_sublayer(self, residual, attn_norm_w, rms_eps, positions, k_cache, v_cache, layer, block_tables,
                        context_lens, max_context_len, block_indices, pos_in_blocks, out=None):
@@ -259,41 +272,23 @@ class AttentionBlockDecode:
         ``out=residual`` updates the residual stream in place.  Returns
         ``(out, k_new, v_new)``."""
         x, pos = self._x(residual, positions)
-        B = int(x.shape[0])
-        dt = x.dtype
+        B, dt = int(x.shape[0]), x.dtype
         nw, _ = _to_device(attn_norm_w, "attn_norm_w")
         nw = nw.to(dt).contiguous()
         if tuple(nw.shape) != (self.n_embd,):
             raise ValueError(f"attn_norm_w must be [{self.n_embd}]")
-        for name, p in (("k_cache", k_cache), ("v_cache", v_cache)):
-            if not isinstance(p, torch.Tensor) or p.dtype != dt or p.device.type != "cuda" or not p.is_contiguous():
-                raise TypeError(f"{name} must be a contiguous {dt} device tensor")
-            if p.dim() != 4 or tuple(p.shape[2:]) != (self.n_head_kv, self.head_dim):
-                raise ValueError(f"{name} must be [n_blocks, block_size, {self.n_head_kv}, {self.head_dim}]")
-        bt = _ints_to_device(block_tables, "block_tables")
-        cl = _ints_to_device(context_lens, "context_lens")
-        bi = _ints_to_device(block_indices, "block_indices")
-        pi = _ints_to_device(pos_in_blocks, "pos_in_blocks")
-        if bt.dim() != 3 or int(bt.shape[1]) != B or tuple(cl.shape) != tuple(bt.shape[:2]):
-            raise ValueError("block_tables [n_layers, batch, max_blocks] and context_lens [n_layers, batch] expected")
-        if int(bi.numel()) != B or int(pi.numel()) != B:
-            raise ValueError("block_indices and pos_in_blocks must be [batch]")
+        bt, cl, bi, pi = self._paged_args(B, dt, k_cache, v_cache, block_tables, context_lens, block_indices,
+                                          pos_in_blocks)
         if out is None:
             out = torch.empty((B, self.n_embd), dtype=dt, device=x.device)
         elif out.dtype != dt or tuple(out.shape) != (B, self.n_embd) or not out.is_contiguous():
             raise ValueError(f"out must be a contiguous {dt} [{B}, {self.n_embd}] tensor")
         k_new = torch.empty((B, self.n_head_kv, self.head_dim), dtype=dt, device=x.device)
         v_new = torch.empty_like(k_new)
-        nbytes = L.lib().fmoe_attention_sublayer_decode_paged_workspace_bytes(
-            B, int(max_context_len), self.n_head, self.n_head_kv, self.n_embd, self.n_embd_kv, self.act)
-        if self._ws is None or self._ws.numel() < nbytes:
-            self._ws = _workspace(nbytes)
-        ws = self._ws
-        L.call("fmoe_attention_sublayer_decode_paged", _ptr(x), _ptr(nw), float(rms_eps), _ptr(pos), _ptr(k_cache),
-               _ptr(v_cache), int(k_cache.shape[0]), int(k_cache.shape[1]), int(layer), _ptr(bt), _ptr(cl),
-               int(bt.shape[0]), int(bt.shape[2]), int(max_context_len), _ptr(bi), _ptr(pi), *self._weights(), B,
-               self.n_head, self.n_head_kv, self.n_embd, self.n_embd_kv, self.freq_base, self.freq_scale, self.act,
-               _ptr(out), _ptr(k_new), _ptr(v_new), _ptr(ws), ws.numel(), _stream())
+        ws = self._get_ws(B, int(max_context_len), sublayer=True)
+        L.call("fmoe_attention_sublayer_decode_paged", _ptr(x), _ptr(nw), float(rms_eps), _ptr(pos),
+               *self._paging(k_cache, v_cache, layer, bt, cl, max_context_len, bi, pi), *self._weights(),
+               *self._tail(B, out, k_new, v_new, ws))
         return out, k_new, v_new
 
 
