@@ -46,30 +46,33 @@ __global__ __launch_bounds__(kCopyThreads) void kv_gather_kernel(const uint32_t*
   for (int w = threadIdx.x; w < row_words; w += kCopyThreads) dst[w] = src ? src[w] : 0u;
 }
 
-// One row per sequence; when several sequences name the same slot the last
-// one wins, as in the reference's sequential loop (oracles/kvcache.py:134-139).
-// blockIdx.y selects the pool (cache, vals) or (cache2, vals2).
-__global__ __launch_bounds__(kCopyThreads) void kv_scatter_decode_kernel(uint32_t* __restrict__ cache,
-                                                                         uint32_t* __restrict__ cache2, int64_t n_blocks,
-                                                                         int block_size, int row_words,
-                                                                         const uint32_t* __restrict__ vals,
-                                                                         const uint32_t* __restrict__ vals2,
-                                                                         const int* __restrict__ block_idx,
-                                                                         const int* __restrict__ pos_idx, int batch) {
-  if (blockIdx.y == 1) {
-    cache = cache2;
-    vals = vals2;
-  }
-  const int b = blockIdx.x;
+// Sequence b's new row into slot (block_idx[b], pos_idx[b]) of `cache`, by
+// a whole block of NT threads.  When several sequences name the same slot
+// the last one wins, as in the reference's sequential loop
+// (oracles/kvcache.py:134-139); slots outside the pool are skipped.
+template <int NT>
+__device__ void scatter_decode_row(uint32_t* __restrict__ cache, int64_t n_blocks, int block_size, int row_words,
+                                   const uint32_t* __restrict__ vals, const int* __restrict__ block_idx,
+                                   const int* __restrict__ pos_idx, int batch, int b) {
   const int bi = block_idx[b], p = pos_idx[b];
   bool later = false;
-  for (int b2 = b + 1 + static_cast<int>(threadIdx.x); b2 < batch; b2 += kCopyThreads)
+  for (int b2 = b + 1 + static_cast<int>(threadIdx.x); b2 < batch; b2 += NT)
     later |= block_idx[b2] == bi && pos_idx[b2] == p;
   if (__syncthreads_or(later)) return;
   if (bi < 0 || bi >= n_blocks || p < 0 || p >= block_size) return;
   uint32_t* dst = cache + (static_cast<int64_t>(bi) * block_size + p) * row_words;
   const uint32_t* src = vals + static_cast<int64_t>(b) * row_words;
-  for (int w = threadIdx.x; w < row_words; w += kCopyThreads) dst[w] = src[w];
+  for (int w = threadIdx.x; w < row_words; w += NT) dst[w] = src[w];
+}
+
+__global__ __launch_bounds__(kCopyThreads) void kv_scatter_decode_kernel(uint32_t* __restrict__ cache,
+                                                                         int64_t n_blocks, int block_size,
+                                                                         int row_words,
+                                                                         const uint32_t* __restrict__ vals,
+                                                                         const int* __restrict__ block_idx,
+                                                                         const int* __restrict__ pos_idx, int batch) {
+  scatter_decode_row<kCopyThreads>(cache, n_blocks, block_size, row_words, vals, block_idx, pos_idx, batch,
+                                   blockIdx.x);
 }
 
 __global__ __launch_bounds__(kCopyThreads) void kv_scatter_prefill_kernel(
@@ -469,13 +472,23 @@ constexpr int kCombineThreads = 128;  // >= head_dim
 constexpr int kCombineChunk = 1024;   // splits whose weights are held in LDS at once
 constexpr int kCombineUnroll = 8;
 
+// Blocks x = n_head and n_head + 1 (launched only with a scatter) write
+// k_new / v_new into the pools: the split kernel has read them by then.
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a, int D,
                                                                        const void* __restrict__ k_new,
                                                                        const void* __restrict__ v_new, int act,
-                                                                       void* __restrict__ out) {
+                                                                       void* __restrict__ out, KvScatterDecode sc) {
   __shared__ float wts[kCombineChunk];
   __shared__ float stat[3];  // M, 1 / l, exp(s_new - M) / l
   const int h = blockIdx.x, b = blockIdx.y;
+  if (h >= a.n_head) {  // block-uniform
+    const bool v = h > a.n_head;
+    scatter_decode_row<kCombineThreads>(static_cast<uint32_t*>(v ? sc.v_cache : sc.k_cache), sc.n_blocks,
+                                        sc.block_size, sc.row_bytes / 4,
+                                        static_cast<const uint32_t*>(v ? v_new : k_new), sc.block_idx, sc.pos_idx,
+                                        static_cast<int>(gridDim.y), b);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int kvh = h / (a.n_head / a.n_head_kv);
   const int n_b = min(max(a.ctx_lens[b], 0), a.max_ctx);
@@ -570,8 +583,12 @@ int attn_decode_splits(int max_ctx) { return (max_ctx + kSplitLen - 1) / kSplitL
 hipError_t launch_attn_decode(const float* q_rot, const void* k_pool, const void* v_pool, int64_t n_blocks,
                               int block_size, const int* tables, int max_blocks, const int* ctx_lens, int max_ctx,
                               const void* k_new, const void* v_new, int batch, int n_head, int n_head_kv,
-                              int head_dim, int dtype, float scale, float* part, void* out, hipStream_t s) {
+                              int head_dim, int dtype, float scale, float* part, void* out, hipStream_t s,
+                              const KvScatterDecode* scatter) {
   if (!attn_decode_supported(head_dim, n_head / n_head_kv) || n_head % n_head_kv) return hipErrorNotSupported;
+  if (scatter && (scatter->row_bytes % 4 || !scatter->k_cache || !scatter->v_cache || !scatter->block_idx ||
+                  !scatter->pos_idx))
+    return hipErrorInvalidValue;
   if (batch == 0) return hipSuccess;
   AttnArgs a;
   a.q = q_rot;
@@ -594,8 +611,8 @@ hipError_t launch_attn_decode(const float* q_rot, const void* k_pool, const void
                                          : launch_split_d<bf16_t>(a, head_dim, G, batch, s);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head, batch), dim3(kCombineThreads), 0, s, a, head_dim, k_new, v_new,
-                     dtype, out);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head + (scatter ? 2 : 0), batch), dim3(kCombineThreads), 0, s, a,
+                     head_dim, k_new, v_new, dtype, out, scatter ? *scatter : KvScatterDecode{});
   return hipGetLastError();
 }
 
@@ -644,20 +661,9 @@ hipError_t launch_kv_gather(const void* cache, int64_t n_blocks, int block_size,
 hipError_t launch_kv_scatter_decode(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
                                     const int* block_idx, const int* pos_idx, int batch, hipStream_t s) {
   if (batch == 0 || row_bytes == 0) return hipSuccess;
-  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch, 1), dim3(kCopyThreads), 0, s, static_cast<uint32_t*>(cache),
-                     nullptr, n_blocks, block_size, row_bytes / 4, static_cast<const uint32_t*>(vals), nullptr,
-                     block_idx, pos_idx, batch);
-  return hipGetLastError();
-}
-
-hipError_t launch_kv_scatter_decode2(void* k_cache, void* v_cache, int64_t n_blocks, int block_size, int row_bytes,
-                                     const void* k_vals, const void* v_vals, const int* block_idx, const int* pos_idx,
-                                     int batch, hipStream_t s) {
-  if (batch == 0 || row_bytes == 0) return hipSuccess;
-  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch, 2), dim3(kCopyThreads), 0, s,
-                     static_cast<uint32_t*>(k_cache), static_cast<uint32_t*>(v_cache), n_blocks, block_size,
-                     row_bytes / 4, static_cast<const uint32_t*>(k_vals), static_cast<const uint32_t*>(v_vals),
-                     block_idx, pos_idx, batch);
+  hipLaunchKernelGGL(kv_scatter_decode_kernel, dim3(batch), dim3(kCopyThreads), 0, s, static_cast<uint32_t*>(cache),
+                     n_blocks, block_size, row_bytes / 4, static_cast<const uint32_t*>(vals), block_idx, pos_idx,
+                     batch);
   return hipGetLastError();
 }
 

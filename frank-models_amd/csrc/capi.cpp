@@ -544,20 +544,21 @@ AttnLayout attn_layout(const AttnShape& a, int64_t max_ctx, int act) {
   return L;
 }
 
-// out[B, N] fp32 = x[B, K] @ W for a one-expert packed weight [N, K];
-// order/offsets hold the identity grouping of the B rows.  The streaming
-// kernel splits K so that the few column tiles of one weight still fill the
-// GPU: *nsplit partial sums, B * N floats apart, to be added in order.
+// out[B, N] fp32 = x[B, K] @ W for a one-expert packed weight [N, K].  The
+// streaming kernel reads the B rows in order with no grouping arrays and
+// splits K so that the few column tiles of one weight still fill the GPU:
+// *nsplit partial sums, B * N floats apart, to be added in order.  The other
+// paths get the identity grouping written into order [B] / offsets [2].
 int run_linear(const void* x, int64_t K, const void* packed, const float* scales, int w_dtype, int64_t N, float* out,
-               int B, int act, const int* order, const int* offsets, hipStream_t s, int* nsplit) {
+               int B, int act, int* order, int* offsets, hipStream_t s, int* nsplit) {
   const int out_dtype = FMOE_F32;
   *nsplit = 1;
   GroupedGemmArgs g;
   g.a = x;
   g.lda = K;
   g.a_mode = A_DIRECT;
-  g.order = order;
-  g.offsets = offsets;
+  g.order = nullptr;
+  g.offsets = nullptr;
   g.n_tokens = B;
   g.n_assign = B;
   g.n_expert = 1;
@@ -589,6 +590,9 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
     *nsplit = g.ksplit;
     return FMOE_OK;
   }
+  g.order = order;
+  g.offsets = offsets;
+  FMOE_HIP(launch_iota(order, B, offsets, 0, B, s));
   return run_grouped_gemm(g, s);
 }
 
@@ -609,12 +613,12 @@ struct AttnWeights {
 int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, const int64_t* positions,
                   const void* k_pool, const void* v_pool, int64_t n_blocks, int block_size, const int* tables,
                   int max_blocks, const int* lens, int max_ctx, int act, void* out, void* k_new, void* v_new,
-                  void* workspace, const AttnLayout& L, hipStream_t s, const void* residual = nullptr) {
+                  void* workspace, const AttnLayout& L, hipStream_t s, const void* residual = nullptr,
+                  const KvScatterDecode* scatter = nullptr) {
   const int B = static_cast<int>(a.B);
   const int nq = static_cast<int>(a.n_embd), nkv = static_cast<int>(a.n_embd_kv);
   int* order = at<int>(workspace, L.order);
   int* offsets = at<int>(workspace, L.offsets);
-  FMOE_HIP(launch_iota(order, B, offsets, 0, B, s));
   float* qkv = at<float>(workspace, L.qkv);
   float* q_rot = at<float>(workspace, L.q_rot);
   const bool bias = w.use_bias != 0;
@@ -633,7 +637,7 @@ int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, c
     ScopedTimer t(FMOE_TIMER_ATTENTION, s);
     FMOE_HIP(launch_attn_decode(q_rot, k_pool, v_pool, n_blocks, block_size, tables, max_blocks, lens, max_ctx, k_new,
                                 v_new, B, static_cast<int>(a.n_head), static_cast<int>(a.n_head_kv),
-                                static_cast<int>(a.D), act, scale, at<float>(workspace, L.part), attn, s));
+                                static_cast<int>(a.D), act, scale, at<float>(workspace, L.part), attn, s, scatter));
   }
   float* y = at<float>(workspace, L.y);
   {
@@ -1250,14 +1254,19 @@ static int attention_paged(const void* input, const void* residual, const void* 
     FMOE_HIP(launch_rms_norm(input, norm_w, rms_eps, xn, batch, static_cast<int>(n_embd), act_dtype, s));
     x = xn;
   }
+  // scatter_decode once the attention has read the pools
+  // (transformer_layer_moe_decode.mlir:202-206), in the combine launch.
+  KvScatterDecode sc;
+  sc.k_cache = k_cache;
+  sc.v_cache = v_cache;
+  sc.n_blocks = n_blocks;
+  sc.block_size = static_cast<int>(block_size);
+  sc.row_bytes = static_cast<int>(n_embd_kv * dtype_bytes(act_dtype));
+  sc.block_idx = block_indices;
+  sc.pos_idx = pos_in_blocks;
   FMOE_TRY(run_attention(a, w, x, positions, k_cache, v_cache, n_blocks, static_cast<int>(block_size),
                          block_tables + layer * batch * max_blocks_per_seq, static_cast<int>(max_blocks_per_seq),
                          context_lens + layer * batch, static_cast<int>(max_context_len), act_dtype, out, kn, vn,
-                         workspace, L, s, residual));
-  // scatter_decode after the attention has read the pools
-  // (transformer_layer_moe_decode.mlir:202-206).
-  const int rb = static_cast<int>(n_embd_kv * dtype_bytes(act_dtype));
-  FMOE_HIP(launch_kv_scatter_decode2(k_cache, v_cache, n_blocks, static_cast<int>(block_size), rb, kn, vn,
-                                     block_indices, pos_in_blocks, static_cast<int>(batch), s));
+                         workspace, L, s, residual, &sc));
   return ok();
 }

@@ -54,7 +54,7 @@ __device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t 
                                        float v2, float v3) {
   if (EPI == EPI_SWIGLU || g.out_dtype == DT_BF16) {
     int64_t row = p;
-    if (EPI != EPI_SWIGLU) row = g.order[p];
+    if (EPI != EPI_SWIGLU && g.order) row = g.order[p];
     if (EPI == EPI_SCATTER_WEIGHTED) {
       const float w = g.route_w[row];
       v0 *= w, v1 *= w, v2 *= w, v3 *= w;
@@ -62,7 +62,7 @@ __device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t 
     u32x2_t pk{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
     *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(g.out) + row * g.ldo + n) = pk;
   } else {
-    const int64_t row = g.order[p];
+    const int64_t row = g.order ? g.order[p] : p;
     if (EPI == EPI_SCATTER_WEIGHTED) {
       const float w = g.route_w[row];
       v0 *= w, v1 *= w, v2 *= w, v3 *= w;
@@ -310,8 +310,8 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   __shared__ f32x4_t partial[kStreamWaves - 1][kStreamTiles][NSETS][kWave];
   const int e = blockIdx.x / col_tiles;
   const int ct = blockIdx.x - e * col_tiles;
-  const int row_begin = g.offsets[e];
-  const int count = g.offsets[e + 1] - row_begin;
+  const int row_begin = g.offsets ? g.offsets[e] : 0;
+  const int count = g.offsets ? g.offsets[e + 1] - row_begin : g.n_assign;
   if (count == 0) return;  // block-uniform
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -441,6 +441,13 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   }
 }
 
+// The grouping of assignment rows: order + offsets, or (streaming kernel
+// only, identity_ok) neither, for one expert whose rows are read in order.
+bool grouping_ok(const GroupedGemmArgs& g, bool identity_ok) {
+  if (g.order && g.offsets) return true;
+  return identity_ok && !g.order && !g.offsets && g.n_expert == 1 && g.a_mode == A_DIRECT;
+}
+
 bool mfma_common_ok(const GroupedGemmArgs& g) {
   if (g.act_dtype != DT_BF16) return false;
   if (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) return false;
@@ -510,18 +517,19 @@ hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
 }  // namespace
 
 bool gemm_tiled_supported(const GroupedGemmArgs& g) {
-  return gemm_tiled256_supported(g) || (mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0);
+  return gemm_tiled256_supported(g) || (mfma_common_ok(g) && grouping_ok(g, false) && g.K % kBK == 0 && g.K > 0);
 }
 
 bool gemm_stream_supported(const GroupedGemmArgs& g) {
   const bool split_ok = g.ksplit <= 1 || (g.epi == EPI_SCATTER && g.out_dtype == DT_F32 && g.split_stride > 0 &&
                                           g.ksplit <= 64);
-  return mfma_common_ok(g) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0 && split_ok;
+  return mfma_common_ok(g) && grouping_ok(g, true) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0 &&
+         split_ok;
 }
 
 int resolve_tiled_variant(const GroupedGemmArgs& g, int variant) {
   const bool large_ok = gemm_tiled256_supported(g);
-  const bool small_ok = mfma_common_ok(g) && g.K % kBK == 0 && g.K > 0 && g.ksplit == 1;
+  const bool small_ok = mfma_common_ok(g) && grouping_ok(g, false) && g.K % kBK == 0 && g.K > 0 && g.ksplit == 1;
   // The 256-tile kernel skips the MFMAs of empty row groups, so it wins at
   // every batch the tiled path serves (measured from ~64 rows per expert);
   // the 128-row kernel covers what it does not support.

@@ -72,6 +72,8 @@ struct GroupedGemmArgs {
   int a_mode = A_DIRECT;
   const int* order = nullptr;   // [n_assign] expert-sorted flat assignment ids
   const int* offsets = nullptr; // [n_expert + 1]
+  // The streaming kernel also takes order == offsets == nullptr for one
+  // expert and the identity grouping (rows 0..n_assign-1 in order).
   int n_tokens = 0;
   int n_assign = 0;             // k * n_tokens
   int n_expert = 0;
@@ -185,10 +187,18 @@ hipError_t launch_kv_gather(const void* cache, int64_t n_blocks, int block_size,
                             int max_blocks, const int* ctx_lens, int max_ctx, int batch, void* out, hipStream_t s);
 hipError_t launch_kv_scatter_decode(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
                                     const int* block_idx, const int* pos_idx, int batch, hipStream_t s);
-// The same for the K and V pools in one launch.
-hipError_t launch_kv_scatter_decode2(void* k_cache, void* v_cache, int64_t n_blocks, int block_size, int row_bytes,
-                                     const void* k_vals, const void* v_vals, const int* block_idx, const int* pos_idx,
-                                     int batch, hipStream_t s);
+// Where the decode step writes its new K/V rows (row b of k_new / v_new into
+// slot (block_idx[b], pos_idx[b]) of each pool): done by launch_attn_decode
+// once the pools have been read.
+struct KvScatterDecode {
+  void* k_cache = nullptr;
+  void* v_cache = nullptr;
+  int64_t n_blocks = 0;
+  int block_size = 0;
+  int row_bytes = 0;
+  const int* block_idx = nullptr;
+  const int* pos_idx = nullptr;
+};
 hipError_t launch_kv_scatter_prefill(void* cache, int64_t n_blocks, int block_size, int row_bytes, const void* vals,
                                      int seq_len, const int* tables, int max_blocks, const int* start, int batch,
                                      hipStream_t s);
@@ -214,9 +224,12 @@ int attn_decode_splits(int max_ctx);
 // One new token per sequence against max_ctx positions of the paged pools
 // (zero rows at and past ctx_lens[b]) and its own k_new / v_new; out
 // [B, n_head * head_dim] in dtype (the pools' and k_new / v_new's dtype).
+// With `scatter` non-null the combine launch also writes k_new / v_new into
+// the pools it names (after the split kernel has read them).
 hipError_t launch_attn_decode(const float* q_rot, const void* k_pool, const void* v_pool, int64_t n_blocks,
                               int block_size, const int* tables, int max_blocks, const int* ctx_lens, int max_ctx,
                               const void* k_new, const void* v_new, int batch, int n_head, int n_head_kv,
-                              int head_dim, int dtype, float scale, float* part, void* out, hipStream_t s);
+                              int head_dim, int dtype, float scale, float* part, void* out, hipStream_t s,
+                              const KvScatterDecode* scatter = nullptr);
 
 }  // namespace fmoe

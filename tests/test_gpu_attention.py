@@ -266,6 +266,46 @@ def test_paged_equals_gather_then_block(fm):
     assert_close_rms(_host(o2), _host(o1), 1e-5)
 
 
+def test_paged_scatter_after_read_duplicates_out_of_pool(fm):
+    """The paged decode's scatter of the new K/V (written by the combine
+    launch) on 130 sequences: a slot named twice keeps the later row, slots
+    outside the pool are skipped, and slots inside a sequence's own context
+    are written only after the attention has read them (gather-then-scatter
+    order of transformer_layer_moe_decode.mlir:180-206)."""
+    rng = np.random.default_rng(31)
+    B, n_embd, H, Hkv, bs, n_blocks, max_ctx = 130, 64, 4, 2, 4, 80, 16
+    D = n_embd // H
+    tables = rng.integers(0, n_blocks, (1, B, 5)).astype(np.int32)
+    lens = rng.integers(1, 21, (1, B)).astype(np.int32)
+    kp = rng.standard_normal((n_blocks, bs, Hkv, D)).astype(np.float32)
+    vp = rng.standard_normal((n_blocks, bs, Hkv, D)).astype(np.float32)
+    bi = rng.integers(0, n_blocks, B).astype(np.int32)
+    pi = rng.integers(0, bs, B).astype(np.int32)
+    bi[129], pi[129] = bi[0], pi[0]        # a duplicate slot: row 129 wins
+    bi[64], pi[64] = bi[3], pi[3]          # and one where the earlier row is 3
+    bi[5], bi[6], pi[7] = n_blocks, -1, bs  # outside the pool: skipped
+    bi[8], pi[8] = tables[0, 8, 0], 0      # inside sequence 8's own context
+    w, b, hw = _weights(rng, n_embd, Hkv * D, torch.float32)
+    blk = fm.AttentionBlockDecode(*(_dev(w[k], torch.float32) for k in ("wq", "wk", "wv", "wo")), n_head=H,
+                                  n_head_kv=Hkv, n_embd=n_embd, act_dtype=torch.float32)
+    x = rng.standard_normal((B, n_embd)).astype(np.float32)
+    pos = lens[0].astype(np.int64)
+    kd, vd = _dev(kp, torch.float32), _dev(vp, torch.float32)
+    out, k_new, v_new = blk.paged(_dev(x, torch.float32), torch.from_numpy(pos).cuda(), kd, vd, 0, tables, lens,
+                                  max_ctx, bi, pi)
+    torch.cuda.synchronize()
+    kc = oa.kv_gather(kp, 0, tables, lens, max_ctx)
+    vc = oa.kv_gather(vp, 0, tables, lens, max_ctx)
+    ref = oa.attention_block_decode(x, pos, kc, vc, hw["wq"], hw["wk"], hw["wv"], hw["wo"], None, None, None, None,
+                                    False, H, Hkv, n_embd)
+    assert_close_rms(_host(out), ref[0], 1e-4, what="paged B=130 output (pools read before the scatter)")
+    ok = (bi >= 0) & (bi < n_blocks) & (pi >= 0) & (pi < bs)
+    assert ok.sum() == B - 3
+    for pool, new, name in ((kp, k_new, "K"), (vp, v_new, "V")):
+        want = oa.kv_scatter_decode(pool, _host(new)[ok], bi[ok], pi[ok])
+        np.testing.assert_array_equal(_host(kd if name == "K" else vd), want, err_msg=f"{name} pool")
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_attention_sublayer_decode_paged(fm, dt):
     """attn_norm + paged attention + residual add in one call; in place
