@@ -229,6 +229,11 @@ __device__ __forceinline__ void load_chunk<bf16_t, 8>(const bf16_t* p, float (&v
 __device__ __forceinline__ float load_one(const float* p) { return *p; }
 __device__ __forceinline__ float load_one(const bf16_t* p) { return bf16_to_f32(*p); }
 
+__device__ __forceinline__ f32x4_t attn_mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                0, 0, 0);
+}
+
 struct AttnArgs {
   const float* q;         // [B, n_head * D] fp32, RoPE applied
   const void* k_pool;     // [n_blocks, block_size, n_head_kv, D]
@@ -276,6 +281,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
   constexpr int NV = kQ / PP;                             // V load instructions per wave
   constexpr int VR = NV < 16 ? NV : 16;                   // per round
   static_assert(kSteps % SR == 0 && NV % VR == 0, "rounds must tile the wave's positions");
+  constexpr bool kMfmaScores = sizeof(T) == 2 && (D == 64 || D == 128) && G <= 8 && kQ % 8 == 0;
   __shared__ float sc[G][kSplitLen];
   __shared__ int rows[kSplitLen];
   __shared__ float red[kAttnWaves][G][D];
@@ -308,6 +314,63 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
   }
   const T* kp = static_cast<const T*>(a.k_pool) + static_cast<int64_t>(kvh) * D;
   const T* vp = static_cast<const T*>(a.v_pool) + static_cast<int64_t>(kvh) * D;
+  const int tw = wave * kQ;  // this wave's first position
+  if constexpr (kMfmaScores) {
+    // ---- scores on the matrix cores (v_mfma_f32_16x16x32_bf16), 8
+    // positions per tile.  A row i = 2p + s holds half s of position p's K
+    // row, B column j = 2h + s' half s' of query head h (heads >= G zero):
+    // at step ks, lane group kg (lane >> 4) of row / column parity s takes
+    // the 8 dimensions of chunk 8 ks + 4 s + kg, so the 8 lanes of a
+    // position read 128 contiguous bytes per load.  score(p, h) =
+    // D[2p][2h] + D[2p+1][2h+1]; the cross terms (s != s') are unused.  q is
+    // split into bf16 high and low parts (two MFMAs per step): the products
+    // carry q * scale to about 16 significant bits, K is exact in bf16 and
+    // the sums are fp32.
+    constexpr int NKS = D / 64, PT = kQ / 8;
+    const int kg = lane >> 4, par = lane & 1, hh = (lane & 15) >> 1;
+    u32x4_t qh[NKS], ql[NKS];
+    {
+      const float* qg = a.q + (static_cast<int64_t>(b) * a.n_head + kvh * G + (hh < G ? hh : 0)) * D;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = (ks * 8 + par * 4 + kg) * 8 + 2 * e;
+          const float x0 = hh < G ? qg[d] * a.scale : 0.f;
+          const float x1 = hh < G ? qg[d + 1] * a.scale : 0.f;
+          const uint32_t h = pack_bf16x2(x0, x1);
+          qh[ks][e] = h;
+          ql[ks][e] = pack_bf16x2(x0 - __uint_as_float(h << 16), x1 - __uint_as_float(h & 0xFFFF0000u));
+        }
+    }
+    __syncthreads();  // rows[]
+    u32x4_t kr[PT][NKS];
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      const int r = rows[tw + pt * 8 + hh];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        kr[pt][ks] = r >= 0 ? *reinterpret_cast<const u32x4_t*>(kp + r * row_elems + (ks * 8 + par * 4 + kg) * 8)
+                            : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt) {
+      f32x4_t c{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        c = attn_mfma16(kr[pt][ks], qh[ks], c);
+        c = attn_mfma16(kr[pt][ks], ql[ks], c);
+      }
+      // lane (kg, column 2h + s'): c[r] = D[4 kg + r][2h + s'], rows 4 kg + r
+      // = position 2 kg + (r >> 1), half r & 1
+      const float odd1 = __shfl_xor(c[1], 1, kWave), odd3 = __shfl_xor(c[3], 1, kWave);
+      if (par == 0 && hh < G) {
+        const int t = tw + pt * 8 + 2 * kg;
+        sc[hh][t] = rows[t] == -2 ? -INFINITY : c[0] + odd1;  // a zero row scores 0
+        sc[hh][t + 1] = rows[t + 1] == -2 ? -INFINITY : c[2] + odd3;
+      }
+    }
+  } else {
   const int pi = lane / LP, sub = lane % LP;
   float q[G][DL];
 #pragma unroll
@@ -319,7 +382,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
         q[g][c * CW + e] =
             a.q[(static_cast<int64_t>(b) * a.n_head + kvh * G + g) * D + c * LP * CW + sub * CW + e] * a.scale;
   __syncthreads();
-  const int tw = wave * kQ;  // this wave's first position
 
   // ---- scores, SR steps of 8 positions per round of loads; K stays in its
   // storage format (CWW 32-bit words per chunk) until it is used
@@ -369,6 +431,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
         if (sub == g) sc[g][t] = rr[u] == -2 ? -INFINITY : acc;  // a zero row scores 0
       }
     }
+  }
   }
 
   // ---- V rows of this wave, first round issued before the softmax
