@@ -124,6 +124,13 @@ CASES = [
     (5, 1000, 1024, 16, 2, True, "bf16"),  # head_dim 64
     (4, 513, 4096, 32, 8, True, "bf16"),   # Mixtral heads: head_dim 128, 4 per KV head
     (1, 256, 4096, 32, 8, False, "bf16"),  # exactly one split
+    # bf16 scores on the matrix cores (head_dim 64 / 128) for every group
+    # size, with contexts that end inside an 8-position tile
+    (3, 77, 512, 4, 4, False, "bf16"),     # head_dim 128, MHA
+    (2, 301, 1024, 8, 1, False, "bf16"),   # head_dim 128, 8 per KV head
+    (3, 19, 256, 4, 2, True, "bf16"),      # head_dim 64, 2 per KV head
+    (2, 130, 512, 8, 2, False, "bf16"),    # head_dim 64, 4 per KV head
+    (2, 45, 256, 8, 4, False, "bf16"),     # head_dim 32: bf16 scores on the vector units
 ]
 
 
