@@ -156,13 +156,8 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const float* __restrict__
     x0 += bias[c];
     x1 += bias[c + 1];
   }
-  const int pi = (c % D) / 2;
-  const double freq = freq_scale / pow(freq_base, static_cast<double>(2 * pi) / D);
-  double sn, cs;
-  sincos(static_cast<double>(positions[b]) * freq, &sn, &cs);
-  const float cf = static_cast<float>(cs), sf = static_cast<float>(sn);
-  const float y0 = x0 * cf - x1 * sf;
-  const float y1 = x0 * sf + x1 * cf;
+  float y0, y1;
+  rope_pair(x0, x1, positions[b], (c % D) / 2, D, freq_base, freq_scale, y0, y1);
   if (is_q) {
     q_rot[static_cast<int64_t>(b) * nq + c] = y0;
     q_rot[static_cast<int64_t>(b) * nq + c + 1] = y1;

@@ -549,10 +549,14 @@ AttnLayout attn_layout(const AttnShape& a, int64_t max_ctx, int act) {
 // splits K so that the few column tiles of one weight still fill the GPU:
 // *nsplit partial sums, B * N floats apart, to be added in order.  The other
 // paths get the identity grouping written into order [B] / offsets [2].
+// With `pe` the streaming kernel applies that epilogue itself (no K split,
+// `out` unused) where it supports it, and *fused reports whether it did.
 int run_linear(const void* x, int64_t K, const void* packed, const float* scales, int w_dtype, int64_t N, float* out,
-               int B, int act, int* order, int* offsets, hipStream_t s, int* nsplit) {
+               int B, int act, int* order, int* offsets, hipStream_t s, int* nsplit,
+               const ProjEpilogue* pe = nullptr, bool* fused = nullptr) {
   const int out_dtype = FMOE_F32;
   *nsplit = 1;
+  if (fused) *fused = false;
   GroupedGemmArgs g;
   g.a = x;
   g.lda = K;
@@ -576,6 +580,19 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
   g.max_rows_per_expert = B;
   // Decode batches read each weight once in the streaming kernel, with
   // about 1024 blocks (4 per CU) and at least 4 input steps per wave.
+  if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && pe && fused) {
+    GroupedGemmArgs f = g;
+    f.epi = pe->kind;
+    f.pe = *pe;
+    f.out = pe->kind == EPI_LINEAR ? pe->out : nullptr;
+    f.out_dtype = FMOE_BF16;
+    if (gemm_stream_supported(f)) {
+      FMOE_HIP(launch_gemm_stream(f, s));
+      g_last_path = FMOE_PATH_STREAM;
+      *fused = true;
+      return FMOE_OK;
+    }
+  }
   if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && gemm_stream_supported(g)) {
     // Split K so that each wave streams one full trip of 8 steps (K / 32 /
     // (4 waves * 8)) while the grid has fewer than ~2048 blocks.
@@ -624,12 +641,34 @@ int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, c
   const bool bias = w.use_bias != 0;
   {
     ScopedTimer t(FMOE_TIMER_QKV, s);
+    // bias + RoPE in the GEMM's epilogue where the streaming kernel takes
+    // it, else over the fp32 (K-split) result.  Fused only up to 16 rows:
+    // the epilogue's double-precision angles run on one wave per block, and
+    // at 64 rows the separate RoPE launch is faster (Q/K/V phase 38.6
+    // against 44.5 us fused at 64 x 1024 positions).  At 16 x 4096 the
+    // fused step is 1.3 us shorter, at 1 x 512 3.5 us (43.0 -> 39.5 us).
+    ProjEpilogue pe;
+    pe.kind = EPI_QKV_ROPE;
+    pe.bias = bias ? w.bq : nullptr;
+    pe.bias_k = bias ? w.bk : nullptr;
+    pe.bias_v = bias ? w.bv : nullptr;
+    pe.positions = positions;
+    pe.nq = nq;
+    pe.nkv = nkv;
+    pe.head_dim = static_cast<int>(a.D);
+    pe.freq_base = w.freq_base;
+    pe.freq_scale = w.freq_scale;
+    pe.q_out = q_rot;
+    pe.k_out = k_new;
+    pe.v_out = v_new;
     int ns = 1;
+    bool fused = false;
     FMOE_TRY(run_linear(input, a.n_embd, w.wqkv, w.wqkv_scales, w.w_dtype, nq + 2 * nkv, qkv, B, act, order,
-                        offsets, s, &ns));
-    FMOE_HIP(launch_qkv_rope(qkv, ns, static_cast<int64_t>(B) * (nq + 2 * nkv), bias ? w.bq : nullptr,
-                             bias ? w.bk : nullptr, bias ? w.bv : nullptr, positions, B, nq, nkv,
-                             static_cast<int>(a.D), w.freq_base, w.freq_scale, q_rot, k_new, v_new, act, s));
+                        offsets, s, &ns, act == FMOE_BF16 && B <= 16 ? &pe : nullptr, &fused));
+    if (!fused)
+      FMOE_HIP(launch_qkv_rope(qkv, ns, static_cast<int64_t>(B) * (nq + 2 * nkv), bias ? w.bq : nullptr,
+                               bias ? w.bk : nullptr, bias ? w.bv : nullptr, positions, B, nq, nkv,
+                               static_cast<int>(a.D), w.freq_base, w.freq_scale, q_rot, k_new, v_new, act, s));
   }
   void* attn = at<char>(workspace, L.attn);
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(a.D)));
@@ -642,10 +681,18 @@ int run_attention(const AttnShape& a, const AttnWeights& w, const void* input, c
   float* y = at<float>(workspace, L.y);
   {
     ScopedTimer t(FMOE_TIMER_OUT_PROJ, s);
+    ProjEpilogue pe;
+    pe.kind = EPI_LINEAR;
+    pe.bias = bias ? w.bo : nullptr;
+    pe.residual = residual;
+    pe.out = out;
     int ns = 1;
-    FMOE_TRY(run_linear(attn, a.n_embd, w.wo, w.wo_scales, w.w_dtype, nq, y, B, act, order, offsets, s, &ns));
-    FMOE_HIP(launch_bias_cast(y, ns, static_cast<int64_t>(B) * nq, bias ? w.bo : nullptr, residual, out, B, nq, act,
-                              s));
+    bool fused = false;
+    FMOE_TRY(run_linear(attn, a.n_embd, w.wo, w.wo_scales, w.w_dtype, nq, y, B, act, order, offsets, s, &ns,
+                        act == FMOE_BF16 ? &pe : nullptr, &fused));
+    if (!fused)
+      FMOE_HIP(launch_bias_cast(y, ns, static_cast<int64_t>(B) * nq, bias ? w.bo : nullptr, residual, out, B, nq,
+                                act, s));
   }
   return FMOE_OK;
 }

@@ -55,6 +55,20 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * (u * __builtin_amdgcn_rcpf(1.f + __expf(-u)));
 }
 
+// RoPE of the adjacent pair (x0, x1) = dimensions (2i, 2i+1) of a head of
+// size D at position pos: angle pos * freq_scale / freq_base^(2i/D) in
+// double precision (components/position/rope.mlir:38-104,
+// oracles/position.py:6-50).
+__device__ __forceinline__ void rope_pair(float x0, float x1, int64_t pos, int i, int D, double freq_base,
+                                          double freq_scale, float& y0, float& y1) {
+  const double freq = freq_scale / pow(freq_base, static_cast<double>(2 * i) / D);
+  double sn, cs;
+  sincos(static_cast<double>(pos) * freq, &sn, &cs);
+  const float cf = static_cast<float>(cs), sf = static_cast<float>(sn);
+  y0 = x0 * cf - x1 * sf;
+  y1 = x0 * sf + x1 * cf;
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
   bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};

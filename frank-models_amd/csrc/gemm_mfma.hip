@@ -48,10 +48,63 @@ __device__ __forceinline__ int64_t a_source_row(const GroupedGemmArgs& g, int p)
   return p;
 }
 
+// Fused projection epilogues (one expert, rows in order, bf16 output):
+// columns [n, n+4) of row p.  EPI_LINEAR rounds acc + bias to bf16 before
+// adding the residual (the reference adds the rounded attention output,
+// transformer_layer_moe_decode.mlir:208-221); the residual may alias out
+// (each element is read and written by the same lane).  EPI_QKV_ROPE: the
+// column groups of 4 lie inside one of the q | k | v parts (nq, nkv
+// multiples of 4) and hold two RoPE pairs of one head (head_dim even).
+template <int EPI>
+__device__ __forceinline__ void store4_proj(const GroupedGemmArgs& g, int p, int64_t n, float v0, float v1,
+                                            float v2, float v3) {
+  const ProjEpilogue& e = g.pe;
+  if (EPI == EPI_LINEAR) {
+    if (e.bias) v0 += e.bias[n], v1 += e.bias[n + 1], v2 += e.bias[n + 2], v3 += e.bias[n + 3];
+    const int64_t i = static_cast<int64_t>(p) * g.N + n;
+    u32x2_t pk{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+    if (e.residual) {
+      const u32x2_t r = *reinterpret_cast<const u32x2_t*>(static_cast<const bf16_t*>(e.residual) + i);
+      pk = u32x2_t{pack_bf16x2(__uint_as_float(pk[0] << 16) + __uint_as_float(r[0] << 16),
+                               __uint_as_float(pk[0] & 0xFFFF0000u) + __uint_as_float(r[0] & 0xFFFF0000u)),
+                   pack_bf16x2(__uint_as_float(pk[1] << 16) + __uint_as_float(r[1] << 16),
+                               __uint_as_float(pk[1] & 0xFFFF0000u) + __uint_as_float(r[1] & 0xFFFF0000u))};
+    }
+    *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(e.out) + i) = pk;
+  } else {
+    const int nq = e.nq, nkv = e.nkv;
+    if (n >= nq + nkv) {  // v: bias only
+      const int64_t c = n - nq - nkv;
+      if (e.bias_v) v0 += e.bias_v[c], v1 += e.bias_v[c + 1], v2 += e.bias_v[c + 2], v3 += e.bias_v[c + 3];
+      *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(e.v_out) + static_cast<int64_t>(p) * nkv + c) =
+          u32x2_t{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+      return;
+    }
+    const bool is_q = n < nq;
+    const int64_t c = is_q ? n : n - nq;
+    const float* b = is_q ? e.bias : e.bias_k;
+    if (b) v0 += b[c], v1 += b[c + 1], v2 += b[c + 2], v3 += b[c + 3];
+    const int64_t pos = e.positions[p];
+    const int i0 = static_cast<int>(c % e.head_dim) / 2;
+    float y0, y1, y2, y3;
+    rope_pair(v0, v1, pos, i0, e.head_dim, e.freq_base, e.freq_scale, y0, y1);
+    rope_pair(v2, v3, pos, i0 + 1, e.head_dim, e.freq_base, e.freq_scale, y2, y3);
+    if (is_q)
+      *reinterpret_cast<float4*>(e.q_out + static_cast<int64_t>(p) * nq + c) = float4{y0, y1, y2, y3};
+    else
+      *reinterpret_cast<u32x2_t*>(static_cast<bf16_t*>(e.k_out) + static_cast<int64_t>(p) * nkv + c) =
+          u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+  }
+}
+
 // Writes 4 consecutive columns [n, n+4) of row p's result.
 template <int EPI>
 __device__ __forceinline__ void store4(const GroupedGemmArgs& g, int p, int64_t n, float v0, float v1,
                                        float v2, float v3) {
+  if (EPI == EPI_LINEAR || EPI == EPI_QKV_ROPE) {
+    store4_proj<EPI>(g, p, n, v0, v1, v2, v3);
+    return;
+  }
   if (EPI == EPI_SWIGLU || g.out_dtype == DT_BF16) {
     int64_t row = p;
     if (EPI != EPI_SWIGLU && g.order) row = g.order[p];
@@ -301,11 +354,15 @@ constexpr int kStreamWaves = kThreads / kWave;
 // multi-tile gate/up kernels put their accumulators in AGPRs and fit only 2
 // waves per SIMD (measured: 3 is 2-5% faster at 64 tokens); 1-set kernels
 // keep the occupancy they reach anyway (6 for one tile spills).
-template <int NSETS, int kStreamTiles>
-constexpr int stream_waves_per_eu() { return NSETS == 2 ? 3 : kStreamTiles == 1 ? 5 : 4; }
+// The RoPE epilogue's double-precision angles need more registers; its
+// projection has one or two blocks per CU anyway.
+template <int EPI, int NSETS, int kStreamTiles>
+constexpr int stream_waves_per_eu() {
+  return EPI == EPI_QKV_ROPE ? 2 : NSETS == 2 ? 3 : kStreamTiles == 1 ? 5 : 4;
+}
 
 template <int EPI, int NSETS, bool F8, int kStreamTiles>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<NSETS, kStreamTiles>())))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<EPI, NSETS, kStreamTiles>())))
 void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   __shared__ f32x4_t partial[kStreamWaves - 1][kStreamTiles][NSETS][kWave];
   const int e = blockIdx.x / col_tiles;
@@ -492,6 +549,10 @@ void launch_stream_tiles(const GroupedGemmArgs& g, hipStream_t s, dim3 grid, int
   grid.y = g.ksplit > 1 ? g.ksplit : 1;
   if (g.epi == EPI_SWIGLU)
     hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
+  else if (g.epi == EPI_LINEAR)
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_LINEAR, 1, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
+  else if (g.epi == EPI_QKV_ROPE)
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_QKV_ROPE, 1, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
   else if (g.epi == EPI_SCATTER_WEIGHTED)
     hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER_WEIGHTED, 1, F8, TILES>), grid, dim3(kThreads), 0, s, g,
                        col_tiles);
@@ -517,10 +578,26 @@ hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
 }  // namespace
 
 bool gemm_tiled_supported(const GroupedGemmArgs& g) {
-  return gemm_tiled256_supported(g) || (mfma_common_ok(g) && grouping_ok(g, false) && g.K % kBK == 0 && g.K > 0);
+  return gemm_tiled256_supported(g) ||
+         (g.epi <= EPI_SCATTER_WEIGHTED && mfma_common_ok(g) && grouping_ok(g, false) && g.K % kBK == 0 && g.K > 0);
+}
+
+// The fused projection epilogues: one expert read in row order, no K split,
+// bf16 outputs stored 8 bytes (4 columns) at a time.
+bool proj_epilogue_ok(const GroupedGemmArgs& g) {
+  const ProjEpilogue& e = g.pe;
+  if (g.ksplit > 1 || g.n_expert != 1 || g.order || g.offsets || g.a_mode != A_DIRECT) return false;
+  auto al8 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 8 == 0; };
+  if (g.epi == EPI_LINEAR) return e.out && al8(e.out) && al8(e.residual);
+  return e.positions && e.q_out && e.k_out && e.v_out && reinterpret_cast<uintptr_t>(e.q_out) % 16 == 0 &&
+         al8(e.k_out) && al8(e.v_out) && e.nq > 0 && e.nkv > 0 && e.nq % 4 == 0 && e.nkv % 4 == 0 &&
+         e.head_dim > 0 && e.head_dim % 4 == 0 && e.nq % e.head_dim == 0 && e.nkv % e.head_dim == 0 &&
+         g.N == static_cast<int64_t>(e.nq) + 2 * e.nkv;
 }
 
 bool gemm_stream_supported(const GroupedGemmArgs& g) {
+  if ((g.epi == EPI_LINEAR || g.epi == EPI_QKV_ROPE) && !proj_epilogue_ok(g)) return false;
+  if (g.epi > EPI_QKV_ROPE || g.epi < 0) return false;
   const bool split_ok = g.ksplit <= 1 || (g.epi == EPI_SCATTER && g.out_dtype == DT_F32 && g.split_stride > 0 &&
                                           g.ksplit <= 64);
   return mfma_common_ok(g) && grouping_ok(g, true) && g.K > 0 && g.K % (g.w_dtype == DT_F8 ? 64 : 32) == 0 &&
@@ -529,7 +606,8 @@ bool gemm_stream_supported(const GroupedGemmArgs& g) {
 
 int resolve_tiled_variant(const GroupedGemmArgs& g, int variant) {
   const bool large_ok = gemm_tiled256_supported(g);
-  const bool small_ok = mfma_common_ok(g) && grouping_ok(g, false) && g.K % kBK == 0 && g.K > 0 && g.ksplit == 1;
+  const bool small_ok = g.epi <= EPI_SCATTER_WEIGHTED && mfma_common_ok(g) && grouping_ok(g, false) &&
+                        g.K % kBK == 0 && g.K > 0 && g.ksplit == 1;
   // The 256-tile kernel skips the MFMAs of empty row groups, so it wins at
   // every batch the tiled path serves (measured from ~64 rows per expert);
   // the 128-row kernel covers what it does not support.

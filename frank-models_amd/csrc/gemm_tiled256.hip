@@ -648,7 +648,7 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
   if (g.act_dtype != DT_BF16 || (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) || g.w_format != WF_MFMA16)
     return false;
-  if (!g.order || !g.offsets) return false;
+  if (!g.order || !g.offsets || g.epi > EPI_SCATTER_WEIGHTED) return false;
   // bf16: an even number of 32-input stages per split; fp8: whole 64-input
   // blocks; at least two stages per split.
   if (g.K <= 0 || g.K % (2 * kBK) || g.K / (2 * kBK) < 2 * g.ksplit || g.N % 16 || g.lda % 8 || g.ldo % 4)

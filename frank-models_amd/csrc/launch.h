@@ -63,7 +63,27 @@ enum AMode {
 enum Epilogue {
   EPI_SWIGLU = 0,            // out[p, n] = g * silu(u) from the two weight sets
   EPI_SCATTER = 1,           // out[order[p], n] = acc
-  EPI_SCATTER_WEIGHTED = 2   // out[order[p], n] = acc * route_w[order[p]]
+  EPI_SCATTER_WEIGHTED = 2,  // out[order[p], n] = acc * route_w[order[p]]
+  // One-expert projections on the streaming kernel (bf16 activations, no K
+  // split), with the fields of ProjEpilogue:
+  EPI_LINEAR = 3,            // out[p, n] = bf16(acc + bias[n]) (+ residual[p, n])
+  EPI_QKV_ROPE = 4           // bias, then RoPE on the q and k columns -> q_out / k_out / v_out
+};
+
+// The epilogue of a fused projection (EPI_LINEAR / EPI_QKV_ROPE).
+struct ProjEpilogue {
+  int kind = EPI_LINEAR;
+  const float* bias = nullptr;      // EPI_LINEAR: [N]; EPI_QKV_ROPE: q bias [nq] (or null)
+  const float* bias_k = nullptr;    // EPI_QKV_ROPE: [nkv] (or null)
+  const float* bias_v = nullptr;    // EPI_QKV_ROPE: [nkv] (or null)
+  const void* residual = nullptr;   // EPI_LINEAR: [rows, N] bf16 added after rounding; may alias out
+  void* out = nullptr;              // EPI_LINEAR: [rows, N] bf16
+  const int64_t* positions = nullptr;  // EPI_QKV_ROPE: [rows]
+  int nq = 0, nkv = 0, head_dim = 0;   // EPI_QKV_ROPE: N = nq + 2 nkv, columns q | k | v
+  double freq_base = 10000.0, freq_scale = 1.0;
+  float* q_out = nullptr;           // [rows, nq] fp32
+  void* k_out = nullptr;            // [rows, nkv] bf16, RoPE applied
+  void* v_out = nullptr;            // [rows, nkv] bf16
 };
 
 struct GroupedGemmArgs {
@@ -100,6 +120,7 @@ struct GroupedGemmArgs {
   // block: n_tokens, since top-k picks distinct experts per token); 0 =
   // unknown.  A tuning hint: kernels are correct for any count.
   int max_rows_per_expert = 0;
+  ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
 };
 
 // Upper bound on the number of bm-row tiles of a grouping of n_assign rows

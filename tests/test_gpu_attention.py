@@ -124,6 +124,7 @@ CASES = [
     (5, 1000, 1024, 16, 2, True, "bf16"),  # head_dim 64
     (4, 513, 4096, 32, 8, True, "bf16"),   # Mixtral heads: head_dim 128, 4 per KV head
     (1, 256, 4096, 32, 8, False, "bf16"),  # exactly one split
+    (40, 100, 512, 4, 2, True, "bf16"),    # 40 rows: RoPE after a K-split Q/K/V product
     # bf16 scores on the matrix cores (head_dim 64 / 128) for every group
     # size, with contexts that end inside an 8-position tile
     (3, 77, 512, 4, 4, False, "bf16"),     # head_dim 128, MHA
@@ -313,24 +314,27 @@ def test_paged_scatter_after_read_duplicates_out_of_pool(fm):
         np.testing.assert_array_equal(_host(kd if name == "K" else vd), want, err_msg=f"{name} pool")
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
-def test_attention_sublayer_decode_paged(fm, dt):
+@pytest.mark.parametrize("dt,B", [("f32", 3), ("bf16", 3), ("bf16", 40)])
+def test_attention_sublayer_decode_paged(fm, dt, B):
     """attn_norm + paged attention + residual add in one call; in place
-    (out=residual) equals out of place bit for bit."""
-    rng = np.random.default_rng(31)
+    (out=residual) equals out of place bit for bit.  bf16 at 3 rows runs
+    bias + RoPE and bias + residual in the projections' epilogues; at 40
+    rows RoPE runs as its own launch over a K-split Q/K/V product."""
+    rng = np.random.default_rng(31 + B)
     tdt = DT[dt]
-    B, n_embd, H, Hkv, bs, n_blocks, max_ctx = 3, 256, 8, 2, 16, 40, 100
+    n_embd, H, Hkv, bs, max_ctx = 256, 8, 2, 16, 100
+    n_blocks = max(40, B * 8)
     D = n_embd // H
     tables = rng.permutation(n_blocks)[: B * 8].reshape(1, B, 8).astype(np.int32)
-    lens = np.array([[100, 37, 64]], np.int32)
+    lens = np.array([[100, 37, 64]], np.int32) if B == 3 else rng.integers(1, 101, (1, B)).astype(np.int32)
     kp = _round(rng.standard_normal((n_blocks, bs, Hkv, D)), tdt)
     vp = _round(rng.standard_normal((n_blocks, bs, Hkv, D)), tdt)
     bi = np.array([tables[0, b, 7] for b in range(B)], np.int32)
-    pi = np.array([15, 15, 15], np.int32)
+    pi = np.full(B, 15, np.int32)
     w, b, hw = _weights(rng, n_embd, Hkv * D, tdt)
     res = _round(rng.standard_normal((B, n_embd)), tdt)
     nw = _round(rng.standard_normal(n_embd) * 0.5 + 1.0, tdt)
-    pos = np.array([100, 37, 64], np.int64)
+    pos = lens[0].astype(np.int64)
     blk = fm.AttentionBlockDecode(*(_dev(w[k], tdt) for k in ("wq", "wk", "wv", "wo")),
                                   *(torch.from_numpy(b[k]).cuda() for k in ("bq", "bk", "bv", "bo")),
                                   use_bias=True, n_head=H, n_head_kv=Hkv, n_embd=n_embd, act_dtype=tdt)
