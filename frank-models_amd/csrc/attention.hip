@@ -529,6 +529,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
 constexpr int kCombineThreads = 128;  // >= head_dim
 constexpr int kCombineChunk = 1024;   // splits whose weights are held in LDS at once
 constexpr int kCombineUnroll = 8;
+constexpr int kCombinePre = 16;       // splits (4096 positions) prefetched into registers
 
 // Blocks x = n_head and n_head + 1 (launched only with a scatter) write
 // k_new / v_new into the pools: the split kernel has read them by then.
@@ -555,12 +556,21 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
   const float* qh = a.q + (static_cast<int64_t>(b) * a.n_head + h) * D;
   const int64_t kv0 = (static_cast<int64_t>(b) * a.n_head_kv + kvh) * D;
   const float* part = a.part + (static_cast<int64_t>(b) * a.n_head + h) * a.n_split * (D + 2);
+  // The first kCombinePre splits' outputs and v_new are loaded before the
+  // statistics, so their latency overlaps wave 0's reductions.
+  const int n_pre = min(n_used, kCombinePre);
+  float pv[kCombinePre];
+#pragma unroll
+  for (int u = 0; u < kCombinePre; ++u)
+    pv[u] = tid < D && u < n_pre ? part[static_cast<int64_t>(u) * (D + 2) + tid] : 0.f;
+  const float vn = tid < D ? load_act(v_new, act, kv0 + tid) : 0.f;
   if (tid < kWave) {
     float dot = 0.f;
     for (int d = lane; d < D; d += kWave) dot = fmaf(qh[d] * a.scale, load_act(k_new, act, kv0 + d), dot);
     const float s_new = wave_sum(dot);
-    float M = fmaxf(s_new, n_zero > 0 ? 0.f : -INFINITY);
-    for (int s = lane; s < n_used; s += kWave) M = fmaxf(M, part[static_cast<int64_t>(s) * (D + 2) + D]);
+    const float m0 = lane < n_used ? part[static_cast<int64_t>(lane) * (D + 2) + D] : -INFINITY;
+    float M = fmaxf(fmaxf(s_new, n_zero > 0 ? 0.f : -INFINITY), m0);
+    for (int s = lane + kWave; s < n_used; s += kWave) M = fmaxf(M, part[static_cast<int64_t>(s) * (D + 2) + D]);
     M = wave_max(M);
     float l = 0.f;
     for (int s = lane; s < n_used; s += kWave) {
@@ -568,23 +578,33 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
       l = fmaf(ps[D + 1], __expf(ps[D] - M), l);
     }
     l = wave_sum(l) + __expf(s_new - M) + (n_zero > 0 ? static_cast<float>(n_zero) * __expf(-M) : 0.f);
+    const float inv = 1.f / l;
+    // the first chunk's split weights exp(m_s - M) / l
+    for (int s = lane; s < min(n_used, kCombineChunk); s += kWave)
+      wts[s] = __expf((s == lane ? m0 : part[static_cast<int64_t>(s) * (D + 2) + D]) - M) * inv;
     if (lane == 0) {
       stat[0] = M;
-      stat[1] = 1.f / l;
+      stat[1] = inv;
       stat[2] = __expf(s_new - M) / l;
     }
   }
   __syncthreads();
   const float M = stat[0], inv = stat[1];
-  float o = tid < D ? stat[2] * load_act(v_new, act, kv0 + tid) : 0.f;
+  float o = stat[2] * vn;
+  // splits in order: the prefetched ones, then the rest of each chunk
+#pragma unroll
+  for (int u = 0; u < kCombinePre; ++u)
+    if (u < n_pre) o = fmaf(pv[u], wts[u], o);
   for (int c0 = 0; c0 < n_used; c0 += kCombineChunk) {
     const int cn = min(kCombineChunk, n_used - c0);
-    __syncthreads();
-    for (int s = tid; s < cn; s += kCombineThreads)
-      wts[s] = __expf(part[static_cast<int64_t>(c0 + s) * (D + 2) + D] - M) * inv;
-    __syncthreads();
+    if (c0 > 0) {
+      __syncthreads();
+      for (int s = tid; s < cn; s += kCombineThreads)
+        wts[s] = __expf(part[static_cast<int64_t>(c0 + s) * (D + 2) + D] - M) * inv;
+      __syncthreads();
+    }
     if (tid < D) {
-      for (int s0 = 0; s0 < cn; s0 += kCombineUnroll) {
+      for (int s0 = c0 == 0 ? n_pre : 0; s0 < cn; s0 += kCombineUnroll) {
         float v[kCombineUnroll];
 #pragma unroll
         for (int u = 0; u < kCombineUnroll; ++u)

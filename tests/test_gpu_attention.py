@@ -159,6 +159,33 @@ def test_attention_block_decode(fm, B, ctx, n_embd, H, Hkv, bias, dt):
     assert_close_rms(_host(v_new), ref[2], rtol, what=what + " v_new")
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_rope_large_positions(fm, dt):
+    """RoPE angles up to 1e6 rad (positions near 1e6, the head's first pair):
+    the angles are formed in double precision, so the rotated k_new follows
+    the float64 oracle as closely as at small positions (bf16: RoPE in the
+    Q/K/V GEMM's epilogue; f32: the separate RoPE kernel)."""
+    rng = np.random.default_rng(5)
+    tdt = DT[dt]
+    B, ctx, n_embd, H, Hkv = 4, 3, 256, 4, 2
+    D = n_embd // H
+    w, b, hw = _weights(rng, n_embd, Hkv * D, tdt)
+    x = _round(rng.standard_normal((B, n_embd)), tdt)
+    kc = _round(rng.standard_normal((B, ctx, Hkv, D)), tdt)
+    vc = _round(rng.standard_normal((B, ctx, Hkv, D)), tdt)
+    pos = np.array([999_983, 524_287, 65_537, 1_000_000], np.int64)
+    blk = fm.AttentionBlockDecode(*(_dev(w[k], tdt) for k in ("wq", "wk", "wv", "wo")),
+                                  *(torch.from_numpy(b[k]).cuda() for k in ("bq", "bk", "bv", "bo")),
+                                  use_bias=True, n_head=H, n_head_kv=Hkv, n_embd=n_embd, act_dtype=tdt)
+    out, k_new, _ = blk(_dev(x, tdt), torch.from_numpy(pos).cuda(), _dev(kc, tdt), _dev(vc, tdt))
+    torch.cuda.synchronize()
+    ref = oa.attention_block_decode(x, pos, kc, vc, hw["wq"], hw["wk"], hw["wv"], hw["wo"], b["bq"], b["bk"], b["bv"],
+                                    b["bo"], True, H, Hkv, n_embd)
+    rtol = 1e-4 if dt == "f32" else 1e-2
+    assert_close_rms(_host(k_new), ref[1], rtol, what=f"k_new at large positions {dt}")
+    assert_close_rms(_host(out), ref[0], 1e-4 if dt == "f32" else 2e-2, what=f"output at large positions {dt}")
+
+
 def test_attention_block_decode_reference_signature(fm):
     """NumPy in / NumPy out through the reference's positional signature."""
     rng = np.random.default_rng(11)
