@@ -16,7 +16,10 @@
 // positions, KV head, sequence) computes, for the G query heads sharing the
 // KV head, the split's max score, sum of exp and unnormalised output; a
 // combine kernel merges the splits in order with the zero rows and the new
-// token.
+// token and, in the paged calls, writes the new K/V rows into the pools.
+// Where the streaming GEMM does not apply its own epilogue (fp32
+// activations, more than 16 rows for Q/K/V), the separate bias + RoPE and
+// bias + cast kernels here finish the projections.
 #include "common.h"
 #include "launch.h"
 
