@@ -544,6 +544,16 @@ AttnLayout attn_layout(const AttnShape& a, int64_t max_ctx, int act) {
   return L;
 }
 
+// Rows up to which a one-expert projection streams its weight (K split over
+// fp32 partials); above it, the 256-row tile kernel with K split.  Measured
+// on the decode attention's projections (n_embd 4096): at 64 rows the tile
+// kernel takes the Q/K/V product from 39 to 32 us, at 128 rows from 88 (the
+// unsplit tile kernel) to 38 us and the output projection from 84 to 31 us;
+// at 32 rows streaming is ahead (Q/K/V 27 against 29 us).  The fused
+// epilogues below stream up to 64 rows (the output projection with its bias
+// and residual at 64 rows: 24.7 us, level with the split product + launch).
+constexpr int kLinearStreamRows = 32;
+
 // out[B, N] fp32 = x[B, K] @ W for a one-expert packed weight [N, K].  The
 // streaming kernel reads the B rows in order with no grouping arrays and
 // splits K so that the few column tiles of one weight still fill the GPU:
@@ -578,8 +588,9 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
   g.w_format = packed_format(N, K, w_dtype);
   g.out_dtype = out_dtype;
   g.max_rows_per_expert = B;
-  // Decode batches read each weight once in the streaming kernel, with
-  // about 1024 blocks (4 per CU) and at least 4 input steps per wave.
+  // Decode batches read each weight once in the streaming kernel (see
+  // kLinearStreamRows), with up to ~2048 blocks and at least 4 input steps
+  // per wave.
   if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && pe && fused) {
     GroupedGemmArgs f = g;
     f.epi = pe->kind;
@@ -593,7 +604,7 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
       return FMOE_OK;
     }
   }
-  if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= 64 && gemm_stream_supported(g)) {
+  if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && B <= kLinearStreamRows && gemm_stream_supported(g)) {
     // Split K so that each wave streams one full trip of 8 steps (K / 32 /
     // (4 waves * 8)) while the grid has fewer than ~2048 blocks.
     const int64_t tiles = (N + 15) / 16;
@@ -610,6 +621,23 @@ int run_linear(const void* x, int64_t K, const void* packed, const float* scales
   g.order = order;
   g.offsets = offsets;
   FMOE_HIP(launch_iota(order, B, offsets, 0, B, s));
+  // Larger batches: the 256-row tile kernel, K split so that the few column
+  // tiles of one weight still give the GPU about 256 blocks.
+  if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO) {
+    GroupedGemmArgs t = g;
+    t.split_stride = static_cast<int64_t>(B) * N;
+    const int64_t tiles = static_cast<int64_t>(max_row_tiles(B, 1, 256)) * ((N + 255) / 256);
+    int ks = 1;
+    while (ks * 2 <= kLinearMaxSplit && tiles * ks * 2 <= 256) ks *= 2;
+    t.ksplit = ks;
+    while (t.ksplit > 1 && !gemm_tiled256_supported(t)) t.ksplit /= 2;
+    if (t.ksplit > 1) {
+      FMOE_HIP(launch_gemm_tiled(t, s, TILED_256));
+      g_last_path = FMOE_PATH_TILED_LARGE;
+      *nsplit = t.ksplit;
+      return FMOE_OK;
+    }
+  }
   return run_grouped_gemm(g, s);
 }
 
