@@ -204,15 +204,19 @@ def test_attention_block_decode_reference_signature(fm):
         assert_close_rms(g, r, 1e-4)
 
 
-def test_attention_block_decode_fp8_weights(fm):
-    rng = np.random.default_rng(12)
-    B, ctx, n_embd, H, Hkv = 3, 400, 1024, 8, 2
+@pytest.mark.parametrize("B", [3, 20, 48])
+def test_attention_block_decode_fp8_weights(fm, B):
+    """fp8-e4m3 projection weights: streamed with the fused epilogues (3
+    rows), streamed with a K split and the separate RoPE (20 rows), and on
+    the 256-row tile kernel with a K split (48 rows)."""
+    rng = np.random.default_rng(12 + B)
+    ctx, n_embd, H, Hkv = 400, 1024, 8, 2
     D = n_embd // H
     w, b, hw = _weights(rng, n_embd, Hkv * D, torch.bfloat16, fp8=True)
     x = _round(rng.standard_normal((B, n_embd)), torch.bfloat16)
     kc = _round(rng.standard_normal((B, ctx, Hkv, D)), torch.bfloat16)
     vc = _round(rng.standard_normal((B, ctx, Hkv, D)), torch.bfloat16)
-    pos = np.array([5, 100, 1000], np.int64)
+    pos = rng.integers(0, 4096, B).astype(np.int64)
     blk = fm.AttentionBlockDecode(*(_dev(w[k], torch.bfloat16) for k in ("wq", "wk", "wv", "wo")), n_head=H,
                                   n_head_kv=Hkv, n_embd=n_embd, act_dtype=torch.bfloat16, weight_dtype="fp8")
     out, _, _ = blk(_dev(x, torch.bfloat16), torch.from_numpy(pos).cuda(), _dev(kc, torch.bfloat16),
