@@ -531,7 +531,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs a) {
 // dimension d over the splits, kCombineUnroll loads at a time.
 constexpr int kCombineThreads = 128;  // >= head_dim
 constexpr int kCombineChunk = 1024;   // splits whose weights are held in LDS at once
-constexpr int kCombineUnroll = 8;
+constexpr int kCombineUnroll = 16;
 constexpr int kCombinePre = 16;       // splits (4096 positions) prefetched into registers
 
 // Blocks x = n_head and n_head + 1 (launched only with a scatter) write
