@@ -125,6 +125,7 @@ CASES = [
     (4, 513, 4096, 32, 8, True, "bf16"),   # Mixtral heads: head_dim 128, 4 per KV head
     (1, 256, 4096, 32, 8, False, "bf16"),  # exactly one split
     (40, 100, 512, 4, 2, True, "bf16"),    # 40 rows: RoPE after a K-split Q/K/V product
+    (40, 50, 320, 5, 5, True, "bf16"),     # 40 rows, 960 / 320 outputs: partial 256-column tiles, K split
     # bf16 scores on the matrix cores (head_dim 64 / 128) for every group
     # size, with contexts that end inside an 8-position tile
     (3, 77, 512, 4, 4, False, "bf16"),     # head_dim 128, MHA
