@@ -189,43 +189,11 @@ __global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------ split attention
-template <typename T, int CW>
-__device__ __forceinline__ void load_chunk(const T* p, float (&v)[CW]);
-
-template <>
-__device__ __forceinline__ void load_chunk<float, 2>(const float* p, float (&v)[2]) {
-  const float2 x = *reinterpret_cast<const float2*>(p);
-  v[0] = x.x, v[1] = x.y;
-}
-template <>
-__device__ __forceinline__ void load_chunk<float, 4>(const float* p, float (&v)[4]) {
-  const float4 x = *reinterpret_cast<const float4*>(p);
-  v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
-}
+// Two bf16 (low element first) -> two floats.
 __device__ __forceinline__ void unpack2(uint32_t w, float* v) {
   v[0] = __uint_as_float(w << 16);
   v[1] = __uint_as_float(w & 0xFFFF0000u);
 }
-template <>
-__device__ __forceinline__ void load_chunk<bf16_t, 2>(const bf16_t* p, float (&v)[2]) {
-  unpack2(*reinterpret_cast<const uint32_t*>(p), v);
-}
-template <>
-__device__ __forceinline__ void load_chunk<bf16_t, 4>(const bf16_t* p, float (&v)[4]) {
-  const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
-  unpack2(x[0], v);
-  unpack2(x[1], v + 2);
-}
-template <>
-__device__ __forceinline__ void load_chunk<bf16_t, 8>(const bf16_t* p, float (&v)[8]) {
-  const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
-  unpack2(x[0], v);
-  unpack2(x[1], v + 2);
-  unpack2(x[2], v + 4);
-  unpack2(x[3], v + 6);
-}
-__device__ __forceinline__ float load_one(const float* p) { return *p; }
-__device__ __forceinline__ float load_one(const bf16_t* p) { return bf16_to_f32(*p); }
 
 __device__ __forceinline__ f32x4_t attn_mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
