@@ -423,6 +423,7 @@ class MoEFFNBlock:
                             self.n_expert, self.n_embd, self.n_ff)
         self._ws = None
         self._ws_key = None
+        self._last = None  # n_tokens of the last call that completed its launches
 
     def workspace_bytes(self, n_tokens: int, sublayer: bool = False) -> int:
         fn = "fmoe_moe_ffn_sublayer_workspace_bytes" if sublayer else "fmoe_moe_ffn_block_workspace_bytes"
@@ -443,13 +444,26 @@ class MoEFFNBlock:
             raise ValueError(f"x must be [n_tokens, {self.n_embd}]")
         x = x.contiguous()
         T = int(x.shape[0])
-        if out is None:
-            out = torch.empty((T, self.n_embd), dtype=x.dtype, device=x.device)
+        out = self._check_out(out, T, x.device)
         ws = self._get_ws(T)
+        self._last = None
         L.call("fmoe_moe_ffn_block", _ptr(x), _ptr(self.wr), _ptr(self.up.data), _ptr(self.gate.data),
                _ptr(self.down.data), _ptr(self.up.scales), _ptr(self.gate.scales), _ptr(self.down.scales),
                self.wdt, _ptr(out), T, self.n_expert, self.k, self.n_embd, self.n_ff,
                int(self.normalize), self.act, _ptr(ws), ws.numel(), _stream())
+        self._last = T
+        return out
+
+    def _check_out(self, out, T, device):
+        """The output tensor: a new one, or the caller's ``out=`` after the
+        checks the C ABI cannot make (it writes T * n_embd elements of the
+        activation dtype through the raw pointer)."""
+        dt = _DT_TO_TORCH[self.act]
+        if out is None:
+            return torch.empty((T, self.n_embd), dtype=dt, device=device)
+        if (not isinstance(out, torch.Tensor) or out.device != device or out.dtype != dt
+                or tuple(out.shape) != (T, self.n_embd) or not out.is_contiguous()):
+            raise ValueError(f"out must be a contiguous {dt} [{T}, {self.n_embd}] tensor on {device}")
         return out
 
     def sublayer(self, residual: torch.Tensor, ffn_norm_w, rms_eps: float,
@@ -470,23 +484,27 @@ class MoEFFNBlock:
         nw = nw.to(dt).contiguous()
         residual = residual.contiguous()
         T = int(residual.shape[0])
-        if out is None:
-            out = torch.empty((T, self.n_embd), dtype=dt, device=residual.device)
-        elif out.dtype != dt or tuple(out.shape) != (T, self.n_embd) or not out.is_contiguous():
-            raise ValueError(f"out must be a contiguous {dt} [{T}, {self.n_embd}] tensor")
+        out = self._check_out(out, T, residual.device)
         ws = self._get_ws(T, sublayer=True)
+        self._last = None
         L.call("fmoe_moe_ffn_sublayer", _ptr(residual), _ptr(nw), float(rms_eps), _ptr(self.wr),
                _ptr(self.up.data), _ptr(self.gate.data), _ptr(self.down.data), _ptr(self.up.scales),
                _ptr(self.gate.scales), _ptr(self.down.scales), self.wdt, _ptr(out), T, self.n_expert, self.k,
                self.n_embd, self.n_ff, int(self.normalize), self.act, _ptr(ws), ws.numel(), _stream())
+        self._last = T
         return out
 
-    def routing(self, n_tokens: int):
-        """Device views of the routing computed by the last call:
-        ``(ids [k, T], weights [k, T], order [k*T], offsets [E+1])``."""
+    def routing(self, n_tokens: Optional[int] = None):
+        """Device views of the routing computed by the last call (block or
+        sub-layer): ``(ids [k, T], weights [k, T], order [k*T], offsets
+        [E+1])``.  ``n_tokens``, when given, must be that call's T."""
         ws = self._ws
-        if ws is None:
-            raise RuntimeError("no call has run yet")
+        if ws is None or self._last is None:
+            raise RuntimeError("no call has completed on this block yet")
+        if n_tokens is None:
+            n_tokens = self._last
+        elif int(n_tokens) != self._last:
+            raise ValueError(f"n_tokens={n_tokens}, but the last call ran {self._last} tokens")
         ptrs = [ctypes.c_void_p() for _ in range(4)]
         L.call("fmoe_moe_ffn_block_routing", _ptr(ws), n_tokens, self.n_expert, self.k, self.n_embd,
                self.n_ff, self.act, self.wdt, *[ctypes.byref(p) for p in ptrs])

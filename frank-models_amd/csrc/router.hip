@@ -106,10 +106,11 @@ __device__ __forceinline__ float ror16(float v) {
 // once, one per 16-lane row: row g takes token t0 + g, whose logits are
 // lg[g * ld + e]; lane j of the row holds experts j, j + 16, ... (NV each:
 // each is a few VALU instructions per slot, at 4 cycles each for a wave).  Reductions over the row
-// use DPP rotations.  The selection runs on the logits (the softmax is
-// monotonic with one denominator per token, so the order and exact ties
-// are those of the probabilities): larger first, lower expert index on
-// ties.  Each token's denominator is the one its lane 0 summed.
+// use DPP rotations.  The selection runs on the fp32 probabilities, as the
+// reference's top-k does: logits a few ulps apart can round to one
+// probability, and that tie goes to the lower expert index.  Larger first,
+// lower expert index on ties.  Each token's denominator is the one its
+// lane 0 summed.
 template <int NV>
 __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int n_expert, int k, bool normalize,
                               int* ids, float* weights, int* ids_copy = nullptr) {
@@ -131,21 +132,27 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
   m = fmaxf(m, ror16<1>(m));
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (j + 16 * i < n_expert) s += expf(v[i] - m);
+  for (int i = 0; i < NV; ++i) {
+    v[i] = j + 16 * i < n_expert ? expf(v[i] - m) : 0.f;
+    s += v[i];
+  }
   s += ror16<8>(s);
   s += ror16<4>(s);
   s += ror16<2>(s);
   s += ror16<1>(s);
   s = __shfl(s, lane & ~15, kWave);
-  float my_l = -INFINITY;
+  // Probabilities; -1 marks an expert that cannot be selected (absent, or
+  // already taken).
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = j + 16 * i < n_expert ? v[i] / s : -1.f;
+  float my_w = 0.f;
   int my_id = 0;
   for (int slot = 0; slot < k; ++slot) {
-    float bv = -INFINITY;
+    float bv = -1.f;
     int bi = 0x7FFFFFFF;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      if (j + 16 * i < n_expert && v[i] > bv) {  // i ascending: ties keep the lower expert
+      if (v[i] > bv) {  // i ascending: ties keep the lower expert
         bv = v[i];
         bi = j + 16 * i;
       }
@@ -166,13 +173,12 @@ __device__ void softmax_topk4(const float* lg, int ld, int t0, int n_tokens, int
 #undef FMOE_TOPK_STEP
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (j + 16 * i == bi) v[i] = -INFINITY;
+      if (j + 16 * i == bi) v[i] = -1.f;
     if (j == slot) {
-      my_l = bv;
+      my_w = bv;
       my_id = bi;
     }
   }
-  float my_w = expf(my_l - m) / s;
   if (normalize) {
     // Sum in slot order (the linalg reduction of moe_ffn_block.mlir:97-107).
     float wsum = 0.f;

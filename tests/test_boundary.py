@@ -194,3 +194,47 @@ def test_packed_layout_is_a_bijection(shape, dt):
 
     idx = packed_index(*shape, dt).reshape(-1)
     assert np.array_equal(np.sort(idx), np.arange(idx.size))
+
+
+def _bare_block(fm, n_embd=8):
+    """A MoEFFNBlock shell holding only what its host-side checks read (no
+    packed weights, so no device is needed)."""
+    blk = fm.MoEFFNBlock.__new__(fm.MoEFFNBlock)
+    blk.act = fm.lowlevel.BF16
+    blk.n_embd = n_embd
+    blk._ws = None
+    blk._last = None
+    return blk
+
+
+def test_block_out_argument_is_checked(fm):
+    """out= reaches the C ABI as a raw pointer that the combine kernel writes
+    T * n_embd elements through: shape, dtype, device and contiguity are
+    checked first."""
+    blk = _bare_block(fm)
+    cpu = torch.device("cpu")
+    good = torch.empty((3, 8), dtype=torch.bfloat16)
+    assert blk._check_out(good, 3, cpu) is good
+    assert blk._check_out(None, 3, cpu).shape == (3, 8)
+    for bad in (torch.empty((2, 8), dtype=torch.bfloat16),          # too few rows
+                torch.empty((3, 9), dtype=torch.bfloat16),          # wrong width
+                torch.empty((3, 8), dtype=torch.float32),           # wrong dtype
+                torch.empty((8, 3), dtype=torch.bfloat16).t(),      # not contiguous
+                torch.empty((24,), dtype=torch.bfloat16)):          # flat
+        with pytest.raises(ValueError):
+            blk._check_out(bad, 3, cpu)
+    with pytest.raises(ValueError):
+        blk._check_out(good, 3, torch.device("meta"))               # another device
+
+
+def test_block_routing_needs_the_last_calls_token_count(fm):
+    blk = _bare_block(fm)
+    with pytest.raises(RuntimeError):
+        blk.routing()
+    blk._ws = torch.zeros(4096, dtype=torch.uint8)
+    blk._last = None  # a call that raised before completing its launches
+    with pytest.raises(RuntimeError):
+        blk.routing(16)
+    blk._last = 16
+    with pytest.raises(ValueError):
+        blk.routing(17)

@@ -11,7 +11,8 @@ import oracle
 from oracle import moe as om
 from oracle import numerics as nm
 from helpers import assert_close, packed_index
-from test_oracle import BLOCK_REFERENCE_CASES, MMID_REFERENCE_CASES, REFERENCE_IDS, _mmid_case, block_inputs
+from test_oracle import (BLOCK_REFERENCE_CASES, MMID_REFERENCE_CASES, REFERENCE_IDS, _mmid_case, block_inputs,
+                         ulp_tie_router_inputs)
 
 pytestmark = pytest.mark.gpu
 
@@ -161,6 +162,24 @@ def test_router_ties_lower_index(fm):
             wr[:, :3] = logits
             ids, w = fm.router(torch.from_numpy(xx).to("cuda", dt), torch.from_numpy(wr).to("cuda", dt), 2, False)
             np.testing.assert_array_equal(ids.cpu().numpy(), [[1, 0, 0], [2, 1, 1]])
+
+
+# Logits one ulp apart have one fp32 probability: the selection runs on the
+# probabilities (lower expert index first), on every router kernel: the SIMT
+# kernel (fp32), the MFMA kernel (bf16, T > 64), the decode pair (bf16,
+# T <= 64), and the one-token-per-wave top-k (k > 16).
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [1, 16, 100])
+@pytest.mark.parametrize("E,k", [(8, 3), (40, 18)])
+def test_router_ulp_apart_logits(fm, dt, T, E, k):
+    x, wr = ulp_tie_router_inputs(E, 64, T)
+    want, want_w = om.router(x, wr, k, False, dtype=np.float32)
+    assert list(want[:3, 0]) == [2, 5, 0]
+    for norm in (False, True):
+        ids, w = fm.router(torch.from_numpy(x).to("cuda", dt), torch.from_numpy(wr).to("cuda", dt), k, norm)
+        ids, w = ids.cpu().numpy(), w.cpu().numpy()
+        np.testing.assert_array_equal(ids, want)
+        assert np.array_equal(w[0], w[1])  # the tied pair has one weight
 
 
 def test_router_many_experts_and_k(fm):

@@ -108,6 +108,39 @@ def test_router_ties_go_to_lower_index():
     assert not np.array_equal(bad, ids)
 
 
+def ulp_tie_router_inputs(E, H, T):
+    """Router inputs whose fp32 logits for experts 2 and 5 are one ulp apart
+    (c and c + 2**-37 with c = 1.5 * 2**-14, both exact in bf16 and in an
+    fp32 sum) while every other expert's logit is -1: exp of a -7.3e-12
+    difference rounds to 1 in fp32, so the two probabilities are equal.  The
+    larger logit sits at the higher index, so selecting on logits and
+    selecting on fp32 probabilities disagree on the slot order."""
+    c = 1.5 * 2.0**-14
+    x = np.zeros((T, H), np.float32)
+    x[:, :2] = 1.0
+    wr = np.zeros((E, H), np.float32)
+    wr[:, 0] = -1.0
+    wr[2, 0] = c
+    wr[5, 0] = c
+    wr[5, 1] = 2.0**-37
+    return x, wr
+
+
+def test_router_ulp_apart_logits_tie_on_fp32_probabilities():
+    E, k = 8, 3
+    x, wr = ulp_tie_router_inputs(E, 64, 4)
+    logits = (wr @ x.T).astype(np.float32)
+    assert logits[5, 0] == np.nextafter(logits[2, 0], np.float32(1))  # one ulp apart
+    ids32, w32 = om.router(x, wr, k, False, dtype=np.float32)
+    # fp32 probabilities tie: the lower index first, then expert 0 (lowest of
+    # the equal -1 logits)
+    np.testing.assert_array_equal(ids32[:, 0], [2, 5, 0])
+    assert w32[0, 0] == w32[1, 0]
+    # in float64 the larger logit wins: exact ties exist only at fp32
+    ids64, _ = om.router(x, wr, k, False)
+    np.testing.assert_array_equal(ids64[:, 0], [5, 2, 0])
+
+
 def test_router_renormalisation():
     rng = np.random.default_rng(2)
     x = rng.standard_normal((20, 16))
