@@ -41,6 +41,9 @@ PATH_STREAM = 3
 PATH_TILED_LARGE = 4
 
 
+# FMOE_NOALLOC_SCRATCH_BYTES: the allocation-free block's fixed scratch size
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
 # fmoe_timer
 TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id", "norm", "qkv", "attention", "out_proj")
 
@@ -95,6 +98,11 @@ SIGNATURES = {
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp, _sz, _vp],
+    ),
+    "fmoe_moe_ffn_block_noalloc": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp],
     ),
     "fmoe_rms_norm": (_c_int, [_vp, _vp, ctypes.c_float, _vp, _c_i64, _c_i64, _c_int, _vp]),
     "fmoe_moe_ffn_sublayer_workspace_bytes": (_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),

@@ -437,7 +437,11 @@ class MoEFFNBlock:
             self._ws_key = key
         return self._ws
 
-    def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, noalloc: bool = False) -> torch.Tensor:
+        """``noalloc=True`` runs fmoe_moe_ffn_block_noalloc: no workspace,
+        the library's fixed per-GPU scratch instead (at most
+        NOALLOC_SCRATCH_BYTES of workspace; calls on one GPU must not
+        overlap), and ``routing()`` is not available afterwards."""
         if x.dtype != _DT_TO_TORCH[self.act] or x.device.type != "cuda":
             raise TypeError(f"x must be a {_DT_TO_TORCH[self.act]} device tensor")
         if x.dim() != 2 or x.shape[1] != self.n_embd:
@@ -445,8 +449,14 @@ class MoEFFNBlock:
         x = x.contiguous()
         T = int(x.shape[0])
         out = self._check_out(out, T, x.device)
-        ws = self._get_ws(T)
         self._last = None
+        if noalloc:
+            L.call("fmoe_moe_ffn_block_noalloc", _ptr(x), _ptr(self.wr), _ptr(self.up.data), _ptr(self.gate.data),
+                   _ptr(self.down.data), _ptr(self.up.scales), _ptr(self.gate.scales), _ptr(self.down.scales),
+                   self.wdt, _ptr(out), T, self.n_expert, self.k, self.n_embd, self.n_ff,
+                   int(self.normalize), self.act, _stream())
+            return out
+        ws = self._get_ws(T)
         L.call("fmoe_moe_ffn_block", _ptr(x), _ptr(self.wr), _ptr(self.up.data), _ptr(self.gate.data),
                _ptr(self.down.data), _ptr(self.up.scales), _ptr(self.gate.scales), _ptr(self.down.scales),
                self.wdt, _ptr(out), T, self.n_expert, self.k, self.n_embd, self.n_ff,

@@ -118,8 +118,8 @@ hipEvent_t take_event() {
 
 class ScopedTimer {
  public:
-  ScopedTimer(int timer, hipStream_t s) : timer_(timer), s_(s) {
-    if (!g_timing.load(std::memory_order_relaxed)) return;
+  ScopedTimer(int timer, hipStream_t s, bool allowed = true) : timer_(timer), s_(s) {
+    if (!allowed || !g_timing.load(std::memory_order_relaxed)) return;
     std::lock_guard<std::mutex> lk(g_t_mu);
     start_ = take_event();
     stop_ = take_event();
@@ -333,6 +333,7 @@ struct BlockCall {
   void* workspace;
   size_t workspace_bytes;
   void* stream;
+  bool timers = true;    // false: no timing events (the allocation-free entry point)
 };
 
 // The block's workspace followed by the normalised input rows.
@@ -350,6 +351,7 @@ SublayerLayout sublayer_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64
 }
 
 int check_workspace(const void* ws, size_t bytes, size_t need) {
+  if (!ws) return fail(FMOE_ERR_INVALID_ARGUMENT, "null workspace");
   if (bytes < need) return fail(FMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", bytes, need);
   if (reinterpret_cast<uintptr_t>(ws) % kAlign)
     return fail(FMOE_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
@@ -368,7 +370,7 @@ int validate_block(const BlockCall& c) {
   if (c.normalize_weights != 0 && c.normalize_weights != 1)
     return fail(FMOE_ERR_INVALID_ARGUMENT, "normalize_weights must be 0 or 1");
   if (c.n_tokens == 0) return FMOE_OK;
-  if (!c.input || !c.w_router || !c.packed_up || !c.packed_gate || !c.packed_down || !c.out || !c.workspace)
+  if (!c.input || !c.w_router || !c.packed_up || !c.packed_gate || !c.packed_down || !c.out)
     return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
   if (c.w_dtype == FMOE_F8E4M3FN && (!c.up_scales || !c.gate_scales || !c.down_scales))
     return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
@@ -401,17 +403,17 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   const bool decode_router = L.rpart_bytes > 0 && reinterpret_cast<uintptr_t>(c.input) % 16 == 0 &&
                              reinterpret_cast<uintptr_t>(c.w_router) % 16 == 0;
   if (decode_router) {
-    ScopedTimer t(FMOE_TIMER_ROUTER, s);
+    ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
     FMOE_HIP(launch_router_decode(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
                                   static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype,
                                   at<float>(workspace, L.rpart), ids, rw, order, offsets, err, s));
   } else {
     {
-      ScopedTimer t(FMOE_TIMER_ROUTER, s);
+      ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
       FMOE_HIP(launch_router(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
                              static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype, ids, rw, s));
     }
-    ScopedTimer t(FMOE_TIMER_PERMUTE, s);
+    ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
     FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err,
                             at<int>(workspace, L.perm.scratch), s));
   }
@@ -443,7 +445,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   g.out_dtype = L.h_dtype;
   g.max_rows_per_expert = T;  // top-k experts are distinct per token
   {
-    ScopedTimer t(FMOE_TIMER_GATE_UP, s);
+    ScopedTimer t(FMOE_TIMER_GATE_UP, s, c.timers);
     FMOE_TRY(run_grouped_gemm(g, s));
   }
 
@@ -473,14 +475,14 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   d.max_rows_per_expert = T;
   int down_split = 1;
   {
-    ScopedTimer t(FMOE_TIMER_DOWN, s);
+    ScopedTimer t(FMOE_TIMER_DOWN, s, c.timers);
     FMOE_TRY(run_grouped_gemm(d, s, &down_split));
   }
 
   // Step 11: slot-ordered sum + transpose to [n_tokens, n_embd] (mlir:179-206),
   // plus the residual for the sub-layer.
   {
-    ScopedTimer t(FMOE_TIMER_COMBINE, s);
+    ScopedTimer t(FMOE_TIMER_COMBINE, s, c.timers);
     FMOE_HIP(launch_combine(y, L.y_dtype, c.residual, c.out, act_dtype, T, static_cast<int>(n_expert_used),
                             static_cast<int>(n_embd), down_split, L.y_part_elems, s));
   }
@@ -996,6 +998,35 @@ int fmoe_moe_ffn_block(const void* input, const void* w_router, const void* pack
   const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
   FMOE_TRY(check_workspace(workspace, workspace_bytes, L.total));
   FMOE_TRY(ensure_device());
+  return run_block(c, L);
+}
+
+int fmoe_moe_ffn_block_noalloc(const void* input, const void* w_router, const void* packed_up,
+                               const void* packed_gate, const void* packed_down, const float* up_scales,
+                               const float* gate_scales, const float* down_scales, int w_dtype, void* out,
+                               int64_t n_tokens, int64_t n_expert, int64_t n_expert_used, int64_t n_embd,
+                               int64_t n_ff, int normalize_weights, int act_dtype, void* stream) {
+  BlockCall c{input,     w_router,   packed_up,     packed_gate, packed_down,       up_scales,
+              gate_scales, down_scales, w_dtype,    out,         nullptr,           n_tokens,
+              n_expert,  n_expert_used, n_embd,     n_ff,        normalize_weights, act_dtype,
+              nullptr,   0,          stream};
+  c.timers = false;
+  FMOE_TRY(validate_block(c));
+  if (n_tokens == 0) return ok();
+  const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
+  if (L.total > FMOE_NOALLOC_SCRATCH_BYTES)
+    return fail(FMOE_ERR_WORKSPACE,
+                "fmoe_moe_ffn_block_noalloc: %lld tokens need %zu bytes of scratch, above its fixed %zu bytes "
+                "(FMOE_NOALLOC_SCRATCH_BYTES); use fmoe_moe_ffn_block with a workspace",
+                static_cast<long long>(n_tokens), L.total, static_cast<size_t>(FMOE_NOALLOC_SCRATCH_BYTES));
+  int dev = 0;
+  FMOE_TRY(ensure_device(&dev));
+  // The scratch array's device address on this device (hipGetSymbolAddress
+  // on first use, then cached); never the array itself.
+  void* scratch = nullptr;
+  FMOE_HIP(noalloc_scratch(dev, &scratch));
+  c.workspace = scratch;
+  c.workspace_bytes = FMOE_NOALLOC_SCRATCH_BYTES;
   return run_block(c, L);
 }
 

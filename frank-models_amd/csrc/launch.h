@@ -195,6 +195,11 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert,
                                     hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
+// Device address of the allocation-free entry point's scratch array
+// (FMOE_NOALLOC_SCRATCH_BYTES, noalloc.hip) on `device`, which must be the
+// current device; looked up on first use and cached per device.
+hipError_t noalloc_scratch(int device, void** ptr);
+
 // Dense src [n_in, n_part] (x @ W layout; F32 or BF16) -> rows [row0,
 // row0 + n_part) of the one-expert packed weight [n_total, n_in] (pack.hip).
 hipError_t launch_pack_linear(const void* src, int src_dtype, int n_in, int n_part, int row0, int n_total,

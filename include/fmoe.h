@@ -203,6 +203,29 @@ int fmoe_moe_ffn_block(const void *input, const void *w_router, const void *pack
                        int act_dtype, void *workspace, size_t workspace_bytes,
                        void *stream);
 
+/* The MoE FFN block without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Arguments and results are those of fmoe_moe_ffn_block; the
+ * workspace is a device-resident scratch array of FMOE_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends.
+ * The call allocates nothing (no hipMalloc, no library allocation; kernel
+ * timing is not recorded for it).  A call whose
+ * fmoe_moe_ffn_block_workspace_bytes exceed FMOE_NOALLOC_SCRATCH_BYTES
+ * (Mixtral shapes: about 500 tokens) fails with FMOE_ERR_WORKSPACE before
+ * any device work.  Every call on one GPU shares that GPU's array and
+ * leaves its contents behind: calls that overlap on one GPU (two streams,
+ * two host threads) race, so the caller serialises them.
+ * fmoe_moe_ffn_block_routing cannot read this scratch. */
+#define FMOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int fmoe_moe_ffn_block_noalloc(const void *input, const void *w_router, const void *packed_up,
+                               const void *packed_gate, const void *packed_down,
+                               const float *up_scales, const float *gate_scales,
+                               const float *down_scales, int w_dtype, void *out,
+                               int64_t n_tokens, int64_t n_expert, int64_t n_expert_used,
+                               int64_t n_embd, int64_t n_ff, int normalize_weights,
+                               int act_dtype, void *stream);
+
 /* RMS normalisation of each row: out = (x / sqrt(mean(x^2) + eps)) * weight,
  * x and out [n_rows, n_embd], weight [n_embd], all of `dtype` (F32 or BF16),
  * fp32 arithmetic.  Replaces @rms_norm_linalg

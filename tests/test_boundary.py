@@ -238,3 +238,20 @@ def test_block_routing_needs_the_last_calls_token_count(fm):
     blk._last = 16
     with pytest.raises(ValueError):
         blk.routing(17)
+
+
+def test_noalloc_block_rejects_oversize_before_device(fm):
+    """fmoe_moe_ffn_block_noalloc checks its fixed scratch size (and its
+    arguments) before it touches a device."""
+    ll = fm.lowlevel
+    lib = ll.lib()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced
+    need = lib.fmoe_moe_ffn_block_workspace_bytes(4096, 8, 2, 4096, 14336, ll.BF16, ll.BF16)
+    assert need > ll.NOALLOC_SCRATCH_BYTES
+    r = st(fm, "fmoe_moe_ffn_block_noalloc", fake, fake, fake, fake, fake, None, None, None, ll.BF16, fake,
+           4096, 8, 2, 4096, 14336, 0, ll.BF16, None)
+    assert r == ll.ERR_WORKSPACE and "FMOE_NOALLOC_SCRATCH_BYTES" in ll.last_error()
+    assert st(fm, "fmoe_moe_ffn_block_noalloc", None, None, None, None, None, None, None, None, ll.BF16, None,
+              0, 8, 2, 64, 128, 0, ll.BF16, None) == ll.OK  # no tokens
+    assert st(fm, "fmoe_moe_ffn_block_noalloc", fake, None, fake, fake, fake, None, None, None, ll.BF16, fake,
+              16, 8, 2, 64, 128, 0, ll.BF16, None) == ll.ERR_INVALID_ARGUMENT  # null router
