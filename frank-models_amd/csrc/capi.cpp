@@ -138,11 +138,9 @@ class ScopedTimer {
   hipEvent_t start_ = nullptr, stop_ = nullptr;
 };
 
-// Runs one grouped GEMM on the family the process-wide setting asks for,
-// falling back to the automatic choice when that family cannot run it.
-// `g.split_stride` > 0 offers room for a K split into fp32 partials; the
-// split used is returned in *ksplit_used (1 if none).
-int run_grouped_gemm(GroupedGemmArgs g, hipStream_t s, int* ksplit_used = nullptr) {
+// The kernel family (FMOE_PATH_*) and tiled variant run_grouped_gemm takes
+// for g under the process-wide setting.
+int pick_path(const GroupedGemmArgs& g, int* variant_out) {
   const int want = g_path.load(std::memory_order_relaxed);
   GroupedGemmArgs probe = g;
   probe.ksplit = 1;
@@ -173,11 +171,21 @@ int run_grouped_gemm(GroupedGemmArgs g, hipStream_t s, int* ksplit_used = nullpt
     else if (can_stream)
       path = FMOE_PATH_STREAM;
   }
+  if (path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE) variant = resolve_tiled_variant(probe, variant);
+  *variant_out = variant;
+  return path;
+}
+
+// Runs one grouped GEMM on the family the process-wide setting asks for,
+// falling back to the automatic choice when that family cannot run it.
+// `g.split_stride` > 0 offers room for a K split into fp32 partials; the
+// split used is returned in *ksplit_used (1 if none).
+int run_grouped_gemm(GroupedGemmArgs g, hipStream_t s, int* ksplit_used = nullptr) {
+  int variant = TILED_AUTO;
+  const int path = pick_path(g, &variant);
   g.ksplit = 1;
-  if (path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE) {
-    variant = resolve_tiled_variant(probe, variant);
-    if (variant == TILED_256 && g.split_stride > 0) g.ksplit = gemm_tiled256_ksplit(g);
-  }
+  if ((path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE) && variant == TILED_256 && g.split_stride > 0)
+    g.ksplit = gemm_tiled256_ksplit(g);
   hipError_t e;
   if (path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE)
     e = launch_gemm_tiled(g, s, variant);
@@ -234,6 +242,7 @@ struct BlockLayout {
   size_t ids, weights;
   PermuteLayout perm;
   size_t h, y, total;
+  size_t xkb, xkb_bytes;  // token rows gathered K-blocked in expert order (0 bytes when no prefill GEMM can use them)
   size_t rpart;          // decode router's split logits (0 bytes when the shape takes the general router)
   size_t rpart_bytes;
   int h_dtype, y_dtype;
@@ -284,6 +293,12 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   L.y_parts = (n > 0 && H > 0 && F > 0) ? gemm_tiled256_ksplit(down_shape(T, E, k, H, F, act, wdt)) : 1;
   L.y = off;
   off += align_up(static_cast<size_t>(n) * H * dtype_bytes(L.y_dtype) * L.y_parts);
+  // Prefill-sized bf16 batches: room for the token rows gathered into expert
+  // order, K-blocked, so the gate/up GEMM reads whole cache lines.
+  const bool kb_candidate = act == FMOE_BF16 && n > 8 * E && H % 64 == 0 && F % 64 == 0;
+  L.xkb = off;
+  L.xkb_bytes = kb_candidate ? static_cast<size_t>(n) * H * 2 : 0;
+  off += align_up(L.xkb_bytes);
   L.total = off;
   return L;
 }
@@ -444,35 +459,48 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   g.w_format = packed_format(n_ff, n_embd, w_dtype);
   g.out_dtype = L.h_dtype;
   g.max_rows_per_expert = T;  // top-k experts are distinct per token
+  GroupedGemmArgs d = down_shape(T, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
+  d.a = h;
+  d.order = order;
+  d.offsets = offsets;
+  d.w0 = c.packed_down;
+  d.s0 = w_dtype == FMOE_F8E4M3FN ? c.down_scales : nullptr;
+  d.out = y;
+  d.route_w = rw;
+  d.act_dtype = L.h_dtype;
+  d.split_stride = L.y_parts > 1 ? L.y_part_elems : 0;
+  d.max_rows_per_expert = T;
+
+  // When both GEMMs take the 256-tile kernel, their A operands go K-blocked
+  // (64-byte row pieces, one contiguous run per 32-input stage of a tile):
+  // the token rows are gathered into expert order first, and the gate/up
+  // epilogue writes h in that layout for the down GEMM.
+  if (L.xkb_bytes) {
+    int vg = 0, vd = 0;
+    const int pg = pick_path(g, &vg), pd = pick_path(d, &vd);
+    GroupedGemmArgs gk = g, dk = d;
+    void* xkb = at<char>(workspace, L.xkb);
+    gk.a = xkb;
+    gk.a_mode = A_DIRECT;
+    gk.a_kb_rows = n;
+    gk.out_kb_rows = n;
+    dk.a_kb_rows = n;
+    const bool tiled_g = pg == FMOE_PATH_TILED || pg == FMOE_PATH_TILED_LARGE;
+    const bool tiled_d = pd == FMOE_PATH_TILED || pd == FMOE_PATH_TILED_LARGE;
+    if (tiled_g && tiled_d && vg == TILED_256 && vd == TILED_256 && gemm_tiled256_supported(gk) &&
+        gemm_tiled256_supported(dk)) {
+      ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
+      FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), xkb, s));
+      g = gk;
+      d = dk;
+    }
+  }
   {
     ScopedTimer t(FMOE_TIMER_GATE_UP, s, c.timers);
     FMOE_TRY(run_grouped_gemm(g, s));
   }
 
   // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
-  GroupedGemmArgs d;
-  d.a = h;
-  d.lda = n_ff;
-  d.a_mode = A_DIRECT;
-  d.order = order;
-  d.offsets = offsets;
-  d.n_tokens = T;
-  d.n_assign = n;
-  d.n_expert = static_cast<int>(n_expert);
-  d.w0 = c.packed_down;
-  d.s0 = w_dtype == FMOE_F8E4M3FN ? c.down_scales : nullptr;
-  d.N = n_embd;
-  d.K = n_ff;
-  d.out = y;
-  d.ldo = n_embd;
-  d.epi = EPI_SCATTER_WEIGHTED;
-  d.route_w = rw;
-  d.act_dtype = L.h_dtype;
-  d.w_dtype = w_dtype;
-  d.w_format = packed_format(n_embd, n_ff, w_dtype);
-  d.out_dtype = L.y_dtype;
-  d.split_stride = L.y_parts > 1 ? L.y_part_elems : 0;
-  d.max_rows_per_expert = T;
   int down_split = 1;
   {
     ScopedTimer t(FMOE_TIMER_DOWN, s, c.timers);

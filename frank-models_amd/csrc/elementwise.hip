@@ -17,6 +17,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <algorithm>
+
 namespace fmoe {
 namespace {
 
@@ -114,6 +116,31 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const TY* __restrict_
       for (int j = 0; j < V; ++j) acc[j] = p[j] + acc[j];
     }
     stv<V>(out, i, acc);
+  }
+}
+
+// dst row p = src row order[p] % n_tokens, written K-blocked (kb_offset):
+// each thread copies one 16-byte chunk.  A wave takes 16 rows x 64 bytes of
+// one 32-column block, so its stores are one contiguous 1 KiB run; the
+// waves of a row group walk its blocks in order, so the source rows are read
+// in whole cache lines by neighbouring waves.
+__global__ __launch_bounds__(kThreads) void gather_rows_kb_kernel(const bf16_t* __restrict__ src,
+                                                                  const int* __restrict__ order, int n_rows,
+                                                                  int n_tokens, int n_cols,
+                                                                  bf16_t* __restrict__ dst) {
+  const int64_t nblk = n_cols / 32;
+  const int64_t total = (static_cast<int64_t>(n_rows) + 15) / 16 * nblk * kWave;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int lane = static_cast<int>(i & (kWave - 1));
+    const int64_t w = i / kWave;
+    const int64_t rg = w / nblk, j = w - rg * nblk;
+    const int64_t p = rg * 16 + (lane >> 2);
+    if (p >= n_rows) continue;
+    const int ch = lane & 3;
+    const int64_t srow = static_cast<uint32_t>(order[p]) % static_cast<uint32_t>(n_tokens);
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + srow * n_cols + j * 32 + ch * 8);
+    *reinterpret_cast<u32x4_t*>(dst + (j * n_rows + p) * 32 + ch * 8) = v;
   }
 }
 
@@ -302,6 +329,18 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert, 
   else
     hipLaunchKernelGGL(zero_invalid_rows_kernel<bf16_t>, dim3(n_assign), dim3(kThreads), 0, stream,
                        ids, n_assign, n_expert, static_cast<bf16_t*>(y), width);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols, void* dst,
+                                 hipStream_t stream) {
+  if (n_rows <= 0 || n_cols <= 0) return hipSuccess;
+  if (n_cols % 32 || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
+    return hipErrorInvalidValue;
+  const int64_t total = (static_cast<int64_t>(n_rows) + 15) / 16 * (n_cols / 32) * kWave;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + kThreads - 1) / kThreads, 1 << 16));
+  hipLaunchKernelGGL(gather_rows_kb_kernel, dim3(blocks), dim3(kThreads), 0, stream,
+                     static_cast<const bf16_t*>(src), order, n_rows, n_tokens, n_cols, static_cast<bf16_t*>(dst));
   return hipGetLastError();
 }
 

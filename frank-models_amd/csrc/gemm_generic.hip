@@ -173,6 +173,7 @@ hipError_t dispatch_w(const GroupedGemmArgs& g, dim3 grid, hipStream_t s) {
 hipError_t launch_gemm_generic(const GroupedGemmArgs& g, hipStream_t stream) {
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
   if (!g.order || !g.offsets || g.epi > EPI_SCATTER_WEIGHTED) return hipErrorInvalidValue;
+  if (g.a_kb_rows || g.out_kb_rows) return hipErrorNotSupported;
   // x: row tiles (unbounded count), y: output column tiles.
   const dim3 grid(static_cast<unsigned>(max_row_tiles(g.n_assign, g.n_expert, kBM)),
                   static_cast<unsigned>((g.N + kBN - 1) / kBN));

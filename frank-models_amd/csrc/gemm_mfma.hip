@@ -506,6 +506,7 @@ bool grouping_ok(const GroupedGemmArgs& g, bool identity_ok) {
 }
 
 bool mfma_common_ok(const GroupedGemmArgs& g) {
+  if (g.a_kb_rows || g.out_kb_rows) return false;  // K-blocked operands: 256-tile kernel only
   if (g.act_dtype != DT_BF16) return false;
   if (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) return false;
   if (g.w_format != WF_MFMA16) return false;

@@ -184,8 +184,9 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
       if constexpr (kWeighted && OUT_F32)
         v = __builtin_bit_cast(u32x4_t, __builtin_bit_cast(f32x4_t, v) * t_w[r]);
       const int64_t row = kScatter ? static_cast<int64_t>(t_order[r]) : static_cast<int64_t>(ti.row0 + r);
-      unsigned char* out = static_cast<unsigned char*>(g.out) +
-                           ((OUT_F32 ? split * g.split_stride : 0) + row * g.ldo + col) * kEsz;
+      const int64_t elem = !kScatter && g.out_kb_rows ? kb_offset(row, col, g.out_kb_rows)
+                                                      : (OUT_F32 ? split * g.split_stride : 0) + row * g.ldo + col;
+      unsigned char* out = static_cast<unsigned char*>(g.out) + elem * kEsz;
       *reinterpret_cast<u32x4_t*>(out) = v;
     }
   }
@@ -198,6 +199,7 @@ struct WaveCtx {
   uint32_t a_off[4];           // byte offsets of the staged token rows: this wave's share (0, 1), wave ^ 4's (2, 3)
   const unsigned char* b_base[4];  // staged weight row blocks, same order
   uint32_t b_lane;
+  uint32_t a_kstride;          // bytes between the 32-input blocks of an A row (64, or 64 * rows K-blocked)
   int a_lane;                  // LDS byte offset of this lane's A fragment in a 16-row group
   int wave, wm, wn;
   int KT;                      // stages of 32 inputs in this block's K range
@@ -225,7 +227,8 @@ __device__ __forceinline__ void issue_full_stage(const WaveCtx& c, int kt, int b
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int share = j < 2 ? c.wave : (c.wave ^ 4);
-    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + kt * 64), st + (share * 2 + (j & 1)) * 1024, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + static_cast<uint32_t>(kt) * c.a_kstride),
+                                     st + (share * 2 + (j & 1)) * 1024, 16, 0, 0);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -348,7 +351,7 @@ __device__ __forceinline__ void issue_one_f8(const WaveCtx& c, int kt, int buf, 
   unsigned char* st = c.lds + buf * kStageF8;
   if (d < 4) {
     const int h = d >> 1, j = d & 1;
-    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + (2 * kt + h) * 64),
+    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + static_cast<uint32_t>(2 * kt + h) * c.a_kstride),
                                      st + h * kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
   } else {
     const int j = d - 4;
@@ -523,17 +526,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   // share (j = 0, 1) and of share wave ^ 4 (j = 2, 3): the bf16 loop has one
   // group load a whole stage, the fp8 loop has every wave load its own share.
   // Rows past the tile re-read its first row.  Byte offsets from the A base
-  // fit 32 bits (checked on the host).
+  // fit 32 bits (checked on the host).  A K-blocked A operand keeps each
+  // 32-input block of the tile's rows in one contiguous run.
   WaveCtx c;
   c.lds = lds;
   c.a_base = static_cast<const unsigned char*>(g.a);
+  const bool a_kb = g.a_kb_rows > 0;
+  c.a_kstride = a_kb ? static_cast<uint32_t>(g.a_kb_rows * 64) : 64u;
+  const int64_t kb_first = static_cast<int64_t>(k_first) * (kStageInputs / 32);  // first 32-input block
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int share = j < 2 ? wave : (wave ^ 4);
     const int r = (share * 2 + (j & 1)) * 16 + (lane >> 2);
     const int p = ti.row0 + (r < ti.rows ? r : 0);
     const int ch = (lane & 3) ^ ((lane >> 3) & 3);
-    c.a_off[j] = static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + k_first * kStageInputs * 2);
+    c.a_off[j] = a_kb ? static_cast<uint32_t>((kb_first * g.a_kb_rows + p) * 64 + ch * 16)
+                      : static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + kb_first * 64);
   }
   // Weight blocks (wave-uniform addresses).  The packed buffer has a
   // 256-row tail, so row blocks past N stay in bounds (their columns are
@@ -660,6 +668,12 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
   // 32-bit byte offsets of A rows
   const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;
   if (a_rows * g.lda * 2 >= (int64_t(1) << 32)) return false;
+  // K-blocked A: expert-sorted rows (A_DIRECT), all of them inside the blocks
+  if (g.a_kb_rows && (g.a_mode != A_DIRECT || g.a_kb_rows < g.n_assign || g.K % 32 ||
+                      g.K * g.a_kb_rows * 2 >= (int64_t(1) << 32)))
+    return false;
+  // K-blocked SwiGLU output: whole 32-column blocks, rows p < out_kb_rows
+  if (g.out_kb_rows && (g.epi != EPI_SWIGLU || g.out_kb_rows < g.n_assign || g.N % 32)) return false;
   if (g.epi == EPI_SWIGLU && (g.out_dtype != DT_BF16 || !g.w1)) return false;
   if (reinterpret_cast<uintptr_t>(g.a) % 16 || reinterpret_cast<uintptr_t>(g.out) % 16) return false;
   return true;

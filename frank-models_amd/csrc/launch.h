@@ -120,8 +120,21 @@ struct GroupedGemmArgs {
   // block: n_tokens, since top-k picks distinct experts per token); 0 =
   // unknown.  A tuning hint: kernels are correct for any count.
   int max_rows_per_expert = 0;
+  // K-blocked operands (256-tile kernel only): with a_kb_rows > 0 the A
+  // operand (A_DIRECT) is stored as 64-byte row pieces, piece j of row r at
+  // byte ((j * a_kb_rows) + r) * 64 (j = input block of 32 bf16), so one
+  // 32-input stage of a row tile is one contiguous run and every fetched
+  // cache line is used whole.  With out_kb_rows > 0 the SwiGLU epilogue
+  // writes its output in that layout (out_kb_rows rows per piece column).
+  int64_t a_kb_rows = 0;
+  int64_t out_kb_rows = 0;
   ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
 };
+
+// Element offset of (row, col) in a K-blocked bf16 matrix of `rows` rows.
+__host__ __device__ inline int64_t kb_offset(int64_t row, int64_t col, int64_t rows) {
+  return ((col >> 5) * rows + row) * 32 + (col & 31);
+}
 
 // Upper bound on the number of bm-row tiles of a grouping of n_assign rows
 // over n_expert experts.
@@ -194,6 +207,11 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert,
                                     void* y, int dtype, int64_t width,
                                     hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+// dst (K-blocked, kb_offset with n_rows rows) row p = src row order[p] % n_tokens
+// (src [n_tokens, n_cols] row-major bf16, n_cols % 32 == 0): the gate/up
+// GEMM's A operand gathered into expert-sorted order.
+hipError_t launch_gather_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols, void* dst,
+                                 hipStream_t stream);
 
 // Device address of the allocation-free entry point's scratch array
 // (FMOE_NOALLOC_SCRATCH_BYTES, noalloc.hip) on `device`, which must be the
