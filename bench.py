@@ -3,8 +3,7 @@
 Workload ("C2"): Mixtral-8x7B-shaped moe_ffn_block,
 bf16 activations and weights, fp32 accumulation, hidden 4096, ffn 14336,
 8 experts, top-2, no renormalisation.  A step is one moe_ffn_block call on
-4096 tokens already resident in HBM (prefill); the 16-token decode call is
-measured the same way and reported under "decode".  Inputs are synthetic and
+4096 tokens already resident in HBM (prefill).  Inputs are synthetic and
 seeded (frank-models_amd/workloads.py): activations N(0,1), weights
 N(0,0.02^2), router rows redrawn until the top-3 probabilities are >= 1e-3
 apart.
@@ -12,17 +11,27 @@ apart.
 The JSON line carries:
   value / ms_per_step   whole-block throughput (tokens/s) over --steps calls,
                         bracketed by torch.cuda.synchronize()
-  roofline              the dominant kernel (grouped gate+up GEMM), its
+  roofline              the dominant kernel alone (grouped gate+up GEMM): its
                         average duration from HIP events recorded by the
                         library on the launch stream, algorithmic FLOPs per
-                        launch (useful work only) against the dense bf16 MFMA
-                        peak (2.5 PFLOP/s); traffic from rocprofv3 PMC
-                        counters when a summary is committed, else null
-  block_mfma_frac       block FLOPs (2*T*H*E + 6*T*k*H*F) / step time / peak
-  decode                T=16: tokens/s and block HBM fraction (bytes of the
-                        touched experts' weights + activations / time / 8 TB/s)
+                        launch against the dense bf16 MFMA peak (2.5 PFLOP/s);
+                        traffic from the committed rocprofv3 PMC summary named
+                        in traffic_source (not measured in this run)
+  block_mfma_frac       the whole block: FLOPs (2*T*H*E + 6*T*k*H*F) / step time / peak
+  mfma_counters         counter FLOPs (SQ_INSTS_VALU_MFMA_MOPS_* x 512) beside the
+                        algorithmic FLOPs of the prefill GEMMs, from the committed
+                        profile named in its source field
+  configs               every BASELINE configuration and token count (C2 T=16/512,
+                        C3, C4, C5, and C5 T=4096 with e4m3 activations): per-call
+                        device time from HIP events, median / p10 / p90 over
+                        --config-steps calls after --config-warmup, the MALL and
+                        L2 flushed before each call when the touched weights
+                        would fit in the 256 MB MALL
+  decode                C2 T=16 (the same as its configs row, kept as a field)
   cpu_baseline          the oracle's expert-grouped NumPy restatement (oracle/)
-                        timed on this host on a bounded token sample
+                        timed on this host's cores on a bounded token sample,
+                        all cores and one thread; the literal gather form where
+                        it fits; the CPU model; IREE llvm-cpu (not installed)
   attention_decode      the decode step's attention half at Mixtral's attention
                         shape (16 sequences x 4096 cached positions, paged
                         bf16 KV): ms/step, per-phase times, KV-read GB/s;
@@ -60,7 +69,7 @@ def block_bytes(T, H, F, E, k, touched, wbytes=2, abytes=2):
     return touched * 3.0 * H * F * wbytes + E * H * abytes + 2.0 * T * H * abytes + 2.0 * T * k * 4
 
 
-def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=False):
+def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=False, fp8_activations=False):
     """Times `steps` block calls at T tokens (and, with `sublayer`, the
     norm + block + residual sub-layer); returns a dict of measurements."""
     x_np, wr_np, gen = wl.router_inputs(cfg, T)
@@ -81,7 +90,7 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=Fals
         weights = (dev_w, packed, pack_s)
     dev_w, packed, pack_s = weights
     block = fm.MoEFFNBlock(wr, *packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
-                           cfg.normalize, act_dtype=torch.bfloat16)
+                           cfg.normalize, act_dtype=torch.bfloat16, fp8_activations=fp8_activations)
     out = torch.empty((T, cfg.n_embd), dtype=torch.bfloat16, device="cuda")
     for _ in range(warmup):
         block(x, out=out)
@@ -104,7 +113,8 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=Fals
     touched = int(torch.unique(ids).numel())
     res = dict(T=T, elapsed=elapsed, ms=elapsed / steps * 1e3, tok_s=steps * T / elapsed,
                kernels={k: (v[0] / v[1] if v[1] else 0.0) for k, v in kernels.items() if v[1]},
-               touched=touched, pack_s=pack_s, gen=gen, x_np=x_np, wr_np=wr_np, weights=weights)
+               touched=touched, pack_s=pack_s, gen=gen, x_np=x_np, wr_np=wr_np, weights=weights,
+               block=block, x=x, out=out)
     if sublayer:
         # The MoE FFN sub-layer on the same batch as residual stream: ffn_norm,
         # block, residual add (unit norm weight; routing is not checked here).
@@ -129,66 +139,184 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=Fals
     return res
 
 
-def cpu_baseline(torch, cfg, res, sample):
-    """Expert-grouped NumPy restatement (oracle/) on `sample` tokens of the
-    same batch, fp32, on this host's cores."""
-    import numpy as np
-    from oracle import moe as om
+def percentile(sorted_vals, q):
+    """Linear-interpolated percentile of an ascending list."""
+    if not sorted_vals:
+        return 0.0
+    pos = (len(sorted_vals) - 1) * q
+    lo = int(pos)
+    hi = min(lo + 1, len(sorted_vals) - 1)
+    return sorted_vals[lo] + (sorted_vals[hi] - sorted_vals[lo]) * (pos - lo)
 
-    dev_w = res["weights"][0]
-    host_w = [w.float().cpu().numpy() for w in dev_w]
-    xs = res["x_np"][:sample]
+
+def timed_calls(torch, fn, warmup, iters, flush=None):
+    """Per-call device time of fn() in ms: HIP events on torch's current
+    stream (the stream the library launches on) around each call, after
+    `warmup` untimed calls; `flush` (untimed) runs before every call."""
+    for _ in range(warmup):
+        if flush:
+            flush()
+        fn()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        if flush:
+            flush()
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+    return {"median_ms": percentile(ms, 0.5), "p10_ms": percentile(ms, 0.1), "p90_ms": percentile(ms, 0.9),
+            "mean_ms": sum(ms) / len(ms), "calls": iters, "warmup": warmup}
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:  # pragma: no cover - reporting only
+        pass
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        blas = [{"api": i.get("internal_api"), "threads": i.get("num_threads")} for i in threadpool_info()
+                if i.get("user_api") == "blas"]
     except Exception:  # pragma: no cover - reporting only
-        threads = len(os.sched_getaffinity(0))
+        blas = []
+    try:
+        import iree.compiler  # noqa: F401
+
+        iree = "importable (not timed: the reference's IREE module needs its compile/link harness)"
+    except Exception:
+        iree = "unavailable: iree.compiler is not installed on this host (no network to fetch it)"
+    return {"cpu_model": model, "affinity_cores": len(os.sched_getaffinity(0)), "blas": blas,
+            "iree_llvm_cpu": iree}
+
+
+def _time_oracle(fn, runs):
     times = []
-    for _ in range(3):
+    for _ in range(runs):
         t0 = time.perf_counter()
-        om.moe_ffn_block(xs, res["wr_np"], *host_w, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
-                         cfg.normalize, dtype=np.float32)
+        fn()
         times.append(time.perf_counter() - t0)
-    best = min(times)
-    return {
+    return min(times)
+
+
+def cpu_baseline(torch, wl, cfg, res, sample, sample_1t):
+    """The oracle's expert-grouped NumPy restatement (oracle/moe.py), fp32
+    OpenBLAS, on a bounded sample of the same batch: all cores (the value)
+    and one thread; plus the literal gather form (oracle/moe.py
+    mul_mat_id_literal, the reference's own decomposition) where its gathered
+    weight copies fit: the C1 toy block and C4 at one token."""
+    import numpy as np
+    from oracle import moe as om
+
+    info = cpu_info()
+    dev_w = res["weights"][0]
+    host_w = [w.float().cpu().numpy() for w in dev_w]
+    args = (res["wr_np"], *host_w, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff, cfg.normalize)
+    xs = res["x_np"][:sample]
+    best = _time_oracle(lambda: om.moe_ffn_block(xs, *args, dtype=np.float32), 3)
+    out = {
         "value": sample / best,
         "unit": "tokens/s",
-        "cores": int(threads),
+        "cores": info["affinity_cores"],
         "kind": "port",
-        "sample": (f"{sample} of the {res['T']} tokens, fp32 expert-grouped NumPy/OpenBLAS restatement of "
-                   f"oracles/moe.py (oracle/moe.py), best of {len(times)} runs ({best:.2f}s each)"),
+        "sample": (f"{sample} of the {res['T']} tokens of the C2 batch, fp32 expert-grouped NumPy/OpenBLAS "
+                   f"restatement of oracles/moe.py (oracle/moe.py), best of 3 runs ({best:.2f}s each), "
+                   f"all {info['affinity_cores']} cores"),
+        **info,
     }
+    try:
+        from threadpoolctl import threadpool_limits
+
+        x1 = res["x_np"][:sample_1t]
+        with threadpool_limits(limits=1):
+            b1 = _time_oracle(lambda: om.moe_ffn_block(x1, *args, dtype=np.float32), 2)
+        out["single_thread"] = {"value": sample_1t / b1, "unit": "tokens/s", "cores": 1,
+                                "sample": f"{sample_1t} tokens, best of 2 runs ({b1:.2f}s each)"}
+    except Exception as e:  # pragma: no cover - reporting only
+        out["single_thread"] = f"not timed: {e}"
+    # The literal form (per-assignment weight gather + batched mat-vec).
+    literal = []
+    for name, T in (("C1", 32), ("C4", 1)):
+        c = wl.CONFIGS[name]
+        x, wr, _ = wl.router_inputs(c, T)
+        g = np.random.default_rng(0)
+        ws = [(g.standard_normal(sh, dtype=np.float32) * 0.02) for sh in
+              ((c.n_ff, c.n_embd, c.n_expert), (c.n_ff, c.n_embd, c.n_expert), (c.n_embd, c.n_ff, c.n_expert))]
+        t = _time_oracle(lambda: om.moe_ffn_block_literal(x, wr, *ws, c.n_expert, c.n_expert_used, c.n_embd,
+                                                          c.n_ff, c.normalize), 3)
+        literal.append({"config": name, "tokens": T, "tokens_per_s": T / t, "seconds": t})
+    out["literal_form"] = literal
+    return out
 
 
-def all_configs(fm, wl, torch, args):
-    """Every BASELINE configuration and token count: ms/step, tokens/s, block
-    MFMA fraction (bf16/fp8 peak) and HBM fraction of the touched weights."""
+# Rows of the per-configuration table: (config, tokens, fp8 activations).
+CONFIG_ROWS = [("C2", 16, False), ("C2", 512, False), ("C3", 64, False), ("C3", 2048, False), ("C3", 8192, False),
+               ("C4", 1, False), ("C4", 4, False), ("C4", 16, False), ("C4", 64, False), ("C5", 16, False),
+               ("C5", 4096, False), ("C5", 4096, True)]
+MALL_BYTES = 256e6
+
+
+def config_table(fm, wl, torch, steps, warmup, headline=None):
+    """Every BASELINE configuration and token count (CONFIG_ROWS): per-call
+    device time (median / p10 / p90), tokens/s, MFMA fraction (against the
+    bf16 peak, or the fp8 peak for e4m3 activations), HBM fraction of the
+    touched experts' weights, per-kernel HIP-event times.  Rows whose touched
+    weights would fit in the MALL are timed cold: a 512 MB buffer is written
+    before every call."""
+    flush_buf = torch.empty(int(2 * MALL_BYTES), dtype=torch.uint8, device="cuda")
     rows = []
-    for name in ("C2", "C3", "C4", "C5"):
+    cache = {}
+    if headline is not None:
+        cache["C2"] = headline["weights"]
+    for name, T, a8 in CONFIG_ROWS:
+        if name not in cache:
+            cache.clear()
+            torch.cuda.empty_cache()
         cfg = wl.CONFIGS[name]
         H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
-        weights = None
-        for T in cfg.tokens:
-            res = run_config(fm, wl, torch, cfg, T, max(5, args.steps // 2), 5, weights=weights, sublayer=True)
-            weights = res["weights"]
-            wb = 1 if cfg.weights == "fp8" else 2
-            flops = block_flops(T, H, F, E, k)
-            nbytes = block_bytes(T, H, F, E, k, res["touched"], wbytes=wb)
-            row = {"config": name, "tokens": T, "ms": res["ms"], "tokens_per_s": res["tok_s"],
-                   "mfma_frac": flops / (res["ms"] * 1e-3) / PEAK_BF16_FLOPS,
-                   "hbm_frac": nbytes / (res["ms"] * 1e-3) / PEAK_HBM_BYTES,
-                   "experts_touched": res["touched"], "kernels_ms": res["kernels"],
-                   "sublayer_ms": res["sublayer_ms"], "sublayer_kernels_ms": res["sublayer_kernels"]}
-            rows.append(row)
-            log(f"{name} T={T:5d}: {res['ms']:.3f} ms  {res['tok_s']:.0f} tok/s  mfma {row['mfma_frac']:.3f}  "
-                f"hbm {row['hbm_frac']:.3f}  {res['kernels']}")
-            log(f"{name} T={T:5d}: sub-layer {res['sublayer_ms']:.3f} ms  "
-                f"norm {res['sublayer_kernels'].get('norm', 0.0):.4f} ms  "
-                f"combine {res['sublayer_kernels'].get('combine', 0.0):.4f} ms")
-        del weights
-        torch.cuda.empty_cache()
+        res = run_config(fm, wl, torch, cfg, T, 3, 2, weights=cache.get(name), fp8_activations=a8)
+        cache[name] = res["weights"]
+        wb = 1 if cfg.weights == "fp8" else 2
+        wbytes = res["touched"] * 3.0 * H * F * wb
+        cold = wbytes < 2 * MALL_BYTES
+        block, x, out = res["block"], res["x"], res["out"]
+        st = timed_calls(torch, lambda: block(x, out=out), warmup, steps,
+                         flush=(lambda: flush_buf.zero_()) if cold else None)
+        ms = st["median_ms"]
+        flops = block_flops(T, H, F, E, k)
+        nbytes = block_bytes(T, H, F, E, k, res["touched"], wbytes=wb)
+        peak = 2 * PEAK_BF16_FLOPS if a8 else PEAK_BF16_FLOPS
+        row = {"config": name, "tokens": T, "weights": cfg.weights, "activations": "e4m3" if a8 else "bf16",
+               **{key: round(v, 4) for key, v in st.items() if key.endswith("_ms")},
+               "calls": st["calls"], "warmup": st["warmup"], "tokens_per_s": T / (ms * 1e-3),
+               "mfma_frac": flops / (ms * 1e-3) / peak, "mfma_peak_tflops": peak / 1e12,
+               "hbm_frac": nbytes / (ms * 1e-3) / PEAK_HBM_BYTES, "experts_touched": res["touched"],
+               "mall_flushed": cold, "kernels_us": {kk: round(v * 1e3, 1) for kk, v in res["kernels"].items()}}
+        rows.append(row)
+        log(f"{name} T={T:5d} act={row['activations']}: median {ms:.4f} ms (p10 {st['p10_ms']:.4f}, "
+            f"p90 {st['p90_ms']:.4f}){' cold' if cold else ''}  mfma {row['mfma_frac']:.3f}  "
+            f"hbm {row['hbm_frac']:.3f}  {row['kernels_us']}")
+        del res, block, x, out
+    del flush_buf, cache
+    torch.cuda.empty_cache()
     return rows
+
+
+def read_profile_json(name):
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text())
+    except Exception:
+        return None
 
 
 def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16, cpu_sample=0, moe=None):
@@ -313,35 +441,24 @@ def attention_cpu_baseline(torch, blk, x, pos, kp, vp, tables, lens, ctx, bi, pi
                       f"({dt:.2f}s each), random weights of the same shapes"}
 
 
-def read_traffic(kernel_name):
-    """HBM bytes per launch of `kernel_name` from a committed rocprofv3 PMC
-    summary (profiles/pmc_<name>.json), or None."""
-    p = ROOT / "profiles" / f"pmc_{kernel_name}.json"
-    if not p.exists():
-        return None
-    try:
-        return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
-    except Exception:
-        return None
-
-
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=4096)
-    ap.add_argument("--decode-tokens", type=int, default=16)
+    ap.add_argument("--config-steps", type=int, default=50, help="timed calls per configs row")
+    ap.add_argument("--config-warmup", type=int, default=10, help="untimed calls before each configs row")
     ap.add_argument("--cpu-sample", type=int, default=4096)
+    ap.add_argument("--cpu-sample-1t", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration table")
+    ap.add_argument("--no-decode", action="store_true", help="(with --no-configs) skip the C2 T=16 field")
     ap.add_argument("--attn-batch", type=int, default=16)
     ap.add_argument("--attn-context", type=int, default=4096)
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--attention-only", action="store_true",
                     help="time only the decode attention half (its own JSON line)")
-    ap.add_argument("--all-configs", action="store_true",
-                    help="also time C3/C4/C5 at every token count (table on stderr, 'configs' in the JSON)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -374,9 +491,14 @@ def main():
     gu_ms = pre["kernels"].get("gate_up", 0.0)
     gu_flops = 2.0 * n_assign * H * (2 * F)
     achieved = gu_flops / (gu_ms * 1e-3) / 1e12 if gu_ms else 0.0
+    pmc = read_profile_json("pmc_gate_up_prefill.json")
     roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
-                "frac": achieved * 1e12 / PEAK_BF16_FLOPS, "traffic": read_traffic("gate_up_prefill"),
-                "kernel": "gemm_tiled256_kernel<SWIGLU> (gate+up grouped GEMM, SwiGLU epilogue)",
+                "frac": achieved * 1e12 / PEAK_BF16_FLOPS,
+                "traffic": float(pmc["hbm_bytes_per_launch"]) if pmc else None,
+                "scope": "the gate+up grouped GEMM kernel alone (gemm_tiled256_kernel, SwiGLU epilogue); "
+                         "the whole block's fraction is block_mfma_frac",
+                "traffic_source": ("committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary profiles/pmc_gate_up_prefill"
+                                   ".json (not measured in this run)") if pmc else None,
                 "kernel_ms": gu_ms, "flops_per_launch": gu_flops}
     flops = block_flops(T, H, F, E, k)
     result = {
@@ -401,20 +523,24 @@ def main():
         "kernels_ms": pre["kernels"],
         "pack_s": pre["pack_s"],
     }
+    mc = read_profile_json("pmc_mfma_prefill.json")
+    if mc:
+        result["mfma_counters"] = mc
 
-    if not args.no_decode:
-        Td = args.decode_tokens
-        log(f"decode T={Td}")
-        dec = run_config(fm, wl, torch, cfg, Td, max(args.steps, 20), args.warmup, weights=pre["weights"])
-        nbytes = block_bytes(Td, H, F, E, k, dec["touched"])
-        result["decode"] = {
-            "tokens": Td, "tokens_per_s": dec["tok_s"], "ms_per_step": dec["ms"],
-            "experts_touched": dec["touched"], "algorithmic_bytes": nbytes,
-            "hbm_frac": nbytes / (dec["ms"] * 1e-3) / PEAK_HBM_BYTES,
-            "achieved_GBps": nbytes / (dec["ms"] * 1e-3) / 1e9,
-            "kernels_ms": dec["kernels"],
-        }
-        log(f"decode {dec['ms']:.3f} ms/step, {result['decode']['hbm_frac']:.3f} of HBM peak")
+    if not args.no_configs:
+        log(f"configs: {args.config_warmup} warmup + {args.config_steps} timed calls per row")
+        rows = config_table(fm, wl, torch, args.config_steps, args.config_warmup, headline=pre)
+        result["configs"] = rows
+        dec = next(r for r in rows if r["config"] == "C2" and r["tokens"] == 16)
+        result["decode"] = {"tokens": 16, "tokens_per_s": dec["tokens_per_s"], "ms_per_step": dec["median_ms"],
+                            "experts_touched": dec["experts_touched"], "hbm_frac": dec["hbm_frac"],
+                            "achieved_GBps": dec["hbm_frac"] * PEAK_HBM_BYTES / 1e9, "kernels_us": dec["kernels_us"]}
+    elif not args.no_decode:
+        dec = run_config(fm, wl, torch, cfg, 16, max(args.steps, 20), args.warmup, weights=pre["weights"])
+        nbytes = block_bytes(16, H, F, E, k, dec["touched"])
+        result["decode"] = {"tokens": 16, "tokens_per_s": dec["tok_s"], "ms_per_step": dec["ms"],
+                            "experts_touched": dec["touched"], "hbm_frac": nbytes / (dec["ms"] * 1e-3) / PEAK_HBM_BYTES,
+                            "kernels_ms": dec["kernels"]}
 
     if not args.no_attention:
         log(f"attention decode: batch {args.attn_batch}, context {args.attn_context}")
@@ -426,12 +552,10 @@ def main():
         log(f"attention decode {result['attention_decode']['ms_per_step']:.3f} ms/step, "
             f"kernels(ms) {result['attention_decode']['kernels_ms']}")
 
-    if args.all_configs:
-        result["configs"] = all_configs(fm, wl, torch, args)
-
     if not args.no_cpu_baseline:
-        log(f"cpu baseline on {args.cpu_sample} tokens")
-        result["cpu_baseline"] = cpu_baseline(torch, cfg, pre, min(args.cpu_sample, T))
+        log(f"cpu baseline on {args.cpu_sample} tokens (all cores), {args.cpu_sample_1t} (one thread)")
+        result["cpu_baseline"] = cpu_baseline(torch, wl, cfg, pre, min(args.cpu_sample, T),
+                                              min(args.cpu_sample_1t, T))
         log(f"cpu baseline {result['cpu_baseline']['value']:.1f} tok/s")
     else:
         result["cpu_baseline"] = None

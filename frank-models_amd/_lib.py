@@ -32,6 +32,7 @@ ERR_WORKSPACE = 7
 F32 = 0
 BF16 = 1
 F8E4M3FN = 2
+F8E4M3FN_A8 = 3  # block / sub-layer: e4m3 weights, prefill GEMMs on e4m3 activations
 
 # fmoe_gemm_path
 PATH_AUTO = 0
@@ -45,7 +46,8 @@ PATH_TILED_LARGE = 4
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # fmoe_timer
-TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id", "norm", "qkv", "attention", "out_proj")
+TIMERS = ("router", "permute", "gate_up", "down", "combine", "mul_mat_id", "norm", "qkv", "attention", "out_proj",
+          "quant")
 
 
 class FmoeError(RuntimeError):

@@ -53,6 +53,11 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 bool act_dtype_ok(int dt) { return dt == FMOE_F32 || dt == FMOE_BF16; }
 bool w_dtype_ok(int dt) { return dt == FMOE_F32 || dt == FMOE_BF16 || dt == FMOE_F8E4M3FN; }
+// The block and sub-layer also take FMOE_F8E4M3FN_A8: e4m3fn weights whose
+// prefill GEMMs run on fp8 activations.
+bool block_w_dtype_ok(int dt) { return w_dtype_ok(dt) || dt == FMOE_F8E4M3FN_A8; }
+// Storage type of the packed weights for a block weight dtype.
+int packed_dtype(int dt) { return dt == FMOE_F8E4M3FN_A8 ? FMOE_F8E4M3FN : dt; }
 
 bool aligned_for(const void* p, int dt) {
   return reinterpret_cast<uintptr_t>(p) % dtype_bytes(dt) == 0;
@@ -243,6 +248,9 @@ struct BlockLayout {
   PermuteLayout perm;
   size_t h, y, total;
   size_t xkb, xkb_bytes;  // token rows gathered K-blocked in expert order (0 bytes when no prefill GEMM can use them)
+  // fp8 activations (FMOE_F8E4M3FN_A8, prefill-sized batches): e4m3 token
+  // rows and SwiGLU rows, K-blocked, with their per-row scales (0 bytes otherwise)
+  size_t xq, xs, hq, hs, a8_bytes;
   size_t rpart;          // decode router's split logits (0 bytes when the shape takes the general router)
   size_t rpart_bytes;
   int h_dtype, y_dtype;
@@ -271,7 +279,8 @@ GroupedGemmArgs down_shape(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F
   return d;
 }
 
-BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act, int wdt) {
+BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, int act, int block_wdt) {
+  const int wdt = packed_dtype(block_wdt);
   BlockLayout L;
   const int64_t n = k * T;
   size_t off = 0;
@@ -295,10 +304,27 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   off += align_up(static_cast<size_t>(n) * H * dtype_bytes(L.y_dtype) * L.y_parts);
   // Prefill-sized bf16 batches: room for the token rows gathered into expert
   // order, K-blocked, so the gate/up GEMM reads whole cache lines.
-  const bool kb_candidate = act == FMOE_BF16 && n > 8 * E && H % 64 == 0 && F % 64 == 0;
+  const bool prefill = act == FMOE_BF16 && n > 8 * E;
+  const bool a8 = prefill && block_wdt == FMOE_F8E4M3FN_A8 && H % 128 == 0 && F % 128 == 0 && H <= 16384 &&
+                  F <= 16384;
+  const bool kb_candidate = prefill && !a8 && H % 64 == 0 && F % 64 == 0;
   L.xkb = off;
   L.xkb_bytes = kb_candidate ? static_cast<size_t>(n) * H * 2 : 0;
   off += align_up(L.xkb_bytes);
+  L.a8_bytes = 0;
+  L.xq = off;
+  if (a8) {
+    off += align_up(static_cast<size_t>(n) * H);
+    L.xs = off;
+    off += align_up(static_cast<size_t>(n) * 4);
+    L.hq = off;
+    off += align_up(static_cast<size_t>(n) * F);
+    L.hs = off;
+    off += align_up(static_cast<size_t>(n) * 4);
+    L.a8_bytes = off - L.xq;
+  } else {
+    L.xs = L.hq = L.hs = off;
+  }
   L.total = off;
   return L;
 }
@@ -377,7 +403,7 @@ int check_workspace(const void* ws, size_t bytes, size_t need) {
 // checks none of these; moe_ffn_block.mlir:34-45 only declares the types).
 int validate_block(const BlockCall& c) {
   if (!act_dtype_ok(c.act_dtype)) return fail(FMOE_ERR_DTYPE, "activation dtype %d", c.act_dtype);
-  if (!w_dtype_ok(c.w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", c.w_dtype);
+  if (!block_w_dtype_ok(c.w_dtype)) return fail(FMOE_ERR_DTYPE, "weight dtype %d", c.w_dtype);
   if (c.act_dtype == FMOE_F32 && c.w_dtype != FMOE_F32)
     return fail(FMOE_ERR_DTYPE, "f32 activations need f32 weights");
   FMOE_TRY(validate_router(c.n_tokens, c.n_embd, c.n_expert, c.n_expert_used));
@@ -387,7 +413,7 @@ int validate_block(const BlockCall& c) {
   if (c.n_tokens == 0) return FMOE_OK;
   if (!c.input || !c.w_router || !c.packed_up || !c.packed_gate || !c.packed_down || !c.out)
     return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
-  if (c.w_dtype == FMOE_F8E4M3FN && (!c.up_scales || !c.gate_scales || !c.down_scales))
+  if (packed_dtype(c.w_dtype) == FMOE_F8E4M3FN && (!c.up_scales || !c.gate_scales || !c.down_scales))
     return fail(FMOE_ERR_INVALID_ARGUMENT, "fp8 weights need scales");
   if (!aligned_for(c.input, c.act_dtype) || !aligned_for(c.out, c.act_dtype) ||
       !aligned_for(c.w_router, c.act_dtype))
@@ -401,7 +427,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   void* workspace = c.workspace;
   const int64_t n_embd = c.n_embd, n_ff = c.n_ff, n_expert = c.n_expert, n_expert_used = c.n_expert_used;
-  const int act_dtype = c.act_dtype, w_dtype = c.w_dtype;
+  const int act_dtype = c.act_dtype, w_dtype = packed_dtype(c.w_dtype);
   const int T = static_cast<int>(c.n_tokens);
   const int n = static_cast<int>(c.n_tokens * n_expert_used);
   int* ids = at<int>(workspace, L.ids);
@@ -472,32 +498,59 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   d.max_rows_per_expert = T;
 
   // When both GEMMs take the 256-tile kernel, their A operands go K-blocked
-  // (64-byte row pieces, one contiguous run per 32-input stage of a tile):
-  // the token rows are gathered into expert order first, and the gate/up
-  // epilogue writes h in that layout for the down GEMM.
-  if (L.xkb_bytes) {
+  // (64-byte row pieces, one contiguous run per stage of a tile): the token
+  // rows are gathered into expert order first, and the gate/up epilogue
+  // writes h in that layout for the down GEMM.  With fp8 activations
+  // (FMOE_F8E4M3FN_A8) the gathered rows and h are quantised to e4m3 per row
+  // instead, and both GEMMs run on the fp8 MFMA.
+  bool h_quant = false;
+  GroupedGemmArgs dq = d;
+  if (L.xkb_bytes || L.a8_bytes) {
     int vg = 0, vd = 0;
     const int pg = pick_path(g, &vg), pd = pick_path(d, &vd);
-    GroupedGemmArgs gk = g, dk = d;
-    void* xkb = at<char>(workspace, L.xkb);
-    gk.a = xkb;
-    gk.a_mode = A_DIRECT;
-    gk.a_kb_rows = n;
-    gk.out_kb_rows = n;
-    dk.a_kb_rows = n;
     const bool tiled_g = pg == FMOE_PATH_TILED || pg == FMOE_PATH_TILED_LARGE;
     const bool tiled_d = pd == FMOE_PATH_TILED || pd == FMOE_PATH_TILED_LARGE;
-    if (tiled_g && tiled_d && vg == TILED_256 && vd == TILED_256 && gemm_tiled256_supported(gk) &&
-        gemm_tiled256_supported(dk)) {
-      ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
-      FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), xkb, s));
-      g = gk;
-      d = dk;
+    const bool both256 = tiled_g && tiled_d && vg == TILED_256 && vd == TILED_256;
+    GroupedGemmArgs gk = g, dk = d;
+    gk.a_mode = A_DIRECT;
+    gk.a_kb_rows = n;
+    dk.a_kb_rows = n;
+    if (L.a8_bytes) {
+      gk.a = at<char>(workspace, L.xq);
+      gk.act_dtype = DT_F8;
+      gk.a_scale = at<float>(workspace, L.xs);
+      dk.a = at<char>(workspace, L.hq);
+      dk.act_dtype = DT_F8;
+      dk.a_scale = at<float>(workspace, L.hs);
+      if (both256 && gemm_tiled256_supported(gk) && gemm_tiled256_supported(dk)) {
+        ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
+        FMOE_HIP(launch_quantize_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<char>(workspace, L.xq),
+                                         at<float>(workspace, L.xs), s));
+        g = gk;
+        dq = dk;
+        h_quant = true;
+      }
+    } else {
+      gk.a = at<char>(workspace, L.xkb);
+      gk.out_kb_rows = n;
+      if (both256 && gemm_tiled256_supported(gk) && gemm_tiled256_supported(dk)) {
+        ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
+        FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<char>(workspace, L.xkb),
+                                       s));
+        g = gk;
+        d = dk;
+      }
     }
   }
   {
     ScopedTimer t(FMOE_TIMER_GATE_UP, s, c.timers);
     FMOE_TRY(run_grouped_gemm(g, s));
+  }
+  if (h_quant) {
+    ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
+    FMOE_HIP(launch_quantize_rows_kb(h, nullptr, n, n, static_cast<int>(n_ff), at<char>(workspace, L.hq),
+                                     at<float>(workspace, L.hs), s));
+    d = dq;
   }
 
   // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
@@ -1005,7 +1058,7 @@ int fmoe_mul_mat_id(const void* packed_w, const float* w_scales, int w_dtype, co
 size_t fmoe_moe_ffn_block_workspace_bytes(int64_t n_tokens, int64_t n_expert,
                                           int64_t n_expert_used, int64_t n_embd, int64_t n_ff,
                                           int act_dtype, int w_dtype) {
-  if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
+  if (!act_dtype_ok(act_dtype) || !block_w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
       n_expert_used < 1 || n_embd < 1 || n_ff < 0)
     return 0;
   return block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype).total;
@@ -1075,7 +1128,7 @@ int fmoe_rms_norm(const void* input, const void* weight, float eps, void* out, i
 
 size_t fmoe_moe_ffn_sublayer_workspace_bytes(int64_t n_tokens, int64_t n_expert, int64_t n_expert_used,
                                              int64_t n_embd, int64_t n_ff, int act_dtype, int w_dtype) {
-  if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
+  if (!act_dtype_ok(act_dtype) || !block_w_dtype_ok(w_dtype) || n_tokens < 0 || n_expert < 1 ||
       n_expert_used < 1 || n_embd < 1 || n_ff < 0)
     return 0;
   return sublayer_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype).total;
@@ -1116,7 +1169,7 @@ int fmoe_moe_ffn_block_routing(void* workspace, int64_t n_tokens, int64_t n_expe
                                int w_dtype, int32_t** ids, float** weights, int32_t** order,
                                int32_t** offsets) {
   if (!workspace) return fail(FMOE_ERR_INVALID_ARGUMENT, "null workspace");
-  if (!act_dtype_ok(act_dtype) || !w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "dtype");
+  if (!act_dtype_ok(act_dtype) || !block_w_dtype_ok(w_dtype)) return fail(FMOE_ERR_DTYPE, "dtype");
   const BlockLayout L = block_layout(n_tokens, n_expert, n_expert_used, n_embd, n_ff, act_dtype, w_dtype);
   if (ids) *ids = at<int32_t>(workspace, L.ids);
   if (weights) *weights = at<float>(workspace, L.weights);

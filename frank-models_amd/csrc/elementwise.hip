@@ -144,6 +144,88 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kb_kernel(const bf16_t* 
   }
 }
 
+// Largest |v| of the 8 bf16 values in a 16-byte chunk (NaN ignored).
+__device__ __forceinline__ float absmax_bf16x8(const u32x4_t v) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m = fmaxf(m, fabsf(__uint_as_float(v[i] << 16)));
+    m = fmaxf(m, fabsf(__uint_as_float(v[i] & 0xFFFF0000u)));
+  }
+  return m;
+}
+
+// 8 bf16 values times inv -> 8 e4m3fn codes in two dwords (element order).
+__device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
+  uint32_t w[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t c0 = f32_to_e4m3fn(__uint_as_float(v[2 * d] << 16) * inv);
+    const uint32_t c1 = f32_to_e4m3fn(__uint_as_float(v[2 * d] & 0xFFFF0000u) * inv);
+    const uint32_t c2 = f32_to_e4m3fn(__uint_as_float(v[2 * d + 1] << 16) * inv);
+    const uint32_t c3 = f32_to_e4m3fn(__uint_as_float(v[2 * d + 1] & 0xFFFF0000u) * inv);
+    w[d] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+  }
+  return u32x2_t{w[0], w[1]};
+}
+
+// One wave per row p (grid-stride): lane c of a pass holds chunk c = 16
+// values, inputs 64j + 8g + [0, 8) and 64j + 32 + 8g + [0, 8) for piece
+// j = c / 4, g = c % 4 (the packed fp8 weights' lane order); the row stays
+// in registers (kPasses passes of 64 chunks) while the wave reduces max|v|,
+// then every value is scaled by 1 / scale (a power of two) and rounded to e4m3.
+template <int kPasses>
+__global__ __launch_bounds__(kThreads) void quantize_rows_kb_kernel(const bf16_t* __restrict__ src,
+                                                                    const int* __restrict__ order, int n_rows,
+                                                                    int n_tokens, int n_cols,
+                                                                    uint8_t* __restrict__ dst_q,
+                                                                    float* __restrict__ dst_scale) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int waves = kThreads / kWave;
+  const int n_chunks = n_cols / 16;
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * waves + threadIdx.x / kWave; p < n_rows;
+       p += static_cast<int64_t>(gridDim.x) * waves) {
+    const int64_t srow = order ? static_cast<int64_t>(static_cast<uint32_t>(order[p]) % static_cast<uint32_t>(n_tokens))
+                               : p;
+    const bf16_t* row = src + srow * n_cols;
+    u32x4_t lo[kPasses], hi[kPasses];
+    float amax = 0.f;
+#pragma unroll
+    for (int it = 0; it < kPasses; ++it) {
+      const int c = it * kWave + lane;
+      if (c < n_chunks) {
+        const int j = c >> 2, q = c & 3;
+        lo[it] = *reinterpret_cast<const u32x4_t*>(row + 64 * j + 8 * q);
+        hi[it] = *reinterpret_cast<const u32x4_t*>(row + 64 * j + 32 + 8 * q);
+        amax = fmaxf(amax, fmaxf(absmax_bf16x8(lo[it]), absmax_bf16x8(hi[it])));
+      }
+    }
+    amax = wave_max(amax);
+    // scale = 2^e, the smallest power of two with max|v| / scale <= 448 (448 =
+    // 1.75 * 2^8): exact to apply, and the rounding of each value does not
+    // depend on the row's maximum (only its binade).
+    float scale = 1.f, inv = 1.f;
+    if (amax > 0.f) {
+      const uint32_t ab = __float_as_uint(amax);
+      int e = static_cast<int>(ab >> 23) - 127 - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+      e = min(max(e, -126), 126);
+      scale = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+      inv = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+    }
+#pragma unroll
+    for (int it = 0; it < kPasses; ++it) {
+      const int c = it * kWave + lane;
+      if (c < n_chunks) {
+        const int j = c >> 2, q = c & 3;
+        const u32x2_t a = e4m3_codes8(lo[it], inv), b = e4m3_codes8(hi[it], inv);
+        *reinterpret_cast<u32x4_t*>(dst_q + (static_cast<int64_t>(j) * n_rows + p) * 64 + q * 16) =
+            u32x4_t{a[0], a[1], b[0], b[1]};
+      }
+    }
+    if (lane == 0) dst_scale[p] = scale;
+  }
+}
+
 // One block per row (grid-stride over rows).  Sum of squares in fp32 (per
 // thread, then across the block), rms = sqrt(sum / H + eps), then
 // out = (x / rms) * weight, the reference's operation order.  out may alias
@@ -329,6 +411,25 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert, 
   else
     hipLaunchKernelGGL(zero_invalid_rows_kernel<bf16_t>, dim3(n_assign), dim3(kThreads), 0, stream,
                        ids, n_assign, n_expert, static_cast<bf16_t*>(y), width);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols,
+                                   void* dst_q, float* dst_scale, hipStream_t stream) {
+  if (n_rows <= 0) return hipSuccess;
+  if (n_cols <= 0 || n_cols % 64 || n_cols > 16384 || reinterpret_cast<uintptr_t>(src) % 16 ||
+      reinterpret_cast<uintptr_t>(dst_q) % 16 || (order && n_tokens <= 0))
+    return hipErrorInvalidValue;
+  constexpr int waves = kThreads / kWave;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((n_rows + waves - 1) / waves, 1 << 16));
+  const auto* x = static_cast<const bf16_t*>(src);
+  auto* q = static_cast<uint8_t*>(dst_q);
+  if (n_cols <= 4096)
+    hipLaunchKernelGGL(quantize_rows_kb_kernel<4>, dim3(blocks), dim3(kThreads), 0, stream, x, order, n_rows,
+                       n_tokens, n_cols, q, dst_scale);
+  else
+    hipLaunchKernelGGL(quantize_rows_kb_kernel<16>, dim3(blocks), dim3(kThreads), 0, stream, x, order, n_rows,
+                       n_tokens, n_cols, q, dst_scale);
   return hipGetLastError();
 }
 

@@ -51,6 +51,25 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x
                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+
+// v_mfma_f32_16x16x128_f8f6f4 on e4m3 x e4m3 (format codes 0, 0; scale
+// operands 0 select the unscaled form).  Each operand is a lane's 32 codes:
+// the 16 bytes it read from each of two consecutive 64-input stages.  Lane
+// l of either operand holds row l % 16; the instruction pairs byte b of
+// operand-0 lane (i + 16 g) with byte b of operand-1 lane (j + 16 g), so any
+// input order works as long as weights and activations share it.
+__device__ __forceinline__ f32x4_t mfma_f8x2(const u32x4_t a0, const u32x4_t a1, const u32x4_t b0,
+                                             const u32x4_t b1, f32x4_t c) {
+  const i32x8_t a = {static_cast<int>(a0[0]), static_cast<int>(a0[1]), static_cast<int>(a0[2]),
+                     static_cast<int>(a0[3]), static_cast<int>(a1[0]), static_cast<int>(a1[1]),
+                     static_cast<int>(a1[2]), static_cast<int>(a1[3])};
+  const i32x8_t b = {static_cast<int>(b0[0]), static_cast<int>(b0[1]), static_cast<int>(b0[2]),
+                     static_cast<int>(b0[3]), static_cast<int>(b1[0]), static_cast<int>(b1[1]),
+                     static_cast<int>(b1[2]), static_cast<int>(b1[3])};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
 // lgkmcnt 11:8; a field at its maximum does not wait).  Issued through the
 // builtin so the compiler's own wait insertion accounts for them.
@@ -107,7 +126,7 @@ __device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, i
 // as they are read back, bf16 outputs before rounding (the same fp32
 // product either way).  fp8 weights: the per-output-channel scale
 // multiplies the fp32 dot product.
-template <int EPI, int NSETS, bool F8, bool OUT_F32>
+template <int EPI, int NSETS, bool F8, bool A8, bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInfo& ti, int split, int64_t n0,
                                          int wm, int wn, int lane, unsigned char* lds, const f32x4_t (&acc)[8][4]) {
   constexpr int kFrags = NSETS == 2 ? 4 : 8;       // output fragments per wave
@@ -135,6 +154,15 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
       if (kWeighted) t_w[t] = w;
     }
   }
+  // fp8 activations: each A row's dequantisation scale (rows past the tile: 1)
+  float as[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (A8) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int r = (wm + 4 * m) * 16 + (lane & 15);
+      if (r < ti.rows) as[m] = g.a_scale[ti.row0 + r];
+    }
+  }
   f32x4_t sc0[kFrags], sc1[kFrags];
 #pragma unroll
   for (int n = 0; n < kFrags; ++n) {
@@ -158,10 +186,10 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
       unsigned char* dst = lds + rl * kPitch + colw * kEsz;
 #pragma unroll
       for (int n = 0; n < kFrags; ++n) {
-        const f32x4_t a0 = acc[n][m] * sc0[n];
+        const f32x4_t a0 = acc[n][m] * sc0[n] * as[m];
         f32x4_t v;
         if constexpr (EPI == EPI_SWIGLU) {
-          const f32x4_t a1 = acc[n + 4][m] * sc1[n];
+          const f32x4_t a1 = acc[n + 4][m] * sc1[n] * as[m];
           v = f32x4_t{silu_mul(a0[0], a1[0]), silu_mul(a0[1], a1[1]), silu_mul(a0[2], a1[2]), silu_mul(a0[3], a1[3])};
         } else {
           v = a0 * w;
@@ -256,7 +284,27 @@ __device__ __forceinline__ void issue_full_stage(const WaveCtx& c, int kt, int b
 // buffers; the buffer G1 refills held stage 2j-1 (last read in slot 2j-2),
 // the one G0 refills in slot 2j+1 held stage 2j (last read in slot 2j).
 // Stages past the end are not loaded; the waits then drain everything.
-template <int NM, int NSETS, int G>
+// The MFMAs of one super-step (two stages) for one wave: bf16 operands run
+// one 16x16x32 MFMA per stage and fragment pair; fp8 activations (A8) run
+// one 16x16x128 MFMA per fragment pair over both 64-input stages.
+template <int NM, bool A8>
+__device__ __forceinline__ void multiply2(f32x4_t (&acc)[8][4], const u32x4_t (&fa)[2][4], const u32x4_t (&fb)[2][8]) {
+  if constexpr (A8) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[n][m] = mfma_f8x2(fb[0][n], fb[1][n], fa[0][m], fa[1][m], acc[n][m]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb[h][n], fa[h][m], acc[n][m]);
+  }
+}
+
+template <int NM, int NSETS, int G, bool A8>
 __device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
   constexpr int R = kRing;
   const int KT = c.KT;  // even
@@ -289,12 +337,7 @@ __device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
     if constexpr (G == 0) {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int n = 0; n < 8; ++n)
-#pragma unroll
-          for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb[h][n], fa[h][m], acc[n][m]);
+      multiply2<NM, A8>(acc, fa, fb);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -327,12 +370,7 @@ __device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
       asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int n = 0; n < 8; ++n)
-#pragma unroll
-          for (int m = 0; m < NM; ++m) acc[n][m] = mfma16(fb[h][n], fa[h][m], acc[n][m]);
+      multiply2<NM, A8>(acc, fa, fb);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_barrier" ::: "memory");
@@ -494,7 +532,9 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
 
-template <int EPI, int NSETS, bool F8>
+// F8: e4m3 weights.  A8 (with F8): e4m3 activations too, K-blocked in
+// 64-input pieces, on the bf16 loop's ring with 64-input stages.
+template <int EPI, int NSETS, bool F8, bool A8>
 __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmArgs g, int n_row_tiles,
                                                                      int n_col_tiles) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
@@ -533,7 +573,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   c.a_base = static_cast<const unsigned char*>(g.a);
   const bool a_kb = g.a_kb_rows > 0;
   c.a_kstride = a_kb ? static_cast<uint32_t>(g.a_kb_rows * 64) : 64u;
-  const int64_t kb_first = static_cast<int64_t>(k_first) * (kStageInputs / 32);  // first 32-input block
+  // first A piece of this block's K range (bf16 pieces hold 32 inputs, fp8 pieces 64)
+  const int64_t kb_first = static_cast<int64_t>(k_first) * (A8 ? 1 : kStageInputs / 32);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int share = j < 2 ? wave : (wave ^ 4);
@@ -573,7 +614,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   // ceil(rows / 16).  Wave-uniform, so each wave runs one specialisation.
   const int groups = (ti.rows + 15) >> 4;
   const int nm = groups > wm ? min(4, (groups - wm + 3) >> 2) : 0;
-  if constexpr (F8) {
+  if constexpr (F8 && !A8) {
     if (wave < 4) {
       switch (nm) {
         case 4: k_loop_f8<4, NSETS, 0>(c, acc); break;
@@ -594,36 +635,36 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   } else {
     if (wave < 4) {  // the two ping-pong groups run mirrored loops
       switch (nm) {
-        case 4: k_loop<4, NSETS, 0>(c, acc); break;
-        case 3: k_loop<3, NSETS, 0>(c, acc); break;
-        case 2: k_loop<2, NSETS, 0>(c, acc); break;
-        case 1: k_loop<1, NSETS, 0>(c, acc); break;
-        default: k_loop<0, NSETS, 0>(c, acc); break;
+        case 4: k_loop<4, NSETS, 0, A8>(c, acc); break;
+        case 3: k_loop<3, NSETS, 0, A8>(c, acc); break;
+        case 2: k_loop<2, NSETS, 0, A8>(c, acc); break;
+        case 1: k_loop<1, NSETS, 0, A8>(c, acc); break;
+        default: k_loop<0, NSETS, 0, A8>(c, acc); break;
       }
     } else {
       switch (nm) {
-        case 4: k_loop<4, NSETS, 1>(c, acc); break;
-        case 3: k_loop<3, NSETS, 1>(c, acc); break;
-        case 2: k_loop<2, NSETS, 1>(c, acc); break;
-        case 1: k_loop<1, NSETS, 1>(c, acc); break;
-        default: k_loop<0, NSETS, 1>(c, acc); break;
+        case 4: k_loop<4, NSETS, 1, A8>(c, acc); break;
+        case 3: k_loop<3, NSETS, 1, A8>(c, acc); break;
+        case 2: k_loop<2, NSETS, 1, A8>(c, acc); break;
+        case 1: k_loop<1, NSETS, 1, A8>(c, acc); break;
+        default: k_loop<0, NSETS, 1, A8>(c, acc); break;
       }
     }
   }
 
   if constexpr (EPI == EPI_SWIGLU)
-    epilogue<EPI, NSETS, F8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
   else if (g.out_dtype == DT_F32)
-    epilogue<EPI, NSETS, F8, true>(g, ti, split, n0, wm, wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, true>(g, ti, split, n0, wm, wn, lane, lds, acc);
   else
-    epilogue<EPI, NSETS, F8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
 }
 
-template <int EPI, int NSETS, bool F8>
+template <int EPI, int NSETS, bool F8, bool A8>
 hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
-  constexpr int lds_bytes = F8 ? kLdsF8 : kLds;
+  constexpr int lds_bytes = F8 && !A8 ? kLdsF8 : kLds;
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS, F8>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS, F8, A8>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     (void)hipGetLastError();
     return true;
@@ -633,7 +674,7 @@ hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
   const int col_tiles = static_cast<int>((g.N + kBN / NSETS - 1) / (kBN / NSETS));
   const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles * g.ksplit;
   const unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
-  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
+  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8, A8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
                      row_tiles, col_tiles);
   return hipGetLastError();
 }
@@ -654,7 +695,12 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
 }
 
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
-  if (g.act_dtype != DT_BF16 || (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) || g.w_format != WF_MFMA16)
+  const bool a8 = g.act_dtype == DT_F8;
+  if ((g.act_dtype != DT_BF16 && !a8) || (g.w_dtype != DT_BF16 && g.w_dtype != DT_F8) || g.w_format != WF_MFMA16)
+    return false;
+  // fp8 activations: fp8 weights, K-blocked A with per-row scales, an even
+  // number of 64-input stages per split
+  if (a8 && (g.w_dtype != DT_F8 || !g.a_kb_rows || !g.a_scale || g.K % 128 || g.K / 128 < 2 * g.ksplit))
     return false;
   if (!g.order || !g.offsets || g.epi > EPI_SCATTER_WEIGHTED) return false;
   // bf16: an even number of 32-input stages per split; fp8: whole 64-input
@@ -683,10 +729,17 @@ hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t s) {
   if (!gemm_tiled256_supported(g)) return hipErrorNotSupported;
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
   const bool f8 = g.w_dtype == DT_F8;
-  if (g.epi == EPI_SWIGLU) return f8 ? launch_t<EPI_SWIGLU, 2, true>(g, s) : launch_t<EPI_SWIGLU, 2, false>(g, s);
+  if (g.act_dtype == DT_F8) {
+    if (g.epi == EPI_SWIGLU) return launch_t<EPI_SWIGLU, 2, true, true>(g, s);
+    if (g.epi == EPI_SCATTER_WEIGHTED) return launch_t<EPI_SCATTER_WEIGHTED, 1, true, true>(g, s);
+    return launch_t<EPI_SCATTER, 1, true, true>(g, s);
+  }
+  if (g.epi == EPI_SWIGLU)
+    return f8 ? launch_t<EPI_SWIGLU, 2, true, false>(g, s) : launch_t<EPI_SWIGLU, 2, false, false>(g, s);
   if (g.epi == EPI_SCATTER_WEIGHTED)
-    return f8 ? launch_t<EPI_SCATTER_WEIGHTED, 1, true>(g, s) : launch_t<EPI_SCATTER_WEIGHTED, 1, false>(g, s);
-  return f8 ? launch_t<EPI_SCATTER, 1, true>(g, s) : launch_t<EPI_SCATTER, 1, false>(g, s);
+    return f8 ? launch_t<EPI_SCATTER_WEIGHTED, 1, true, false>(g, s)
+              : launch_t<EPI_SCATTER_WEIGHTED, 1, false, false>(g, s);
+  return f8 ? launch_t<EPI_SCATTER, 1, true, false>(g, s) : launch_t<EPI_SCATTER, 1, false, false>(g, s);
 }
 
 }  // namespace fmoe

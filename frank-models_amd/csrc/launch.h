@@ -128,6 +128,11 @@ struct GroupedGemmArgs {
   // writes its output in that layout (out_kb_rows rows per piece column).
   int64_t a_kb_rows = 0;
   int64_t out_kb_rows = 0;
+  // act_dtype DT_F8 (256-tile kernel, DT_F8 weights): the A operand is e4m3
+  // codes, K-blocked in 64-input pieces whose 16-byte chunk g holds inputs
+  // 8g..8g+7 and 32+8g..32+8g+7 of the piece (the packed fp8 weights' lane
+  // order), each row p dequantised by a_scale[p].
+  const float* a_scale = nullptr;
   ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
 };
 
@@ -207,6 +212,16 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert,
                                     void* y, int dtype, int64_t width,
                                     hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+// Rows of src [*, n_cols] bf16 (row p = src row order[p] % n_tokens, or row p
+// when order is null), quantised to e4m3 with one scale per row: scale[p] =
+// the smallest power of two 2^e with max|row| / 2^e <= 448 (e clamped to
+// [-126, 126]; 1 for an all-zero row), code = RNE(v * 2^-e) saturating at
+// 448, written K-blocked in 64-input pieces (piece j
+// of row p at byte (j * n_rows + p) * 64, 16-byte chunk g holding inputs
+// 64j + 8g + [0, 8) then 64j + 32 + 8g + [0, 8)).  n_cols % 64 == 0 and
+// n_cols <= 16384.
+hipError_t launch_quantize_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols,
+                                   void* dst_q, float* dst_scale, hipStream_t stream);
 // dst (K-blocked, kb_offset with n_rows rows) row p = src row order[p] % n_tokens
 // (src [n_tokens, n_cols] row-major bf16, n_cols % 32 == 0): the gate/up
 // GEMM's A operand gathered into expert-sorted order.

@@ -19,6 +19,8 @@ from __future__ import annotations
 
 import numpy as np
 
+from . import numerics as _nm
+
 # The literal gather refuses to materialise more than this many bytes.
 LITERAL_BUDGET_BYTES = 2 << 30
 
@@ -183,25 +185,35 @@ def moe_ffn_block(
     normalize_weights,
     dtype=np.float64,
     return_routing=False,
+    act_quant=False,
 ):
     """Expert-grouped ``moe_ffn_block`` (same positional signature as
     oracles/moe.py:51-62).  Weighted expert outputs are summed in slot order
-    s = 0..k-1, as the reduction at moe_ffn_block.mlir:179-193."""
+    s = 0..k-1, as the reduction at moe_ffn_block.mlir:179-193.
+
+    ``act_quant=True`` is the fp8-activation variant (no counterpart in the
+    reference): the GEMM inputs -- the token rows, and the SwiGLU rows after
+    rounding to bf16 -- are replaced by their per-row e4m3 quantisation
+    (``numerics.fake_quantize_rows_e4m3fn``); routing still uses the
+    unquantised rows."""
     x = np.asarray(input, dtype=dtype)
     T, H = x.shape
     if H != n_embd:
         raise ValueError(f"input hidden {H} != n_embd {n_embd}")
     ids, w = router(x, gate_inp_w, n_expert_used, normalize_weights, dtype)
+    xg = _nm.fake_quantize_rows_e4m3fn(x).astype(dtype) if act_quant else x
     k = int(n_expert_used)
     y = np.zeros((k, T, H), dtype=dtype)
     for e in np.unique(ids):
         s_idx, t_idx = np.nonzero(ids == e)
-        xe = x[t_idx]
+        xe = xg[t_idx]
         # Contiguous per-expert copies keep the products on BLAS (a strided
         # expert slice would send NumPy down its element-wise matmul loop).
         up = xe @ np.ascontiguousarray(up_exps_w[:, :, int(e)], dtype=dtype).T
         gate = xe @ np.ascontiguousarray(gate_exps_w[:, :, int(e)], dtype=dtype).T
         h = swiglu(gate, up)
+        if act_quant:
+            h = _nm.fake_quantize_rows_e4m3fn(_nm.bf16_round(h)).astype(dtype)
         d = h @ np.ascontiguousarray(down_exps_w[:, :, int(e)], dtype=dtype).T
         y[s_idx, t_idx] = d * w[s_idx, t_idx][:, None]
     out = y[0].copy()

@@ -91,3 +91,28 @@ def quantize_per_channel_e4m3fn(w: np.ndarray):
 def dequantize_e4m3fn(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
     """``decode(q) * scale`` for the ``[n_out, n_in, E]`` / ``[n_out, E]`` pair."""
     return (e4m3fn_decode(q) * np.asarray(scale, np.float32)[:, None, :]).astype(np.float32)
+
+
+def quantize_rows_e4m3fn(a: np.ndarray):
+    """Per-row e4m3fn quantisation of activations (the fp8-activation GEMMs'
+    operand): ``scale[r] = 2**e``, the smallest power of two with
+    ``max_i |a[r, i]| / 2**e <= 448`` (``e`` clamped to [-126, 126]; 1 for an
+    all-zero row), ``q = e4m3fn_encode(a * 2**-e)``.  The scaling is exact, so
+    each value's rounding depends only on the value and its binade, not on the
+    row maximum.  Returns ``(q uint8, scale float32)``; the row's largest
+    magnitude lands in (224, 448]."""
+    a32 = np.asarray(a, dtype=np.float32)
+    amax = np.abs(a32).max(axis=1).astype(np.float32)
+    bits = amax.view(np.uint32).astype(np.int64)
+    # 448 = 1.75 * 2**8: amax = m * 2**E needs e = E - 8, or E - 7 when m > 1.75
+    e = (bits >> 23) - 127 - 8 + ((bits & 0x7FFFFF) > 0x600000)
+    e = np.clip(e, -126, 126)
+    scale = np.where(amax > 0, np.ldexp(np.float32(1.0), e).astype(np.float32), np.float32(1.0)).astype(np.float32)
+    q = e4m3fn_encode((a32 / scale[:, None]).astype(np.float32))
+    return q, scale
+
+
+def fake_quantize_rows_e4m3fn(a: np.ndarray) -> np.ndarray:
+    """``decode(q) * scale`` of ``quantize_rows_e4m3fn(a)`` (float32)."""
+    q, scale = quantize_rows_e4m3fn(a)
+    return (e4m3fn_decode(q) * scale[:, None]).astype(np.float32)

@@ -22,6 +22,27 @@ def assert_close_rms(actual, expected, rtol, what=""):
         assert rel <= rtol, f"{what}: relative Frobenius error {rel:.3e} > {rtol}"
 
 
+def assert_close_requantized(actual, expected, rtol, frob, max_frac, max_rms, what=""):
+    """For results computed from re-quantised intermediates (e4m3 SwiGLU rows):
+    an intermediate that the kernel and the oracle round one bf16 ulp apart
+    next to an e4m3 rounding boundary gets codes one e4m3 ulp apart, which
+    moves that row's outputs by more than the bf16 tolerance.  So: relative
+    Frobenius error <= frob, at most a fraction max_frac of the elements
+    outside ``rtol*|e| + rtol*RMS(e)``, and none beyond ``max_rms*RMS(e)``."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    assert a.shape == e.shape, (a.shape, e.shape)
+    r = rms(e)
+    err = np.abs(a - e)
+    rel = np.linalg.norm(a - e) / np.linalg.norm(e)
+    frac = float(np.mean(err > rtol * np.abs(e) + rtol * r))
+    worst = float(err.max() / r)
+    msg = f"{what}: rel Frobenius {rel:.2e}, {frac:.2e} of elements outside rtol {rtol}, max |err| {worst:.3f} RMS"
+    assert np.all(np.isfinite(a)), msg
+    assert rel <= frob and frac <= max_frac and worst <= max_rms, msg
+    return rel, frac, worst
+
+
 def assert_close(actual, expected, rtol=1e-5, atol=1e-6):
     """The reference's comparison (tests/utils.py:244-251)."""
     np.testing.assert_allclose(np.asarray(actual), np.asarray(expected), rtol=rtol, atol=atol)

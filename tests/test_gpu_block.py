@@ -4,9 +4,8 @@
   compared bit-exactly with the oracle's.
 * Outputs: fp32 rtol 1e-4; bf16 rtol 2e-2; fp8 5e-2 against the oracle on
   the dequantised weights; atol = rtol * RMS(reference) (helpers.assert_close_rms).
-* At full Mixtral size (T=4096) the oracle runs on a seeded sample of
-  tokens: tokens route and mix independently (moe_ffn_block.mlir:21), so the
-  sampled rows of the full-batch output must equal the oracle on those rows.
+* At the prefill sizes (C2/C5 T=4096, C3 T=8192) every output row and the
+  whole routing are compared with the fp32 grouped oracle.
 * Every kernel family (generic SIMT, MFMA tiled, MFMA streaming) that can run
   a case is checked on it.
 """
@@ -17,7 +16,7 @@ import torch
 
 from oracle import moe as om
 from oracle import numerics as nm
-from helpers import assert_close_rms
+from helpers import assert_close_requantized, assert_close_rms
 
 pytestmark = pytest.mark.gpu
 
@@ -156,22 +155,68 @@ def test_full_size_decode(fm, wl, name, T):
     assert_close_rms(out, ref, cfg.rtol, what=f"{name} T={T}")
 
 
-@pytest.mark.parametrize("name,T,sample", [("C2", 512, None), ("C2", 4096, 256), ("C3", 2048, 256),
-                                           ("C3", 8192, 256), ("C5", 4096, 256)])
-def test_full_size_prefill(fm, wl, name, T, sample):
+# Every output row, and the block's whole routing (ids, order, offsets), is
+# compared with the fp32 grouped oracle at the prefill sizes.
+@pytest.mark.parametrize("name,T", [("C2", 512), ("C2", 4096), ("C3", 2048), ("C3", 8192), ("C5", 4096)])
+def test_full_size_prefill(fm, wl, name, T):
     cfg = wl.CONFIGS[name]
     case = Case(fm, wl, cfg, T)
     out = case.run()
-    ids_dev, *_ = case.block.routing(T)
-    if sample is None:
-        ref, ids, _ = case.oracle(dtype=np.float32)
-        _check_routing(case, ids)
-        assert_close_rms(out, ref, cfg.rtol, what=f"{name} T={T}")
-    else:
-        tok = np.sort(np.random.default_rng(T).choice(T, size=sample, replace=False))
-        ref, ids, _ = case.oracle(tokens=tok, dtype=np.float32)
-        np.testing.assert_array_equal(ids_dev.cpu().numpy()[:, tok], ids)
-        assert_close_rms(out[tok], ref, cfg.rtol, what=f"{name} T={T} sampled")
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} T={T}")
+
+
+# ------------------------------------------------------------------ fp8 activations
+# FMOE_F8E4M3FN_A8: prefill GEMMs on the fp8 MFMA with per-row e4m3
+# activations.  Pinned against the oracle with the same activation
+# quantisation (act_quant: token rows, and SwiGLU rows rounded to bf16): the
+# token rows quantise bit-identically (power-of-two scales), the SwiGLU rows
+# can differ by one e4m3 code where the kernel's bf16 value and the oracle's
+# sit one ulp apart across a rounding boundary, so the bf16 tolerance holds
+# for all but a few elements in a million (assert_close_requantized).
+# Against the plain oracle (dequantised weights, bf16 activations) the e4m3
+# rounding of the activations is an error of about 4.7% relative Frobenius
+# norm at C5 (the budget; elementwise it reaches about 0.23 RMS(ref)), held
+# to 5e-2.
+@pytest.mark.parametrize("name,H,F,T", [("C5", 4096, 14336, 4096), ("C5", 512, 1024, 700), ("C3", 512, 256, 900),
+                                        ("C2", 1024, 2048, 300)])
+def test_fp8_activations_prefill(fm, wl, name, H, F, T):
+    cfg = wl.CONFIGS[name] if (H, F) == (wl.CONFIGS[name].n_embd, wl.CONFIGS[name].n_ff) else _scaled(wl, name, H, F)
+    cfg = wl.scaled(cfg, H, F, weights="fp8", rtol=5e-2) if cfg.weights != "fp8" else cfg
+    case = Case(fm, wl, cfg, T)
+    blk = fm.MoEFFNBlock(case.wr, *case.packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                         cfg.normalize, act_dtype=torch.bfloat16, fp8_activations=True)
+    out = blk(case.x)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    ids_dev, _, order, offsets = blk.routing(T)
+    c = cfg
+    ref_q, ids, _ = om.moe_ffn_block(case.x_np, case.wr_np, *case.host_w, c.n_expert, c.n_expert_used, c.n_embd,
+                                     c.n_ff, c.normalize, dtype=np.float32, return_routing=True, act_quant=True)
+    np.testing.assert_array_equal(ids_dev.cpu().numpy(), ids)
+    ro, roff = om.permute(ids, c.n_expert)
+    np.testing.assert_array_equal(order.cpu().numpy(), ro)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), roff)
+    assert_close_requantized(out, ref_q, 2e-2, frob=5e-3, max_frac=1e-4, max_rms=0.1,
+                             what=f"{name} H={H} F={F} T={T} vs act_quant oracle")
+    ref, _, _ = case.oracle(dtype=np.float32)
+    rel = float(np.linalg.norm(out - ref) / np.linalg.norm(ref))
+    print(f"fp8 activations {name} H={H} F={F} T={T}: rel Frobenius error vs bf16-activation oracle {rel:.4f}")
+    assert rel <= 5e-2, rel
+    # the fp8 path really ran: it differs from the bf16-activation block
+    assert not np.array_equal(out, case.run())
+
+
+def test_fp8_activations_decode_keeps_bf16(fm, wl):
+    """Decode-sized batches stream the weights with bf16 activations either way."""
+    cfg = wl.CONFIGS["C5"]
+    case = Case(fm, wl, cfg, 16)
+    blk = fm.MoEFFNBlock(case.wr, *case.packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                         cfg.normalize, act_dtype=torch.bfloat16, fp8_activations=True)
+    a = blk(case.x).float().cpu().numpy()
+    b = case.run()
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 # ------------------------------------------------------------------ properties

@@ -479,3 +479,57 @@ def test_sublayer_is_residual_plus_block_of_norm():
     # planted mistake: routing on the un-normalised residual changes the output
     wrong = res + om.moe_ffn_block_literal(res, wr, up, gate, down, E, k, H, F, False, dtype=np.float64)
     assert not np.allclose(out, wrong, rtol=1e-6, atol=1e-8)
+
+
+# ------------------------------------------------------------------ per-row e4m3 activations
+def test_quantize_rows_e4m3fn_known_answer_and_bounds():
+    rows = np.array([[1.0, -2.0, 0.5, 3.0], [0.0, 0.0, 0.0, 0.0], [448.0, 1.0, -2.0, 0.0],
+                     [449.0, 0.0, 0.0, 0.0], [2.0**-130, 0.0, 0.0, 0.0]], np.float32)
+    q, s = nm.quantize_rows_e4m3fn(rows)
+    # max 3: 3 / 448 lies in (2^-8, 2^-7], so the scale is 2^-7 and the row is exact
+    assert s[0] == 2.0**-7
+    np.testing.assert_array_equal(nm.e4m3fn_decode(q[0]), [128.0, -256.0, 64.0, 384.0])
+    assert s[1] == 1.0 and not q[1].any()  # all-zero row
+    assert s[2] == 1.0 and nm.e4m3fn_decode(q[2])[0] == 448.0  # 448 fits exactly: 2^0
+    assert s[3] == 2.0  # just above 448: the next power of two
+    assert s[4] == 2.0**-126  # a subnormal maximum: the scale is clamped
+    rng = np.random.default_rng(3)
+    a = (rng.standard_normal((64, 512)) * rng.uniform(0.01, 100, (64, 1))).astype(np.float32)
+    q, s = nm.quantize_rows_e4m3fn(a)
+    # powers of two; every row's largest magnitude lands in (224, 448]
+    np.testing.assert_array_equal(np.frexp(s)[0], 0.5)
+    top = np.argmax(np.abs(a), axis=1)
+    big = np.abs(a[np.arange(64), top]) / s
+    assert np.all((big > 224) & (big <= 448))
+    # half an ulp of a 3-bit mantissa: 2^-4 relative, above the subnormal range
+    d = nm.fake_quantize_rows_e4m3fn(a)
+    normal = np.abs(a) >= 2.0**-6 * s[:, None]
+    assert np.all(np.abs(d - a)[normal] <= 2.0**-4 * np.abs(a)[normal] * (1 + 1e-6))
+    # scale invariance: a row times a power of two quantises to the same codes
+    q2, s2 = nm.quantize_rows_e4m3fn(a * np.float32(8.0))
+    np.testing.assert_array_equal(q2, q)
+    np.testing.assert_array_equal(s2, s * 8)
+    # planted mistake: scale = max/448 (not a power of two) changes some codes
+    q_bad = nm.e4m3fn_encode(a / (np.abs(a).max(axis=1, keepdims=True) / 448.0))
+    assert not np.array_equal(q_bad, q)
+
+
+def test_act_quant_block_is_the_block_on_quantised_rows():
+    """E = k = 1: the fp8-activation block is the dense SwiGLU FFN of the
+    per-row e4m3 token rows, with the SwiGLU rows rounded to bf16 and
+    quantised per row before the down projection."""
+    rng = np.random.default_rng(4)
+    T, H, F = 24, 64, 128
+    x = nm.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    wr = np.zeros((1, H), np.float32)
+    up, gate = ((rng.standard_normal((F, H, 1)) * 0.05).astype(np.float32) for _ in range(2))
+    down = (rng.standard_normal((H, F, 1)) * 0.05).astype(np.float32)
+    out = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, dtype=np.float64, act_quant=True)
+    xq = nm.fake_quantize_rows_e4m3fn(x).astype(np.float64)
+    g, u = xq @ gate[:, :, 0].T.astype(np.float64), xq @ up[:, :, 0].T.astype(np.float64)
+    h = nm.fake_quantize_rows_e4m3fn(nm.bf16_round(g * u / (1 + np.exp(-u)))).astype(np.float64)
+    np.testing.assert_allclose(out, h @ down[:, :, 0].T.astype(np.float64), rtol=1e-12, atol=1e-12)
+    # and it differs from the unquantised block by the e4m3 rounding only (a few percent)
+    plain = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, dtype=np.float64)
+    rel = np.linalg.norm(out - plain) / np.linalg.norm(plain)
+    assert 1e-3 < rel < 0.1, rel
