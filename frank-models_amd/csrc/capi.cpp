@@ -250,7 +250,7 @@ struct BlockLayout {
   size_t xkb, xkb_bytes;  // token rows gathered K-blocked in expert order (0 bytes when no prefill GEMM can use them)
   // fp8 activations (FMOE_F8E4M3FN_A8, prefill-sized batches): e4m3 token
   // rows and SwiGLU rows, K-blocked, with their per-row scales (0 bytes otherwise)
-  size_t xq, xs, hq, hs, a8_bytes;
+  size_t xq, xs, hq, hs, hmax, xmax, a8_bytes;
   size_t rpart;          // decode router's split logits (0 bytes when the shape takes the general router)
   size_t rpart_bytes;
   int h_dtype, y_dtype;
@@ -321,9 +321,13 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
     off += align_up(static_cast<size_t>(n) * F);
     L.hs = off;
     off += align_up(static_cast<size_t>(n) * 4);
+    L.hmax = off;
+    off += align_up(static_cast<size_t>(n) * 4);
+    L.xmax = off;
+    off += align_up(static_cast<size_t>(T) * 4);
     L.a8_bytes = off - L.xq;
   } else {
-    L.xs = L.hq = L.hs = off;
+    L.xs = L.hq = L.hs = L.hmax = L.xmax = off;
   }
   L.total = off;
   return L;
@@ -519,13 +523,20 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
       gk.a = at<char>(workspace, L.xq);
       gk.act_dtype = DT_F8;
       gk.a_scale = at<float>(workspace, L.xs);
+      gk.row_amax = at<unsigned>(workspace, L.hmax);
       dk.a = at<char>(workspace, L.hq);
       dk.act_dtype = DT_F8;
       dk.a_scale = at<float>(workspace, L.hs);
       if (both256 && gemm_tiled256_supported(gk) && gemm_tiled256_supported(dk)) {
         ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
-        FMOE_HIP(launch_quantize_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<char>(workspace, L.xq),
-                                         at<float>(workspace, L.xs), s));
+        // max |x| per token (that pass also clears the per-row max the
+        // gate/up epilogue accumulates for h), then the token rows gathered
+        // into expert order and quantised.
+        FMOE_HIP(launch_row_absmax(c.input, T, static_cast<int>(n_embd), at<unsigned>(workspace, L.xmax),
+                                   at<unsigned>(workspace, L.hmax), n, s));
+        FMOE_HIP(launch_quantize_rows_kb(c.input, order, n, T, static_cast<int>(n_embd),
+                                         at<unsigned>(workspace, L.xmax), at<char>(workspace, L.xq),
+                                         at<float>(workspace, L.xs), nullptr, s));
         g = gk;
         dq = dk;
         h_quant = true;
@@ -548,8 +559,8 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   }
   if (h_quant) {
     ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
-    FMOE_HIP(launch_quantize_rows_kb(h, nullptr, n, n, static_cast<int>(n_ff), at<char>(workspace, L.hq),
-                                     at<float>(workspace, L.hs), s));
+    FMOE_HIP(launch_quantize_rows_kb(h, nullptr, n, n, static_cast<int>(n_ff), at<unsigned>(workspace, L.hmax),
+                                     at<char>(workspace, L.hq), at<float>(workspace, L.hs), nullptr, s));
     d = dq;
   }
 

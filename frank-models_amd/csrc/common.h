@@ -106,35 +106,44 @@ __device__ __forceinline__ float e4m3fn_to_f32(uint32_t c) {
 }
 
 // float -> e4m3fn code, round to nearest even, finite overflow saturates to
-// +-448, NaN -> 0x7F.
+// +-448, NaN -> 0x7F.  Branch-free: both the normal rounding (RNE
+// on the 20 dropped mantissa bits, a carry moving into the exponent) and the
+// subnormal one (m * 2^-9, m = rint(|x| * 512), where 8 is the smallest
+// normal code) are computed and one is selected.
 __device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
-  uint32_t bits = __float_as_uint(x);
-  uint32_t sign = (bits >> 24) & 0x80u;
-  float a = fabsf(x);
-  if (a != a) return 0x7Fu;
-  if (a >= 448.0f) return sign | 0x7Eu;
-  uint32_t ab = __float_as_uint(a);
-  int32_t exp = static_cast<int32_t>(ab >> 23) - 127;
-  uint32_t code;
-  if (exp < -6) {
-    // subnormal range: value = m * 2^-9, m in [0, 8]; scale exactly by 2^9.
-    float q = a * 512.0f;  // exact (power of two scaling, no underflow here)
-    float r = rintf(q);    // ties to even
-    code = static_cast<uint32_t>(r);  // 8 becomes the smallest normal 0x08
-  } else {
-    // normal: keep 3 mantissa bits with RNE on the 20 dropped bits.
-    uint32_t mant = ab & 0x7FFFFFu;
-    uint32_t keep = mant >> 20;
-    uint32_t rest = mant & 0xFFFFFu;
-    uint32_t e = static_cast<uint32_t>(exp + 7);
-    uint32_t v = (e << 3) | keep;
-    if (rest > 0x80000u || (rest == 0x80000u && (keep & 1u))) v += 1;
-    code = v > 0x7Eu ? 0x7Eu : v;
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  const float a = fabsf(x);
+  const uint32_t ab = __float_as_uint(a);
+  const uint32_t r = ab + 0x7FFFFu + ((ab >> 20) & 1u);
+  const uint32_t normal = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+  const uint32_t sub = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
+  uint32_t code = a < 0x1p-6f ? sub : normal;
+  code = a >= 448.0f ? 0x7Eu : code;  // also +inf
+  return a != a ? 0x7Fu : (sign | code);
+}
+
+// Largest |v| of the 8 bf16 values in a 16-byte chunk (NaN ignored).
+__device__ __forceinline__ float absmax_bf16x8(const u32x4_t v) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m = fmaxf(m, fabsf(__uint_as_float(v[i] << 16)));
+    m = fmaxf(m, fabsf(__uint_as_float(v[i] & 0xFFFF0000u)));
   }
-  return sign | code;
+  return m;
 }
 
 // ---------------------------------------------------------------- waves
+// Maximum over each 16-lane row of a wave (DPP row rotations; every lane of
+// the row must take part and gets the result).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xF, 0xF, false)));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

@@ -144,17 +144,6 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kb_kernel(const bf16_t* 
   }
 }
 
-// Largest |v| of the 8 bf16 values in a 16-byte chunk (NaN ignored).
-__device__ __forceinline__ float absmax_bf16x8(const u32x4_t v) {
-  float m = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m = fmaxf(m, fabsf(__uint_as_float(v[i] << 16)));
-    m = fmaxf(m, fabsf(__uint_as_float(v[i] & 0xFFFF0000u)));
-  }
-  return m;
-}
-
 // 8 bf16 values times inv -> 8 e4m3fn codes in two dwords (element order).
 __device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
   uint32_t w[2];
@@ -169,60 +158,129 @@ __device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
   return u32x2_t{w[0], w[1]};
 }
 
-// One wave per row p (grid-stride): lane c of a pass holds chunk c = 16
-// values, inputs 64j + 8g + [0, 8) and 64j + 32 + 8g + [0, 8) for piece
-// j = c / 4, g = c % 4 (the packed fp8 weights' lane order); the row stays
-// in registers (kPasses passes of 64 chunks) while the wave reduces max|v|,
-// then every value is scaled by 1 / scale (a power of two) and rounded to e4m3.
-template <int kPasses>
+// Power-of-two scale 2^e of a row whose largest magnitude is amax: the
+// smallest e with amax / 2^e <= 448 (448 = 1.75 * 2^8), clamped to
+// [-126, 126]; 1 for amax = 0.  *inv = 2^-e.  Exact to apply, and each
+// value's rounding depends only on the value and its binade.
+__device__ __forceinline__ float pow2_scale(float amax, float* inv) {
+  if (!(amax > 0.f)) {
+    *inv = 1.f;
+    return 1.f;
+  }
+  const uint32_t ab = __float_as_uint(amax);
+  int e = static_cast<int>(ab >> 23) - 127 - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+  e = min(max(e, -126), 126);
+  *inv = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+  return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
+// max|row| of src [n_rows, n_cols] bf16 as float bits, one wave per row
+// (16-byte loads, four in flight per lane); the first n_zero words of
+// zero_out (may be null) are cleared on the way.
+__global__ __launch_bounds__(kThreads) void row_absmax_kernel(const bf16_t* __restrict__ src, int n_rows, int n_cols,
+                                                              unsigned* __restrict__ amax_out,
+                                                              unsigned* __restrict__ zero_out, int n_zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int waves = kThreads / kWave;
+  if (zero_out)
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n_zero;
+         i += static_cast<int64_t>(gridDim.x) * kThreads)
+      zero_out[i] = 0u;
+  const int n_chunks = n_cols / 8;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * waves + threadIdx.x / kWave; r < n_rows;
+       r += static_cast<int64_t>(gridDim.x) * waves) {
+    const u32x4_t* row = reinterpret_cast<const u32x4_t*>(src + r * n_cols);
+    float m = 0.f;
+    for (int c = lane; c < n_chunks; c += 4 * kWave) {
+      u32x4_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (c + u * kWave < n_chunks) v[u] = row[c + u * kWave];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (c + u * kWave < n_chunks) m = fmaxf(m, absmax_bf16x8(v[u]));
+    }
+    m = wave_max(m);
+    if (lane == 0) amax_out[r] = __float_as_uint(m);
+  }
+}
+
+// A block of 256 threads quantises pieces 32 y .. 32 y + 31 of rows
+// p0 .. p0+15 (p0 = 16 x).  row_amax, when given, holds max|v| of each
+// source row (indexed like src); otherwise each wave first reduces max|v|
+// of four rows (coalesced 16-byte loads) into LDS.  Then wave w
+// writes pieces j = 32 y + w + 4 t (t < 8, all loads first): lane
+// (r = lane / 4, g = lane % 4) converts row p0+r's inputs 64j + 8g + [0, 8)
+// and 64j + 32 + 8g + [0, 8) (the packed fp8 weights' lane order) and stores
+// them as chunk g of the piece, so each store instruction writes the 16
+// rows' pieces as one contiguous 1 KiB run.
 __global__ __launch_bounds__(kThreads) void quantize_rows_kb_kernel(const bf16_t* __restrict__ src,
                                                                     const int* __restrict__ order, int n_rows,
                                                                     int n_tokens, int n_cols,
+                                                                    const unsigned* __restrict__ row_amax,
                                                                     uint8_t* __restrict__ dst_q,
-                                                                    float* __restrict__ dst_scale) {
+                                                                    float* __restrict__ dst_scale,
+                                                                    unsigned* __restrict__ zero_out) {
+  __shared__ int64_t s_row[16];
+  __shared__ float s_inv[16];
   const int lane = threadIdx.x & (kWave - 1);
-  const int waves = kThreads / kWave;
-  const int n_chunks = n_cols / 16;
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * waves + threadIdx.x / kWave; p < n_rows;
-       p += static_cast<int64_t>(gridDim.x) * waves) {
-    const int64_t srow = order ? static_cast<int64_t>(static_cast<uint32_t>(order[p]) % static_cast<uint32_t>(n_tokens))
-                               : p;
-    const bf16_t* row = src + srow * n_cols;
-    u32x4_t lo[kPasses], hi[kPasses];
-    float amax = 0.f;
+  const int wave = threadIdx.x / kWave;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 16;
+  if (threadIdx.x < 16) {
+    const int64_t p = p0 + threadIdx.x;
+    int64_t srow = 0;
+    if (p < n_rows)
+      srow = order ? static_cast<int64_t>(static_cast<uint32_t>(order[p]) % static_cast<uint32_t>(n_tokens)) : p;
+    s_row[threadIdx.x] = srow;
+    if (zero_out && blockIdx.y == 0 && p < n_rows) zero_out[p] = 0u;
+  }
+  __syncthreads();
+  const int n_chunks = n_cols / 8;  // 16-byte chunks of a row
+  for (int q = 0; q < 4; ++q) {
+    const int r = wave * 4 + q;
+    const int64_t p = p0 + r;
+    if (p >= n_rows) break;  // wave-uniform
+    float amax;
+    if (row_amax) {
+      amax = __uint_as_float(row_amax[s_row[r]]);
+    } else {
+      const bf16_t* row = src + s_row[r] * n_cols;
+      amax = 0.f;
+      for (int c = lane; c < n_chunks; c += kWave)
+        amax = fmaxf(amax, absmax_bf16x8(*reinterpret_cast<const u32x4_t*>(row + c * 8)));
+      amax = wave_max(amax);
+    }
+    float inv;
+    const float scale = pow2_scale(amax, &inv);
+    if (lane == 0) {
+      s_inv[r] = inv;
+      if (blockIdx.y == 0) dst_scale[p] = scale;
+    }
+  }
+  __syncthreads();
+  const int r = lane >> 2, g = lane & 3;
+  const int64_t p = p0 + r;
+  if (p >= n_rows) return;
+  const bf16_t* row = src + s_row[r] * n_cols;
+  const float inv = s_inv[r];
+  const int n_pieces = n_cols / 64;
+  u32x4_t lo[8], hi[8];
 #pragma unroll
-    for (int it = 0; it < kPasses; ++it) {
-      const int c = it * kWave + lane;
-      if (c < n_chunks) {
-        const int j = c >> 2, q = c & 3;
-        lo[it] = *reinterpret_cast<const u32x4_t*>(row + 64 * j + 8 * q);
-        hi[it] = *reinterpret_cast<const u32x4_t*>(row + 64 * j + 32 + 8 * q);
-        amax = fmaxf(amax, fmaxf(absmax_bf16x8(lo[it]), absmax_bf16x8(hi[it])));
-      }
+  for (int t = 0; t < 8; ++t) {
+    const int j = static_cast<int>(blockIdx.y) * 32 + wave + 4 * t;
+    if (j < n_pieces) {
+      lo[t] = *reinterpret_cast<const u32x4_t*>(row + 64 * j + 8 * g);
+      hi[t] = *reinterpret_cast<const u32x4_t*>(row + 64 * j + 32 + 8 * g);
     }
-    amax = wave_max(amax);
-    // scale = 2^e, the smallest power of two with max|v| / scale <= 448 (448 =
-    // 1.75 * 2^8): exact to apply, and the rounding of each value does not
-    // depend on the row's maximum (only its binade).
-    float scale = 1.f, inv = 1.f;
-    if (amax > 0.f) {
-      const uint32_t ab = __float_as_uint(amax);
-      int e = static_cast<int>(ab >> 23) - 127 - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0);
-      e = min(max(e, -126), 126);
-      scale = __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
-      inv = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
-    }
+  }
 #pragma unroll
-    for (int it = 0; it < kPasses; ++it) {
-      const int c = it * kWave + lane;
-      if (c < n_chunks) {
-        const int j = c >> 2, q = c & 3;
-        const u32x2_t a = e4m3_codes8(lo[it], inv), b = e4m3_codes8(hi[it], inv);
-        *reinterpret_cast<u32x4_t*>(dst_q + (static_cast<int64_t>(j) * n_rows + p) * 64 + q * 16) =
-            u32x4_t{a[0], a[1], b[0], b[1]};
-      }
+  for (int t = 0; t < 8; ++t) {
+    const int j = static_cast<int>(blockIdx.y) * 32 + wave + 4 * t;
+    if (j < n_pieces) {
+      const u32x2_t a = e4m3_codes8(lo[t], inv), b = e4m3_codes8(hi[t], inv);
+      *reinterpret_cast<u32x4_t*>(dst_q + (static_cast<int64_t>(j) * n_rows + p) * 64 + g * 16) =
+          u32x4_t{a[0], a[1], b[0], b[1]};
     }
-    if (lane == 0) dst_scale[p] = scale;
   }
 }
 
@@ -414,22 +472,31 @@ hipError_t launch_zero_invalid_rows(const int* ids, int n_assign, int n_expert, 
   return hipGetLastError();
 }
 
+hipError_t launch_row_absmax(const void* src, int n_rows, int n_cols, unsigned* amax_out, unsigned* zero_out,
+                             int n_zero, hipStream_t stream) {
+  if (n_rows <= 0 && (!zero_out || n_zero <= 0)) return hipSuccess;
+  if (n_cols <= 0 || n_cols % 8 || reinterpret_cast<uintptr_t>(src) % 16) return hipErrorInvalidValue;
+  constexpr int waves = kThreads / kWave;
+  const int64_t need = std::max<int64_t>((static_cast<int64_t>(n_rows) + waves - 1) / waves,
+                                         (static_cast<int64_t>(n_zero) + kThreads - 1) / kThreads);
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(need, 1), 1 << 16));
+  hipLaunchKernelGGL(row_absmax_kernel, dim3(blocks), dim3(kThreads), 0, stream, static_cast<const bf16_t*>(src),
+                     n_rows, n_cols, amax_out, zero_out, n_zero);
+  return hipGetLastError();
+}
+
 hipError_t launch_quantize_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols,
-                                   void* dst_q, float* dst_scale, hipStream_t stream) {
+                                   const unsigned* row_amax, void* dst_q, float* dst_scale, unsigned* zero_out,
+                                   hipStream_t stream) {
   if (n_rows <= 0) return hipSuccess;
   if (n_cols <= 0 || n_cols % 64 || n_cols > 16384 || reinterpret_cast<uintptr_t>(src) % 16 ||
       reinterpret_cast<uintptr_t>(dst_q) % 16 || (order && n_tokens <= 0))
     return hipErrorInvalidValue;
-  constexpr int waves = kThreads / kWave;
-  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((n_rows + waves - 1) / waves, 1 << 16));
-  const auto* x = static_cast<const bf16_t*>(src);
-  auto* q = static_cast<uint8_t*>(dst_q);
-  if (n_cols <= 4096)
-    hipLaunchKernelGGL(quantize_rows_kb_kernel<4>, dim3(blocks), dim3(kThreads), 0, stream, x, order, n_rows,
-                       n_tokens, n_cols, q, dst_scale);
-  else
-    hipLaunchKernelGGL(quantize_rows_kb_kernel<16>, dim3(blocks), dim3(kThreads), 0, stream, x, order, n_rows,
-                       n_tokens, n_cols, q, dst_scale);
+  const dim3 grid(static_cast<unsigned>((static_cast<int64_t>(n_rows) + 15) / 16),
+                  static_cast<unsigned>((n_cols / 64 + 31) / 32));
+  hipLaunchKernelGGL(quantize_rows_kb_kernel, grid, dim3(kThreads), 0, stream,
+                     static_cast<const bf16_t*>(src), order, n_rows, n_tokens, n_cols, row_amax,
+                     static_cast<uint8_t*>(dst_q), dst_scale, zero_out);
   return hipGetLastError();
 }
 

@@ -207,6 +207,14 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
       const int rl = id / kChunks, ch = id % kChunks;
       const int r = pass * 128 + rl;
       const int64_t col = n0 + ch * (16 / kEsz);
+      if constexpr (A8 && EPI == EPI_SWIGLU) {
+        // The next GEMM's per-row activation scale: max|h| of this tile's
+        // columns of row r (its 16 chunks sit on one 16-lane DPP row).
+        float m = 0.f;
+        if (r < ti.rows && col < N) m = absmax_bf16x8(*reinterpret_cast<const u32x4_t*>(lds + rl * kPitch + ch * 16));
+        m = row16_max(m);
+        if (ch == 0 && r < ti.rows && g.row_amax) atomicMax(g.row_amax + ti.row0 + r, __float_as_uint(m));
+      }
       if (r >= ti.rows || col >= N) continue;
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + rl * kPitch + ch * 16);
       if constexpr (kWeighted && OUT_F32)

@@ -133,6 +133,10 @@ struct GroupedGemmArgs {
   // 8g..8g+7 and 32+8g..32+8g+7 of the piece (the packed fp8 weights' lane
   // order), each row p dequantised by a_scale[p].
   const float* a_scale = nullptr;
+  // SwiGLU epilogue with fp8 activations: atomic max, per output row p, of
+  // the bit patterns of |h| (h rounded to bf16, so non-negative floats order
+  // as unsigned integers) into row_amax[p], which starts at zero.
+  unsigned* row_amax = nullptr;
   ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
 };
 
@@ -220,8 +224,16 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // of row p at byte (j * n_rows + p) * 64, 16-byte chunk g holding inputs
 // 64j + 8g + [0, 8) then 64j + 32 + 8g + [0, 8)).  n_cols % 64 == 0 and
 // n_cols <= 16384.
+// row_amax (may be null): max|v| of each source row as float bits, indexed
+// like src (then the rows are read once); zero_out (may be null): n_rows
+// words set to zero.
+// launch_row_absmax: amax_out[r] = max|src[r, :]| (float bits) for src
+// [n_rows, n_cols] bf16, n_cols % 8 == 0; also clears zero_out[0, n_zero).
 hipError_t launch_quantize_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols,
-                                   void* dst_q, float* dst_scale, hipStream_t stream);
+                                   const unsigned* row_amax, void* dst_q, float* dst_scale, unsigned* zero_out,
+                                   hipStream_t stream);
+hipError_t launch_row_absmax(const void* src, int n_rows, int n_cols, unsigned* amax_out, unsigned* zero_out,
+                             int n_zero, hipStream_t stream);
 // dst (K-blocked, kb_offset with n_rows rows) row p = src row order[p] % n_tokens
 // (src [n_tokens, n_cols] row-major bf16, n_cols % 32 == 0): the gate/up
 // GEMM's A operand gathered into expert-sorted order.

@@ -533,3 +533,34 @@ def test_act_quant_block_is_the_block_on_quantised_rows():
     plain = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, dtype=np.float64)
     rel = np.linalg.norm(out - plain) / np.linalg.norm(plain)
     assert 1e-3 < rel < 0.1, rel
+
+
+def _branchfree_e4m3(x):
+    """The kernels' branch-free float -> e4m3fn encoder (common.h
+    f32_to_e4m3fn), step for step in NumPy integer arithmetic."""
+    x = np.asarray(x, np.float32)
+    sign = (x.view(np.uint32) >> 24) & 0x80
+    a = np.abs(x)
+    ab = a.view(np.uint32).astype(np.uint64)
+    r = (ab + 0x7FFFF + ((ab >> 20) & 1)) & 0xFFFFFFFF
+    normal = ((((r >> 23) - 120) & 0xFFFFFFFF) << 3) | ((r >> 20) & 7)
+    sub = np.rint(a * np.float32(512.0)).astype(np.uint64)
+    code = np.where(a < np.float32(2.0**-6), sub, normal)
+    code = np.where(a >= np.float32(448.0), 0x7E, code)
+    return np.where(np.isnan(a), 0x7F, sign.astype(np.uint64) | code).astype(np.uint8)
+
+
+def test_branchfree_e4m3_encoder_matches_the_oracle():
+    """Every representable value, every midpoint between neighbours and one
+    float32 ulp either side of it (the RNE ties), the subnormal range,
+    saturation, inf and NaN, and a random sweep: the integer-add rounding the
+    kernels use equals the oracle's nearest-value search."""
+    vals = nm.E4M3FN_VALUES[:127]
+    mids = (vals[:-1] + vals[1:]) / 2
+    pts = np.concatenate([vals, mids, np.nextafter(mids.astype(np.float32), np.float32(0)),
+                          np.nextafter(mids.astype(np.float32), np.float32(1e9)), [448.0, 460.0, 464.0, 1e6]])
+    rng = np.random.default_rng(5)
+    pts = np.concatenate([pts, rng.uniform(0, 500, 200000), rng.uniform(0, 2.0**-5, 50000),
+                          2.0 ** rng.uniform(-12, 9, 100000)]).astype(np.float32)
+    pts = np.concatenate([pts, -pts, [np.inf, -np.inf, np.nan, -0.0]]).astype(np.float32)
+    np.testing.assert_array_equal(_branchfree_e4m3(pts), nm.e4m3fn_encode(pts))
