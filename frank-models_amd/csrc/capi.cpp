@@ -307,7 +307,7 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   const bool prefill = act == FMOE_BF16 && n > 8 * E;
   const bool a8 = prefill && block_wdt == FMOE_F8E4M3FN_A8 && H % 128 == 0 && F % 128 == 0 && H <= 16384 &&
                   F <= 16384;
-  const bool kb_candidate = prefill && !a8 && H % 64 == 0 && F % 64 == 0;
+  const bool kb_candidate = prefill && !a8 && H % 64 == 0 && F % 64 == 0 && (F + 127) / 128 >= 16;
   L.xkb = off;
   L.xkb_bytes = kb_candidate ? static_cast<size_t>(n) * H * 2 : 0;
   off += align_up(L.xkb_bytes);
@@ -509,7 +509,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   // instead, and both GEMMs run on the fp8 MFMA.
   bool h_quant = false;
   GroupedGemmArgs dq = d;
-  if (L.xkb_bytes || L.a8_bytes) {
+  if (n > 8 * n_expert && act_dtype == FMOE_BF16) {
     int vg = 0, vd = 0;
     const int pg = pick_path(g, &vg), pd = pick_path(d, &vd);
     const bool tiled_g = pg == FMOE_PATH_TILED || pg == FMOE_PATH_TILED_LARGE;
@@ -542,13 +542,25 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
         h_quant = true;
       }
     } else {
-      gk.a = at<char>(workspace, L.xkb);
-      gk.out_kb_rows = n;
-      if (both256 && gemm_tiled256_supported(gk) && gemm_tiled256_supported(dk)) {
-        ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
-        FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<char>(workspace, L.xkb),
-                                       s));
-        g = gk;
+      // h goes K-blocked at no cost; the token rows are worth gathering only
+      // when many column tiles of the gate/up GEMM re-read them (measured:
+      // Mixtral's 112 tiles gain 77 us for a 19 us gather, Qwen3's 6 tiles
+      // lose 74 us at 8192 tokens).
+      const bool gather_x = (n_ff + 127) / 128 >= 16;
+      GroupedGemmArgs gh = g;  // gate/up reading the token rows in place
+      gh.out_kb_rows = n;
+      if (gather_x) {
+        gk.a = at<char>(workspace, L.xkb);
+        gk.out_kb_rows = n;
+      }
+      GroupedGemmArgs& gsel = gather_x ? gk : gh;
+      if (both256 && gemm_tiled256_supported(gsel) && gemm_tiled256_supported(dk)) {
+        if (gather_x) {
+          ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
+          FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd),
+                                         at<char>(workspace, L.xkb), s));
+        }
+        g = gsel;
         d = dk;
       }
     }

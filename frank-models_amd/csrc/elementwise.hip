@@ -284,6 +284,40 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kb_kernel(const bf16_t
   }
 }
 
+// combine_kernel with the slot count KS and the split count NS fixed, fp32
+// partials and 4-wide rows: all KS * NS loads of an element group are in
+// flight before the first add.  The adds run in the same order (splits,
+// then slots, then the residual), so the result is bit-identical.
+template <typename TO, int KS, int NS>
+__global__ __launch_bounds__(kThreads) void combine_fixed_kernel(const float* __restrict__ y, const TO* residual,
+                                                                 TO* out, int n_tokens, int n_embd,
+                                                                 int64_t split_stride) {
+  const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kThreads * 4) {
+    f32x4_t v[KS][NS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int q = 0; q < NS; ++q) v[s][q] = *reinterpret_cast<const f32x4_t*>(y + i + s * total + q * split_stride);
+    float acc[4], p[4];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      f32x4_t w = v[s][0];
+#pragma unroll
+      for (int q = 1; q < NS; ++q) w += v[s][q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = s == 0 ? w[j] : acc[j] + w[j];
+    }
+    if (residual) {
+      ldv<4>(residual, i, p);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = p[j] + acc[j];
+    }
+    stv<4>(out, i, acc);
+  }
+}
+
 // One block per row (grid-stride over rows).  Sum of squares in fp32 (per
 // thread, then across the block), rms = sqrt(sum / H + eps), then
 // out = (x / rms) * weight, the reference's operation order.  out may alias
@@ -395,6 +429,24 @@ void combine_t(const void* y, const void* residual, void* out, int n_tokens, int
                    reinterpret_cast<uintptr_t>(y) % (4 * sizeof(TY)) == 0 &&
                    reinterpret_cast<uintptr_t>(out) % (4 * sizeof(TO)) == 0 &&
                    reinterpret_cast<uintptr_t>(residual) % (4 * sizeof(TO)) == 0;
+  if constexpr (sizeof(TY) == 4) {
+    if (vec && k >= 1 && k <= 8 && nsplit >= 1 && nsplit <= 2) {
+      using Fn = void (*)(const float*, const TO*, TO*, int, int, int64_t);
+      static constexpr Fn table[8][2] = {
+          {combine_fixed_kernel<TO, 1, 1>, combine_fixed_kernel<TO, 1, 2>},
+          {combine_fixed_kernel<TO, 2, 1>, combine_fixed_kernel<TO, 2, 2>},
+          {combine_fixed_kernel<TO, 3, 1>, combine_fixed_kernel<TO, 3, 2>},
+          {combine_fixed_kernel<TO, 4, 1>, combine_fixed_kernel<TO, 4, 2>},
+          {combine_fixed_kernel<TO, 5, 1>, combine_fixed_kernel<TO, 5, 2>},
+          {combine_fixed_kernel<TO, 6, 1>, combine_fixed_kernel<TO, 6, 2>},
+          {combine_fixed_kernel<TO, 7, 1>, combine_fixed_kernel<TO, 7, 2>},
+          {combine_fixed_kernel<TO, 8, 1>, combine_fixed_kernel<TO, 8, 2>}};
+      hipLaunchKernelGGL(table[k - 1][nsplit - 1], dim3(grid_for(total / 4)), dim3(kThreads), 0, stream,
+                         static_cast<const float*>(y), static_cast<const TO*>(residual), static_cast<TO*>(out),
+                         n_tokens, n_embd, split_stride);
+      return;
+    }
+  }
   if (vec)
     hipLaunchKernelGGL((combine_kernel<TY, TO, 4>), dim3(grid_for(total / 4)), dim3(kThreads), 0, stream,
                        static_cast<const TY*>(y), static_cast<const TO*>(residual), static_cast<TO*>(out),
