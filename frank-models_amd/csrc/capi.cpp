@@ -507,7 +507,11 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   // writes h in that layout for the down GEMM.  With fp8 activations
   // (FMOE_F8E4M3FN_A8) the gathered rows and h are quantised to e4m3 per row
   // instead, and both GEMMs run on the fp8 MFMA.
+  // The 256-tile down GEMM stores its weighted per-slot rows (and K-split
+  // partials) in bf16, the activation type, halving the traffic of its
+  // epilogue and of combine; the other paths keep fp32.
   bool h_quant = false;
+  int y_dtype = L.y_dtype;
   GroupedGemmArgs dq = d;
   if (n > 8 * n_expert && act_dtype == FMOE_BF16) {
     int vg = 0, vd = 0;
@@ -519,6 +523,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
     gk.a_mode = A_DIRECT;
     gk.a_kb_rows = n;
     dk.a_kb_rows = n;
+    dk.out_dtype = FMOE_BF16;
     if (L.a8_bytes) {
       gk.a = at<char>(workspace, L.xq);
       gk.act_dtype = DT_F8;
@@ -540,6 +545,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
         g = gk;
         dq = dk;
         h_quant = true;
+        y_dtype = FMOE_BF16;
       }
     } else {
       // h goes K-blocked at no cost; the token rows are worth gathering only
@@ -562,6 +568,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
         }
         g = gsel;
         d = dk;
+        y_dtype = FMOE_BF16;
       }
     }
   }
@@ -587,7 +594,7 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   // plus the residual for the sub-layer.
   {
     ScopedTimer t(FMOE_TIMER_COMBINE, s, c.timers);
-    FMOE_HIP(launch_combine(y, L.y_dtype, c.residual, c.out, act_dtype, T, static_cast<int>(n_expert_used),
+    FMOE_HIP(launch_combine(y, y_dtype, c.residual, c.out, act_dtype, T, static_cast<int>(n_expert_used),
                             static_cast<int>(n_embd), down_split, L.y_part_elems, s));
   }
   return ok();

@@ -50,36 +50,52 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const T* __restrict__ 
   }
 }
 
-// V consecutive elements (V = 4: one 16-byte fp32 load per partial).
+// V consecutive elements (V = 4 or 8: 16-byte fp32 loads, 8- or 16-byte
+// bf16 loads).
 template <int V>
 __device__ __forceinline__ void ldv(const float* p, int64_t i, float* v) {
-  if constexpr (V == 4) {
-    const f32x4_t q = *reinterpret_cast<const f32x4_t*>(p + i);
-    v[0] = q[0], v[1] = q[1], v[2] = q[2], v[3] = q[3];
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < V / 4; ++c) {
+      const f32x4_t q = *reinterpret_cast<const f32x4_t*>(p + i + 4 * c);
+      v[4 * c] = q[0], v[4 * c + 1] = q[1], v[4 * c + 2] = q[2], v[4 * c + 3] = q[3];
+    }
   } else {
     v[0] = p[i];
   }
 }
+__device__ __forceinline__ void unpack_bf16x2(uint32_t q, float* v) {
+  v[0] = __uint_as_float(q << 16), v[1] = __uint_as_float(q & 0xFFFF0000u);
+}
 template <int V>
 __device__ __forceinline__ void ldv(const bf16_t* p, int64_t i, float* v) {
-  if constexpr (V == 4) {
+  if constexpr (V == 8) {
+    const u32x4_t q = *reinterpret_cast<const u32x4_t*>(p + i);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) unpack_bf16x2(q[c], v + 2 * c);
+  } else if constexpr (V == 4) {
     const u32x2_t q = *reinterpret_cast<const u32x2_t*>(p + i);
-    v[0] = __uint_as_float(q[0] << 16), v[1] = __uint_as_float(q[0] & 0xFFFF0000u);
-    v[2] = __uint_as_float(q[1] << 16), v[3] = __uint_as_float(q[1] & 0xFFFF0000u);
+    unpack_bf16x2(q[0], v), unpack_bf16x2(q[1], v + 2);
   } else {
     v[0] = bf16_to_f32(p[i]);
   }
 }
 template <int V>
 __device__ __forceinline__ void stv(float* p, int64_t i, const float* v) {
-  if constexpr (V == 4)
-    *reinterpret_cast<f32x4_t*>(p + i) = f32x4_t{v[0], v[1], v[2], v[3]};
-  else
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < V / 4; ++c)
+      *reinterpret_cast<f32x4_t*>(p + i + 4 * c) = f32x4_t{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+  } else {
     p[i] = v[0];
+  }
 }
 template <int V>
 __device__ __forceinline__ void stv(bf16_t* p, int64_t i, const float* v) {
-  if constexpr (V == 4)
+  if constexpr (V == 8)
+    *reinterpret_cast<u32x4_t*>(p + i) = u32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                 pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+  else if constexpr (V == 4)
     *reinterpret_cast<u32x2_t*>(p + i) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
   else
     p[i] = f32_to_bf16(v[0]);
@@ -284,37 +300,41 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kb_kernel(const bf16_t
   }
 }
 
-// combine_kernel with the slot count KS and the split count NS fixed, fp32
-// partials and 4-wide rows: all KS * NS loads of an element group are in
-// flight before the first add.  The adds run in the same order (splits,
-// then slots, then the residual), so the result is bit-identical.
-template <typename TO, int KS, int NS>
-__global__ __launch_bounds__(kThreads) void combine_fixed_kernel(const float* __restrict__ y, const TO* residual,
+// combine_kernel with the slot count KS and the split count NS fixed and
+// V-wide rows (fp32 partials: 4, bf16 partials: 8, one 16-byte load each):
+// all KS * NS loads of an element group are in flight before the first add.
+// The adds run in the same order (splits, then slots, then the residual), so
+// the result is bit-identical.
+template <typename TY, typename TO, int KS, int NS>
+__global__ __launch_bounds__(kThreads) void combine_fixed_kernel(const TY* __restrict__ y, const TO* residual,
                                                                  TO* out, int n_tokens, int n_embd,
                                                                  int64_t split_stride) {
+  constexpr int V = 16 / sizeof(TY);
   const int64_t total = static_cast<int64_t>(n_tokens) * n_embd;
-  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4; i < total;
-       i += static_cast<int64_t>(gridDim.x) * kThreads * 4) {
-    f32x4_t v[KS][NS];
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * V; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kThreads * V) {
+    float v[KS][NS][V];
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int q = 0; q < NS; ++q) v[s][q] = *reinterpret_cast<const f32x4_t*>(y + i + s * total + q * split_stride);
-    float acc[4], p[4];
+      for (int q = 0; q < NS; ++q) ldv<V>(y, i + s * total + q * split_stride, v[s][q]);
+    float acc[V], p[V];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      f32x4_t w = v[s][0];
 #pragma unroll
-      for (int q = 1; q < NS; ++q) w += v[s][q];
+      for (int j = 0; j < V; ++j) {
+        float w = v[s][0][j];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = s == 0 ? w[j] : acc[j] + w[j];
+        for (int q = 1; q < NS; ++q) w += v[s][q][j];
+        acc[j] = s == 0 ? w : acc[j] + w;
+      }
     }
     if (residual) {
-      ldv<4>(residual, i, p);
+      ldv<V>(residual, i, p);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = p[j] + acc[j];
+      for (int j = 0; j < V; ++j) acc[j] = p[j] + acc[j];
     }
-    stv<4>(out, i, acc);
+    stv<V>(out, i, acc);
   }
 }
 
@@ -429,23 +449,26 @@ void combine_t(const void* y, const void* residual, void* out, int n_tokens, int
                    reinterpret_cast<uintptr_t>(y) % (4 * sizeof(TY)) == 0 &&
                    reinterpret_cast<uintptr_t>(out) % (4 * sizeof(TO)) == 0 &&
                    reinterpret_cast<uintptr_t>(residual) % (4 * sizeof(TO)) == 0;
-  if constexpr (sizeof(TY) == 4) {
-    if (vec && k >= 1 && k <= 8 && nsplit >= 1 && nsplit <= 2) {
-      using Fn = void (*)(const float*, const TO*, TO*, int, int, int64_t);
-      static constexpr Fn table[8][2] = {
-          {combine_fixed_kernel<TO, 1, 1>, combine_fixed_kernel<TO, 1, 2>},
-          {combine_fixed_kernel<TO, 2, 1>, combine_fixed_kernel<TO, 2, 2>},
-          {combine_fixed_kernel<TO, 3, 1>, combine_fixed_kernel<TO, 3, 2>},
-          {combine_fixed_kernel<TO, 4, 1>, combine_fixed_kernel<TO, 4, 2>},
-          {combine_fixed_kernel<TO, 5, 1>, combine_fixed_kernel<TO, 5, 2>},
-          {combine_fixed_kernel<TO, 6, 1>, combine_fixed_kernel<TO, 6, 2>},
-          {combine_fixed_kernel<TO, 7, 1>, combine_fixed_kernel<TO, 7, 2>},
-          {combine_fixed_kernel<TO, 8, 1>, combine_fixed_kernel<TO, 8, 2>}};
-      hipLaunchKernelGGL(table[k - 1][nsplit - 1], dim3(grid_for(total / 4)), dim3(kThreads), 0, stream,
-                         static_cast<const float*>(y), static_cast<const TO*>(residual), static_cast<TO*>(out),
-                         n_tokens, n_embd, split_stride);
-      return;
-    }
+  // 16-byte partial loads: 4 fp32 or 8 bf16 per thread
+  constexpr int VF = 16 / sizeof(TY);
+  const bool vec16 = n_embd % VF == 0 && split_stride % VF == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % (VF * sizeof(TO)) == 0 &&
+                     reinterpret_cast<uintptr_t>(residual) % (VF * sizeof(TO)) == 0;
+  if (vec16 && k >= 1 && k <= 8 && nsplit >= 1 && nsplit <= 2) {
+    using Fn = void (*)(const TY*, const TO*, TO*, int, int, int64_t);
+    static constexpr Fn table[8][2] = {
+        {combine_fixed_kernel<TY, TO, 1, 1>, combine_fixed_kernel<TY, TO, 1, 2>},
+        {combine_fixed_kernel<TY, TO, 2, 1>, combine_fixed_kernel<TY, TO, 2, 2>},
+        {combine_fixed_kernel<TY, TO, 3, 1>, combine_fixed_kernel<TY, TO, 3, 2>},
+        {combine_fixed_kernel<TY, TO, 4, 1>, combine_fixed_kernel<TY, TO, 4, 2>},
+        {combine_fixed_kernel<TY, TO, 5, 1>, combine_fixed_kernel<TY, TO, 5, 2>},
+        {combine_fixed_kernel<TY, TO, 6, 1>, combine_fixed_kernel<TY, TO, 6, 2>},
+        {combine_fixed_kernel<TY, TO, 7, 1>, combine_fixed_kernel<TY, TO, 7, 2>},
+        {combine_fixed_kernel<TY, TO, 8, 1>, combine_fixed_kernel<TY, TO, 8, 2>}};
+    hipLaunchKernelGGL(table[k - 1][nsplit - 1], dim3(grid_for(total / VF)), dim3(kThreads), 0, stream,
+                       static_cast<const TY*>(y), static_cast<const TO*>(residual), static_cast<TO*>(out), n_tokens,
+                       n_embd, split_stride);
+    return;
   }
   if (vec)
     hipLaunchKernelGGL((combine_kernel<TY, TO, 4>), dim3(grid_for(total / 4)), dim3(kThreads), 0, stream,

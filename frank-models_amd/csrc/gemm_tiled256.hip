@@ -119,7 +119,7 @@ __device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, i
 // finished values to LDS (row pitch = row bytes + 16), barrier, then the
 // block stores them row by row.  SwiGLU rows go to h in expert-sorted order
 // (row p); the scatter epilogues write row order[p], times the routing
-// weight for EPI_SCATTER_WEIGHTED, and fp32 K-split partials at
+// weight for EPI_SCATTER_WEIGHTED, and K-split partials (fp32 or bf16) at
 // split * split_stride.  The scatter epilogues first load the tile's
 // order[p] and routing weights once into an LDS table behind the staging
 // rows, so each pass waits on no global load.  fp32 outputs take the weight
@@ -221,7 +221,7 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
         v = __builtin_bit_cast(u32x4_t, __builtin_bit_cast(f32x4_t, v) * t_w[r]);
       const int64_t row = kScatter ? static_cast<int64_t>(t_order[r]) : static_cast<int64_t>(ti.row0 + r);
       const int64_t elem = !kScatter && g.out_kb_rows ? kb_offset(row, col, g.out_kb_rows)
-                                                      : (OUT_F32 ? split * g.split_stride : 0) + row * g.ldo + col;
+                                                      : split * g.split_stride + row * g.ldo + col;
       unsigned char* out = static_cast<unsigned char*>(g.out) + elem * kEsz;
       *reinterpret_cast<u32x4_t*>(out) = v;
     }
@@ -692,8 +692,8 @@ hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
 int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
   // Split K in two when the tiles would fill the 256 CUs fewer than ~4 times
   // (the down projection at Mixtral shapes: 4096 outputs, 14336 inputs) and
-  // the caller provided room for fp32 partials.
-  if (g.epi != EPI_SCATTER_WEIGHTED || g.out_dtype != DT_F32 || g.split_stride == 0) return 1;
+  // the caller provided room for the partials (fp32 or bf16).
+  if (g.epi != EPI_SCATTER_WEIGHTED || g.split_stride == 0) return 1;
   const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
   const int64_t tiles = static_cast<int64_t>(row_tiles) * ((g.N + kBN - 1) / kBN);
   // (Three splits were measured too: the extra fp32 partial traffic and
@@ -717,7 +717,7 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
     return false;
   // the epilogue stores 16-byte chunks: 8 bf16 or 4 fp32 outputs
   const bool out_f32 = g.epi != EPI_SWIGLU && g.out_dtype == DT_F32;
-  if ((!out_f32 && g.ldo % 8) || (out_f32 && g.split_stride % 4)) return false;
+  if ((!out_f32 && (g.ldo % 8 || g.split_stride % 8)) || (out_f32 && g.split_stride % 4)) return false;
   if (g.w_dtype == DT_F8 && (!g.s0 || (g.epi == EPI_SWIGLU && !g.s1))) return false;
   // 32-bit byte offsets of A rows
   const int64_t a_rows = g.a_mode == A_GATHER_TOKEN ? g.n_tokens : g.n_assign;

@@ -200,7 +200,10 @@ int fmoe_mul_mat_id(const void *packed_w, const float *w_scales, int w_dtype,
  *   packed_up / packed_gate ([n_ff, n_embd] per expert) and packed_down
  *   ([n_embd, n_ff] per expert) in w_dtype, with scales when w_dtype is
  *   F8E4M3FN.  SwiGLU is gate * silu(up).  Weighted expert outputs are summed
- *   in slot order.  Workspace: fmoe_moe_ffn_block_workspace_bytes. */
+ *   in slot order.  Dot products accumulate in fp32; with BF16 activations
+ *   the SwiGLU rows, and at prefill sizes the weighted expert outputs, are
+ *   held in bf16 between kernels (the sum over slots runs in fp32).
+ *   Workspace: fmoe_moe_ffn_block_workspace_bytes. */
 size_t fmoe_moe_ffn_block_workspace_bytes(int64_t n_tokens, int64_t n_expert,
                                           int64_t n_expert_used, int64_t n_embd,
                                           int64_t n_ff, int act_dtype, int w_dtype);
