@@ -331,6 +331,125 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
                                     kMfmaWaves);
 }
 
+// ---- Prefill logits for 32 < n_expert <= 128 (bf16, n_embd % 128 == 0,
+// k <= 16): one 512-thread block per kTileTok = 32 tokens.  The block reads
+// its token rows and the router matrix once each, staged through LDS by
+// global_load_lds in stages of 128 hidden columns (a 3-deep ring, two stages
+// in flight): 2 token tiles x 4 steps of 32 and NCP expert chunks x 4 steps,
+// each a 1 KiB block in MFMA lane order (lane l: row l % 16, columns
+// 8 (l / 16) .. +8 of the step).  Wave w owns expert chunk w % NCP and
+// 2 NCP / 8 token tiles, so no partial logits cross waves.  The 16-token
+// kernel above reads the whole router matrix per 16 tokens (at 128 experts
+// and 2048 columns, 512 KiB for 64 KiB of token rows).
+constexpr int kTileTok = 32;
+constexpr int kTileCols = 128;
+constexpr int kTileRing = 3;
+
+template <int NCP>
+constexpr int tile_stage_bytes() {
+  return (kTileTok / 16 + NCP) * 4 * 1024;
+}
+
+// One wave's loads of stage st: its blocks wave, wave + 8, ... into the
+// stage's ring buffer.
+template <int NPW>
+__device__ __forceinline__ void tile_issue(const bf16_t* const (&src)[NPW], unsigned char* smem, int st, int wave,
+                                           int stage_bytes) {
+  unsigned char* dst = smem + (st % kTileRing) * stage_bytes;
+#pragma unroll
+  for (int j = 0; j < NPW; ++j)
+    __builtin_amdgcn_global_load_lds(src[j] + st * kTileCols, dst + (wave + 8 * j) * 1024, 16, 0, 0);
+}
+
+template <int NCP>
+__global__ __launch_bounds__(512) void router_tile_bf16_kernel(const bf16_t* __restrict__ x,
+                                                               const bf16_t* __restrict__ wr, int n_tokens,
+                                                               int n_embd, int n_expert, int k, int normalize,
+                                                               int* __restrict__ ids, float* __restrict__ weights) {
+  static_assert(NCP == 4 || NCP == 8, "8 waves over NCP expert chunks x 2 token tiles");
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int kTT = kTileTok / 16;          // token tiles
+  constexpr int kTTW = kTT * NCP / 8;         // token tiles per wave
+  constexpr int kStage = tile_stage_bytes<NCP>();
+  constexpr int kBlocks = (kTT + NCP) * 4;    // 1 KiB blocks per stage
+  constexpr int kPerWave = kBlocks / 8;       // loads per wave per stage
+  static_assert(kBlocks % 8 == 0, "stage blocks split evenly over 8 waves");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int tok0 = blockIdx.x * kTileTok;
+  const int chunk = wave % NCP;
+  const int tt0 = (wave / NCP) * kTTW;
+  const int r16 = lane & 15;
+  const int kofs = 8 * (lane >> 4);
+
+  // This wave's share of a stage: blocks wave, wave + 8, ...  Block b < 4 kTT
+  // is token tile b / 4, step b % 4; the rest are expert chunk (b - 4 kTT) / 4.
+  // Rows past the batch or the expert count read the last valid row (their
+  // logits are never used).
+  const bf16_t* src[kPerWave];
+#pragma unroll
+  for (int j = 0; j < kPerWave; ++j) {
+    const int b = wave + 8 * j;
+    if (b < 4 * kTT) {
+      const int t = min(tok0 + (b >> 2) * 16 + r16, n_tokens - 1);
+      src[j] = x + static_cast<int64_t>(t) * n_embd + (b & 3) * 32 + kofs;
+    } else {
+      const int bb = b - 4 * kTT;
+      const int e = min((bb >> 2) * 16 + r16, n_expert - 1);
+      src[j] = wr + static_cast<int64_t>(e) * n_embd + (bb & 3) * 32 + kofs;
+    }
+  }
+
+  f32x4_t acc[kTTW];
+#pragma unroll
+  for (int q = 0; q < kTTW; ++q) acc[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int n_st = n_embd / kTileCols;
+  tile_issue<kPerWave>(src, smem, 0, wave, kStage);
+  if (n_st > 1) tile_issue<kPerWave>(src, smem, 1, wave, kStage);
+  for (int st = 0; st < n_st; ++st) {
+    // Stage st + 2 refills the buffer of stage st - 1, released by the
+    // barrier that ended the last iteration.
+    if (st + 2 < n_st) {
+      tile_issue<kPerWave>(src, smem, st + 2, wave, kStage);
+      __builtin_amdgcn_s_waitcnt(wait_vm(2 * kPerWave, false));
+    } else if (st + 1 < n_st) {
+      __builtin_amdgcn_s_waitcnt(wait_vm(kPerWave, false));
+    } else {
+      __builtin_amdgcn_s_waitcnt(wait_vm(0, false));
+    }
+    asm volatile("s_barrier" ::: "memory");
+    const unsigned char* cur = smem + (st % kTileRing) * kStage;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4_t b = *reinterpret_cast<const u32x4_t*>(cur + ((4 * kTT + chunk * 4 + s) * 1024) + lane * 16);
+#pragma unroll
+      for (int q = 0; q < kTTW; ++q) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(cur + (((tt0 + q) * 4 + s) * 1024) + lane * 16);
+        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                         __builtin_bit_cast(bf16x8_t, b), acc[q], 0, 0, 0);
+      }
+    }
+    // This buffer's reads are done before it is refilled (no wait on the
+    // stages still in flight).
+    __builtin_amdgcn_s_waitcnt(wait_vm(63, true));
+    asm volatile("s_barrier" ::: "memory");
+  }
+  __builtin_amdgcn_s_waitcnt(wait_vm(0, true));
+  // D[token][expert]: the lane holds expert r16 of its chunk, tokens
+  // 4 (lane / 16) + i of each of its tiles.  The logits overwrite the ring.
+  constexpr int ld = NCP * 16 + 1;
+  float* logits = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int q = 0; q < kTTW; ++q)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) logits[((tt0 + q) * 16 + 4 * (lane >> 4) + i) * ld + chunk * 16 + r16] = acc[q][i];
+  __syncthreads();
+  for (int g = wave; g < kTileTok / 4; g += 8) {
+    if (tok0 + 4 * g >= n_tokens) break;
+    softmax_topk4<NCP>(logits + 4 * g * ld, ld, tok0 + 4 * g, n_tokens, n_expert, k, normalize != 0, ids, weights);
+  }
+}
+
 // ---- Decode-sized batches (T <= kDecodeMaxTokens, bf16, k <= 16,
 // n_expert <= 256): the logits are split over many blocks instead of
 // streaming the whole router matrix through one CU, and one block finishes
@@ -457,6 +576,17 @@ hipError_t launch_topk_permute(const float* part, int n_split, int n_tokens, int
   return hipGetLastError();
 }
 
+template <int NCP>
+void launch_router_tile(const bf16_t* x, const bf16_t* wr, int n_tokens, int n_embd, int n_expert, int k,
+                        bool normalize, int* ids, float* weights, hipStream_t stream) {
+  constexpr int lds = kTileRing * tile_stage_bytes<NCP>();
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(router_tile_bf16_kernel<NCP>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)attr;
+  hipLaunchKernelGGL((router_tile_bf16_kernel<NCP>), dim3((n_tokens + kTileTok - 1) / kTileTok), dim3(512), lds,
+                     stream, x, wr, n_tokens, n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
+}
+
 }  // namespace
 
 hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert,
@@ -467,7 +597,15 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
   const dim3 grid((n_tokens + kTok - 1) / kTok);
   const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(wr) % 16 == 0);
-  if (dtype == DT_BF16 && n_embd % 32 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
+  if (dtype == DT_BF16 && n_embd % kTileCols == 0 && n_expert > 32 && n_expert <= kMfmaMaxExpert && k <= 16 &&
+      aligned) {
+    if (n_expert <= 64)
+      launch_router_tile<4>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd, n_expert,
+                            k, normalize, ids, weights, stream);
+    else
+      launch_router_tile<8>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd, n_expert,
+                            k, normalize, ids, weights, stream);
+  } else if (dtype == DT_BF16 && n_embd % 32 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
     const int ld = ((n_expert + 15) / 16) * 16 + 1;
     const size_t lds = static_cast<size_t>(kMfmaWaves + 1) * kTok * ld * sizeof(float);
     static const bool configured = [] {

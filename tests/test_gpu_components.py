@@ -132,10 +132,12 @@ def test_router_wide(fm, wl, E, k, H, T):
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
 
 
-def test_router_wide_ties_lower_index(fm):
+# H = 64 takes the 16-token MFMA kernel, H = 128 the 32-token tile kernel.
+@pytest.mark.parametrize("H", [64, 128])
+def test_router_wide_ties_lower_index(fm, H):
     # one-hot rows over a large batch: token t's logits are router column
     # t % 3, exactly
-    E, H, T = 48, 64, 300
+    E, T = 48, 300
     wr = np.zeros((E, H), np.float32)
     wr[[7, 20, 33], 0] = 5.0   # three-way tie at the top
     wr[[41, 40], 2] = 1.0      # two-way tie; column 1 is all equal
@@ -166,13 +168,14 @@ def test_router_ties_lower_index(fm):
 
 # Logits one ulp apart have one fp32 probability: the selection runs on the
 # probabilities (lower expert index first), on every router kernel: the SIMT
-# kernel (fp32), the MFMA kernel (bf16, T > 64), the decode pair (bf16,
+# kernel (fp32), the MFMA kernels (bf16, T > 64: 16 tokens per block, or 32
+# for 33..128 experts with n_embd % 128 == 0), the decode pair (bf16,
 # T <= 64), and the one-token-per-wave top-k (k > 16).
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("T", [1, 16, 100])
-@pytest.mark.parametrize("E,k", [(8, 3), (40, 18)])
-def test_router_ulp_apart_logits(fm, dt, T, E, k):
-    x, wr = ulp_tie_router_inputs(E, 64, T)
+@pytest.mark.parametrize("E,k,H", [(8, 3, 64), (40, 18, 64), (40, 3, 128), (128, 8, 256)])
+def test_router_ulp_apart_logits(fm, dt, T, E, k, H):
+    x, wr = ulp_tie_router_inputs(E, H, T)
     want, want_w = om.router(x, wr, k, False, dtype=np.float32)
     assert list(want[:3, 0]) == [2, 5, 0]
     for norm in (False, True):
