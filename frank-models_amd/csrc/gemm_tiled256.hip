@@ -111,6 +111,80 @@ __device__ __forceinline__ bool logical_tile(int n_row_tiles, int n_col_tiles, i
   return true;
 }
 
+// ---- The same order over the actual row tiles (up to kSchedExperts
+// experts): ceil(count / 256) per expert, counted from the offsets, so the
+// XCDs split the real tiles evenly.  The grid is sized for the upper bound
+// (every expert with a partial tile); with a skewed routing (Qwen3-like,
+// 128 experts with Zipf counts: 355 real of 384 bounded row tiles at 8192
+// tokens) the bound-sized ranges left whole XCDs short of work.  (Cutting
+// the ranges at equal estimated cost, partial tiles weighted by their
+// MFMA share, measured slower than equal counts: a partial tile streams
+// its whole weight slab.)
+constexpr int kSchedChunks = 4;                 // experts per lane
+constexpr int kSchedExperts = 64 * kSchedChunks;
+
+// v of expert e (wave-uniform e), from the lane and chunk that hold it.
+__device__ __forceinline__ int sched_get(const int (&v)[kSchedChunks], int e) {
+  const int c = e / kWave;
+  int x = v[0];
+#pragma unroll
+  for (int i = 1; i < kSchedChunks; ++i)
+    if (c == i) x = v[i];
+  return __builtin_amdgcn_readfirstlane(__shfl(x, e % kWave, kWave));
+}
+
+// This block's tile: false when the block has none.
+__device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, TileInfo* ti, int* col_tile,
+                                           int* split) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int E = g.n_expert;
+  const int nch = (E + kWave - 1) / kWave;
+  // Per lane and chunk c, expert 64 c + lane: first row, rows, row tiles before it.
+  int off[kSchedChunks], cnt[kSchedChunks], tp[kSchedChunks];
+  int R = 0;
+#pragma unroll
+  for (int c = 0; c < kSchedChunks; ++c) {
+    off[c] = cnt[c] = tp[c] = 0;
+    if (c < nch) {
+      const int e = c * kWave + lane;
+      off[c] = e < E ? g.offsets[e] : 0;
+      cnt[c] = e < E ? g.offsets[e + 1] - off[c] : 0;
+      const int nt = (cnt[c] + kBM - 1) / kBM;
+      const int incl = wave_inclusive_scan(nt);
+      tp[c] = R + incl - nt;
+      R += __shfl(incl, kWave - 1, kWave);
+    }
+  }
+  const int tiles_split = R * n_col;
+  const int total = tiles_split * g.ksplit;
+  const int per = (total + 7) / 8;
+  const int b = static_cast<int>(blockIdx.x);
+  if (b / 8 >= per) return false;
+  const int L = (b % 8) * per + b / 8;
+  if (L >= total) return false;
+  const int sp = L / tiles_split;
+  const int l = L - sp * tiles_split;
+  const int group_span = kGroupN * R;
+  const int grp = l / group_span;
+  const int within = l - grp * group_span;
+  const int cig = min(kGroupN, n_col - grp * kGroupN);
+  const int r = within / cig;
+  // the expert of row tile r: the last one whose tiles start at or before r
+  // (an expert with no rows shares its start with the next one)
+  int n = 0;
+#pragma unroll
+  for (int c = 0; c < kSchedChunks; ++c)
+    if (c < nch) n += __popcll(__ballot(c * kWave + lane < E && tp[c] <= r));
+  const int e = n - 1;
+  const int local = r - sched_get(tp, e);
+  ti->expert = __builtin_amdgcn_readfirstlane(e);
+  ti->row0 = __builtin_amdgcn_readfirstlane(sched_get(off, e) + local * kBM);
+  ti->rows = __builtin_amdgcn_readfirstlane(min(kBM, sched_get(cnt, e) - local * kBM));
+  *col_tile = __builtin_amdgcn_readfirstlane(grp * kGroupN + within % cig);
+  *split = __builtin_amdgcn_readfirstlane(sp);
+  return true;
+}
+
 // The epilogue, staged through LDS so that every global store writes whole
 // contiguous output rows (16 bytes per lane, 256 B - 1 KiB per row) instead
 // of 16 rows x 32-64 B.  The lane holds assignment row (lane & 15) of each
@@ -547,10 +621,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
                                                                      int n_col_tiles) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
 
-  int row_tile, col_tile, split;
-  if (!logical_tile(n_row_tiles, n_col_tiles, g.ksplit, &row_tile, &col_tile, &split)) return;
+  int col_tile, split;
   TileInfo ti;
-  if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
+  if (g.n_expert <= kSchedExperts && static_cast<int64_t>(n_row_tiles) * n_col_tiles * g.ksplit < INT32_MAX) {
+    if (!sched_tile(g, n_col_tiles, &ti, &col_tile, &split)) return;
+  } else {
+    int row_tile;
+    if (!logical_tile(n_row_tiles, n_col_tiles, g.ksplit, &row_tile, &col_tile, &split)) return;
+    if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
