@@ -133,38 +133,44 @@ __device__ __forceinline__ int sched_get(const int (&v)[kSchedChunks], int e) {
   return __builtin_amdgcn_readfirstlane(__shfl(x, e % kWave, kWave));
 }
 
-// This block's tile: false when the block has none.
-__device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, TileInfo* ti, int* col_tile,
-                                           int* split) {
+// The actual row tiles: R, and per lane and chunk c (expert 64 c + lane)
+// its first row, rows and the row tiles before it.
+struct SchedTables {
+  int off[kSchedChunks], cnt[kSchedChunks], tp[kSchedChunks];
+  int R;
+};
+
+__device__ __forceinline__ void sched_tables(const GroupedGemmArgs& g, SchedTables& t) {
   const int lane = threadIdx.x & (kWave - 1);
   const int E = g.n_expert;
   const int nch = (E + kWave - 1) / kWave;
-  // Per lane and chunk c, expert 64 c + lane: first row, rows, row tiles before it.
-  int off[kSchedChunks], cnt[kSchedChunks], tp[kSchedChunks];
-  int R = 0;
+  t.R = 0;
 #pragma unroll
   for (int c = 0; c < kSchedChunks; ++c) {
-    off[c] = cnt[c] = tp[c] = 0;
+    t.off[c] = t.cnt[c] = t.tp[c] = 0;
     if (c < nch) {
       const int e = c * kWave + lane;
-      off[c] = e < E ? g.offsets[e] : 0;
-      cnt[c] = e < E ? g.offsets[e + 1] - off[c] : 0;
-      const int nt = (cnt[c] + kBM - 1) / kBM;
+      t.off[c] = e < E ? g.offsets[e] : 0;
+      t.cnt[c] = e < E ? g.offsets[e + 1] - t.off[c] : 0;
+      const int nt = (t.cnt[c] + kBM - 1) / kBM;
       const int incl = wave_inclusive_scan(nt);
-      tp[c] = R + incl - nt;
-      R += __shfl(incl, kWave - 1, kWave);
+      t.tp[c] = t.R + incl - nt;
+      t.R += __shfl(incl, kWave - 1, kWave);
     }
   }
-  const int tiles_split = R * n_col;
-  const int total = tiles_split * g.ksplit;
-  const int per = (total + 7) / 8;
-  const int b = static_cast<int>(blockIdx.x);
-  if (b / 8 >= per) return false;
-  const int L = (b % 8) * per + b / 8;
-  if (L >= total) return false;
+  t.R = __builtin_amdgcn_readfirstlane(t.R);
+}
+
+// Logical tile L (< R * n_col * ksplit) -> its rows, column tile and split.
+__device__ __forceinline__ void sched_decode(const GroupedGemmArgs& g, const SchedTables& t, int n_col, int L,
+                                             TileInfo* ti, int* col_tile, int* split) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int E = g.n_expert;
+  const int nch = (E + kWave - 1) / kWave;
+  const int tiles_split = t.R * n_col;
   const int sp = L / tiles_split;
   const int l = L - sp * tiles_split;
-  const int group_span = kGroupN * R;
+  const int group_span = kGroupN * t.R;
   const int grp = l / group_span;
   const int within = l - grp * group_span;
   const int cig = min(kGroupN, n_col - grp * kGroupN);
@@ -174,14 +180,36 @@ __device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, 
   int n = 0;
 #pragma unroll
   for (int c = 0; c < kSchedChunks; ++c)
-    if (c < nch) n += __popcll(__ballot(c * kWave + lane < E && tp[c] <= r));
+    if (c < nch) n += __popcll(__ballot(c * kWave + lane < E && t.tp[c] <= r));
   const int e = n - 1;
-  const int local = r - sched_get(tp, e);
+  const int local = r - sched_get(t.tp, e);
   ti->expert = __builtin_amdgcn_readfirstlane(e);
-  ti->row0 = __builtin_amdgcn_readfirstlane(sched_get(off, e) + local * kBM);
-  ti->rows = __builtin_amdgcn_readfirstlane(min(kBM, sched_get(cnt, e) - local * kBM));
+  ti->row0 = __builtin_amdgcn_readfirstlane(sched_get(t.off, e) + local * kBM);
+  ti->rows = __builtin_amdgcn_readfirstlane(min(kBM, sched_get(t.cnt, e) - local * kBM));
   *col_tile = __builtin_amdgcn_readfirstlane(grp * kGroupN + within % cig);
   *split = __builtin_amdgcn_readfirstlane(sp);
+}
+
+// XCD x's range [lo, hi) of the logical order: ceil(total / 8) tiles each.
+__device__ __forceinline__ void sched_range(const GroupedGemmArgs& g, const SchedTables& t, int n_col, int* lo,
+                                            int* hi) {
+  const int total = t.R * n_col * g.ksplit;
+  const int per = (total + 7) / 8;
+  const int x = static_cast<int>(blockIdx.x % 8);
+  *lo = min(x * per, total);
+  *hi = min(*lo + per, total);
+}
+
+// This block's tile (one tile per block): false when the block has none.
+__device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, TileInfo* ti, int* col_tile,
+                                           int* split) {
+  SchedTables t;
+  sched_tables(g, t);
+  int lo, hi;
+  sched_range(g, t, n_col, &lo, &hi);
+  const int L = lo + static_cast<int>(blockIdx.x / 8);
+  if (L >= hi) return false;
+  sched_decode(g, t, n_col, L, ti, col_tile, split);
   return true;
 }
 
@@ -222,7 +250,7 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
       o = g.order[ti.row0 + t];
       if (kWeighted) w = g.route_w[o];
     }
-    __syncthreads();  // the ring is no longer read
+    lds_barrier();  // the ring is no longer read
     if (t < kBM) {
       t_order[t] = o;
       if (kWeighted) t_w[t] = w;
@@ -251,7 +279,7 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
   }
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
-    __syncthreads();  // the ring (or the last pass's rows) is no longer read
+    lds_barrier();  // the ring (or the last pass's rows) is no longer read
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * pass + mm;
@@ -274,7 +302,7 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
           *reinterpret_cast<u32x2_t*>(dst + n * 16 * 2) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int i = 0; i < 128 * kChunks / kThreads; ++i) {
       const int id = i * kThreads + static_cast<int>(threadIdx.x);
@@ -386,20 +414,32 @@ __device__ __forceinline__ void multiply2(f32x4_t (&acc)[8][4], const u32x4_t (&
   }
 }
 
+// The loop's prologue loads: this group's stages (1 - G and 3 - G) that lie
+// in [s_lo, s_hi), each into the buffer of its own index.
+template <int NSETS>
+__device__ __forceinline__ void k_issue_range(const WaveCtx& c, int s_lo, int s_hi) {
+  const int G = c.wave >> 2;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int st = 2 * i + 1 - G;
+    if (st >= s_lo && st < s_hi && st < c.KT) issue_full_stage<NSETS>(c, st, st);
+  }
+}
+
+// The K loop after its prologue loads were issued (k_issue_range over
+// stages 0..3).  With more than two stages the last load a group issued is
+// its stage 3 - G, so vmcnt(8) leaves its first stage complete.
 template <int NM, int NSETS, int G, bool A8>
-__device__ __forceinline__ void k_loop(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
+__device__ __forceinline__ void k_body(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
   constexpr int R = kRing;
   const int KT = c.KT;  // even
   const int JT = KT >> 1;
   u32x4_t fa[2][4], fb[2][8];
   const bool two = KT > 2;
-  issue_full_stage<NSETS>(c, 1 - G, 1 - G);
-  if (two) {
-    issue_full_stage<NSETS>(c, 3 - G, 3 - G);
+  if (two)
     __builtin_amdgcn_s_waitcnt(wait_vm(8, false));
-  } else {
+  else
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  }
   asm volatile("s_barrier" ::: "memory");
   if constexpr (G == 0) {
     if constexpr (NM > 0) {
@@ -614,27 +654,19 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
 
-// F8: e4m3 weights.  A8 (with F8): e4m3 activations too, K-blocked in
-// 64-input pieces, on the bf16 loop's ring with 64-input stages.
-template <int EPI, int NSETS, bool F8, bool A8>
-__global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmArgs g, int n_row_tiles,
-                                                                     int n_col_tiles) {
-  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
-
-  int col_tile, split;
-  TileInfo ti;
-  if (g.n_expert <= kSchedExperts && static_cast<int64_t>(n_row_tiles) * n_col_tiles * g.ksplit < INT32_MAX) {
-    if (!sched_tile(g, n_col_tiles, &ti, &col_tile, &split)) return;
-  } else {
-    int row_tile;
-    if (!logical_tile(n_row_tiles, n_col_tiles, g.ksplit, &row_tile, &col_tile, &split)) return;
-    if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
-  }
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1;  // 16-row groups wm, wm+4, wm+8, wm+12
-  const int wn = wave & 1;   // weight rows of each set: wn half
+// Stage sources of tile (ti, col_tile, split) for this wave.  A stage is
+// staged in 8 shares; share w holds token rows (w*2 + j)*16 + (lane >> 2),
+// 16-byte physical chunk (lane & 3), which holds logical chunk
+// (lane & 3) ^ ((lane >> 3) & 3), and weight row blocks w*2 + j.  Each wave
+// keeps the addresses of its own share (j = 0, 1) and of share wave ^ 4
+// (j = 2, 3): the bf16 loop has one group load a whole stage, the fp8 loop
+// has every wave load its own share.  Rows past the tile re-read its first
+// row.  Byte offsets from the A base fit 32 bits (checked on the host).  A
+// K-blocked A operand keeps each 32-input block of the tile's rows in one
+// contiguous run.
+template <int NSETS, bool F8, bool A8>
+__device__ __forceinline__ WaveCtx tile_ctx(const GroupedGemmArgs& g, const TileInfo& ti, int col_tile, int split,
+                                            unsigned char* lds, int lane, int wave) {
   const int64_t N = g.N, K = g.K;
   const int64_t n0 = static_cast<int64_t>(col_tile) * (kBN / NSETS);
   const int64_t nblocks = N / 16;
@@ -645,16 +677,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   // down to even (the bf16 loop runs two stages per trip).
   const int k_first = split_boundary(static_cast<int>(kblocks), g.ksplit, split);
   const int KT = split_boundary(static_cast<int>(kblocks), g.ksplit, split + 1) - k_first;
-
-  // ---- global -> LDS sources.  A stage is staged in 8 shares; share w
-  // holds token rows (w*2 + j)*16 + (lane >> 2), 16-byte physical chunk
-  // (lane & 3), which holds logical chunk (lane & 3) ^ ((lane >> 3) & 3), and
-  // weight row blocks w*2 + j.  Each wave keeps the addresses of its own
-  // share (j = 0, 1) and of share wave ^ 4 (j = 2, 3): the bf16 loop has one
-  // group load a whole stage, the fp8 loop has every wave load its own share.
-  // Rows past the tile re-read its first row.  Byte offsets from the A base
-  // fit 32 bits (checked on the host).  A K-blocked A operand keeps each
-  // 32-input block of the tile's rows in one contiguous run.
   WaveCtx c;
   c.lds = lds;
   c.a_base = static_cast<const unsigned char*>(g.a);
@@ -687,9 +709,61 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   // (the XOR swizzle depends only on the row within the group).
   c.a_lane = (lane & 15) * 64 + ((((lane >> 4) ^ (((lane & 15) >> 1) & 3))) << 4);
   c.wave = wave;
-  c.wm = wm;
-  c.wn = wn;
+  c.wm = wave >> 1;  // 16-row groups wm, wm+4, wm+8, wm+12
+  c.wn = wave & 1;   // weight rows of each set: wn half
   c.KT = KT;
+  return c;
+}
+
+// The bf16 / fp8-activation K loop of a tile with `rows` rows, after its
+// prologue loads.  Active 16-row groups of this wave: groups wm, wm+4, wm+8,
+// wm+12 below ceil(rows / 16).  Wave-uniform, so each wave runs one
+// specialisation; the two ping-pong groups run mirrored loops.
+template <int NSETS, bool A8>
+__device__ __forceinline__ void run_k_body(const WaveCtx& c, f32x4_t (&acc)[8][4], int rows) {
+  const int groups = (rows + 15) >> 4;
+  const int nm = groups > c.wm ? min(4, (groups - c.wm + 3) >> 2) : 0;
+  if (c.wave < 4) {
+    switch (nm) {
+      case 4: k_body<4, NSETS, 0, A8>(c, acc); break;
+      case 3: k_body<3, NSETS, 0, A8>(c, acc); break;
+      case 2: k_body<2, NSETS, 0, A8>(c, acc); break;
+      case 1: k_body<1, NSETS, 0, A8>(c, acc); break;
+      default: k_body<0, NSETS, 0, A8>(c, acc); break;
+    }
+  } else {
+    switch (nm) {
+      case 4: k_body<4, NSETS, 1, A8>(c, acc); break;
+      case 3: k_body<3, NSETS, 1, A8>(c, acc); break;
+      case 2: k_body<2, NSETS, 1, A8>(c, acc); break;
+      case 1: k_body<1, NSETS, 1, A8>(c, acc); break;
+      default: k_body<0, NSETS, 1, A8>(c, acc); break;
+    }
+  }
+}
+
+// F8: e4m3 weights.  A8 (with F8): e4m3 activations too, K-blocked in
+// 64-input pieces, on the bf16 loop's ring with 64-input stages.  One tile
+// per block.
+template <int EPI, int NSETS, bool F8, bool A8>
+__global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmArgs g, int n_row_tiles,
+                                                                     int n_col_tiles) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+
+  int col_tile, split;
+  TileInfo ti;
+  if (g.n_expert <= kSchedExperts && static_cast<int64_t>(n_row_tiles) * n_col_tiles * g.ksplit < INT32_MAX) {
+    if (!sched_tile(g, n_col_tiles, &ti, &col_tile, &split)) return;
+  } else {
+    int row_tile;
+    if (!logical_tile(n_row_tiles, n_col_tiles, g.ksplit, &row_tile, &col_tile, &split)) return;
+    if (!find_tile(g.offsets, g.n_expert, kBM, row_tile, &ti)) return;
+  }
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const WaveCtx c = tile_ctx<NSETS, F8, A8>(g, ti, col_tile, split, lds, lane, wave);
+  const int64_t n0 = static_cast<int64_t>(col_tile) * (kBN / NSETS);
 
   f32x4_t acc[8][4];
 #pragma unroll
@@ -697,11 +771,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 #pragma unroll
     for (int m = 0; m < 4; ++m) acc[n][m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Active 16-row groups of this wave: groups wm, wm+4, wm+8, wm+12 below
-  // ceil(rows / 16).  Wave-uniform, so each wave runs one specialisation.
-  const int groups = (ti.rows + 15) >> 4;
-  const int nm = groups > wm ? min(4, (groups - wm + 3) >> 2) : 0;
   if constexpr (F8 && !A8) {
+    const int groups = (ti.rows + 15) >> 4;
+    const int nm = groups > c.wm ? min(4, (groups - c.wm + 3) >> 2) : 0;
     if (wave < 4) {
       switch (nm) {
         case 4: k_loop_f8<4, NSETS, 0>(c, acc); break;
@@ -720,31 +792,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
       }
     }
   } else {
-    if (wave < 4) {  // the two ping-pong groups run mirrored loops
-      switch (nm) {
-        case 4: k_loop<4, NSETS, 0, A8>(c, acc); break;
-        case 3: k_loop<3, NSETS, 0, A8>(c, acc); break;
-        case 2: k_loop<2, NSETS, 0, A8>(c, acc); break;
-        case 1: k_loop<1, NSETS, 0, A8>(c, acc); break;
-        default: k_loop<0, NSETS, 0, A8>(c, acc); break;
-      }
-    } else {
-      switch (nm) {
-        case 4: k_loop<4, NSETS, 1, A8>(c, acc); break;
-        case 3: k_loop<3, NSETS, 1, A8>(c, acc); break;
-        case 2: k_loop<2, NSETS, 1, A8>(c, acc); break;
-        case 1: k_loop<1, NSETS, 1, A8>(c, acc); break;
-        default: k_loop<0, NSETS, 1, A8>(c, acc); break;
-      }
-    }
+    k_issue_range<NSETS>(c, 0, 4);
+    run_k_body<NSETS, A8>(c, acc, ti.rows);
   }
 
   if constexpr (EPI == EPI_SWIGLU)
-    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc);
   else if (g.out_dtype == DT_F32)
-    epilogue<EPI, NSETS, F8, A8, true>(g, ti, split, n0, wm, wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, true>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc);
   else
-    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, wm, wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc);
 }
 
 template <int EPI, int NSETS, bool F8, bool A8>
