@@ -223,14 +223,41 @@ __device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, 
 // (row p); the scatter epilogues write row order[p], times the routing
 // weight for EPI_SCATTER_WEIGHTED, and K-split partials (fp32 or bf16) at
 // split * split_stride.  The scatter epilogues first load the tile's
-// order[p] and routing weights once into an LDS table behind the staging
-// rows, so each pass waits on no global load.  fp32 outputs take the weight
+// order[p] (loaded before the K loop) and routing weights once into an LDS
+// table behind the staging rows, so each pass waits on no global load.  fp32 outputs take the weight
 // as they are read back, bf16 outputs before rounding (the same fp32
 // product either way).  fp8 weights: the per-output-channel scale
 // multiplies the fp32 dot product.
+// What the scatter epilogues read from global memory per row of the tile:
+// the destination order[p] of row `threadIdx.x`, loaded before the
+// prologue's stage loads (its round trip overlaps theirs), and the routing
+// weight route_w[order[p]], loaded after the K loop (waiting for order
+// before it would wait for the stage loads issued after it).
+struct EpiRows {
+  int o = 0;
+  float w = 1.f;
+  bool have_w = false;
+};
+
+template <int EPI>
+__device__ __forceinline__ void epi_rows_first(const GroupedGemmArgs& g, const TileInfo& ti, EpiRows& er) {
+  if constexpr (EPI != EPI_SWIGLU) {
+    if (static_cast<int>(threadIdx.x) < ti.rows) er.o = g.order[ti.row0 + threadIdx.x];
+  }
+}
+
+template <int EPI>
+__device__ __forceinline__ void epi_rows_second(const GroupedGemmArgs& g, const TileInfo& ti, EpiRows& er) {
+  if constexpr (EPI == EPI_SCATTER_WEIGHTED) {
+    if (static_cast<int>(threadIdx.x) < ti.rows) er.w = g.route_w[er.o];
+    er.have_w = true;
+  }
+}
+
 template <int EPI, int NSETS, bool F8, bool A8, bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInfo& ti, int split, int64_t n0,
-                                         int wm, int wn, int lane, unsigned char* lds, const f32x4_t (&acc)[8][4]) {
+                                         int wm, int wn, int lane, unsigned char* lds, const f32x4_t (&acc)[8][4],
+                                         const EpiRows& er) {
   constexpr int kFrags = NSETS == 2 ? 4 : 8;       // output fragments per wave
   constexpr int kEsz = OUT_F32 ? 4 : 2;
   constexpr int kRowBytes = (NSETS == 2 ? kBN / 2 : kBN) * kEsz;
@@ -244,15 +271,11 @@ __device__ __forceinline__ void epilogue(const GroupedGemmArgs& g, const TileInf
   float* t_w = reinterpret_cast<float*>(lds + 128 * kPitch + 1024);    // [256]
   if constexpr (kScatter) {
     const int t = static_cast<int>(threadIdx.x);
-    int o = 0;
-    float w = 1.f;
-    if (t < ti.rows) {
-      o = g.order[ti.row0 + t];
-      if (kWeighted) w = g.route_w[o];
-    }
+    float w = er.w;
+    if (kWeighted && !er.have_w && t < ti.rows) w = g.route_w[er.o];
     lds_barrier();  // the ring is no longer read
     if (t < kBM) {
-      t_order[t] = o;
+      t_order[t] = er.o;
       if (kWeighted) t_w[t] = w;
     }
   }
@@ -771,6 +794,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 #pragma unroll
     for (int m = 0; m < 4; ++m) acc[n][m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  EpiRows er;
+  epi_rows_first<EPI>(g, ti, er);
   if constexpr (F8 && !A8) {
     const int groups = (ti.rows + 15) >> 4;
     const int nm = groups > c.wm ? min(4, (groups - c.wm + 3) >> 2) : 0;
@@ -795,13 +820,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     k_issue_range<NSETS>(c, 0, 4);
     run_k_body<NSETS, A8>(c, acc, ti.rows);
   }
+  epi_rows_second<EPI>(g, ti, er);
 
   if constexpr (EPI == EPI_SWIGLU)
-    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc, er);
   else if (g.out_dtype == DT_F32)
-    epilogue<EPI, NSETS, F8, A8, true>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, true>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc, er);
   else
-    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc);
+    epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc, er);
 }
 
 template <int EPI, int NSETS, bool F8, bool A8>
