@@ -45,6 +45,7 @@ constexpr int kStagesF8 = 3;
 constexpr int kStageF8 = 2 * kAStage + kBStage;  // 48 KiB
 constexpr int kLdsF8 = kStagesF8 * kStageF8;     // 144 KiB
 constexpr int kGroupN = 4;                   // column tiles swept together
+constexpr bool kThin = true;                 // tiles of <= 64 rows take the thin loop (bf16)
 
 __device__ __forceinline__ f32x4_t mfma16(const u32x4_t a, const u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -677,6 +678,20 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
 
+// Byte offset (from the A base) of this lane's 16-byte piece of 16-row
+// group `group` of the tile in the stage that starts at A piece kb_first:
+// row group * 16 + (lane >> 2), physical chunk lane & 3, which holds logical
+// chunk (lane & 3) ^ ((lane >> 3) & 3).  Rows past the tile re-read its
+// first row.
+__device__ __forceinline__ uint32_t a_group_offset(const GroupedGemmArgs& g, const TileInfo& ti, int group, int lane,
+                                                   int64_t kb_first) {
+  const int r = group * 16 + (lane >> 2);
+  const int p = ti.row0 + (r < ti.rows ? r : 0);
+  const int ch = (lane & 3) ^ ((lane >> 3) & 3);
+  return g.a_kb_rows ? static_cast<uint32_t>((kb_first * g.a_kb_rows + p) * 64 + ch * 16)
+                     : static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + kb_first * 64);
+}
+
 // Stage sources of tile (ti, col_tile, split) for this wave.  A stage is
 // staged in 8 shares; share w holds token rows (w*2 + j)*16 + (lane >> 2),
 // 16-byte physical chunk (lane & 3), which holds logical chunk
@@ -710,11 +725,7 @@ __device__ __forceinline__ WaveCtx tile_ctx(const GroupedGemmArgs& g, const Tile
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int share = j < 2 ? wave : (wave ^ 4);
-    const int r = (share * 2 + (j & 1)) * 16 + (lane >> 2);
-    const int p = ti.row0 + (r < ti.rows ? r : 0);
-    const int ch = (lane & 3) ^ ((lane >> 3) & 3);
-    c.a_off[j] = a_kb ? static_cast<uint32_t>((kb_first * g.a_kb_rows + p) * 64 + ch * 16)
-                      : static_cast<uint32_t>(source_row(g, p) * g.lda * 2 + ch * 16 + kb_first * 64);
+    c.a_off[j] = a_group_offset(g, ti, share * 2 + (j & 1), lane, kb_first);
   }
   // Weight blocks (wave-uniform addresses).  The packed buffer has a
   // 256-row tail, so row blocks past N stay in bounds (their columns are
@@ -736,6 +747,63 @@ __device__ __forceinline__ WaveCtx tile_ctx(const GroupedGemmArgs& g, const Tile
   c.wn = wave & 1;   // weight rows of each set: wn half
   c.KT = KT;
   return c;
+}
+
+// ---- Thin tiles (bf16, at most 64 rows: one 16-row group per wave pair).
+// Such a tile is bound by how many weight bytes are in flight, not by its
+// few MFMAs, so it runs its own loop: 20 KiB stages (the 4 KiB of token
+// rows it has, then the 16 weight blocks) in an 8-deep ring with 6 stages
+// in flight, against 2-3 of the 32 KiB stages in the main loop.  Waves 0-3
+// load token group `wave` and every wave its two weight blocks; one barrier
+// per stage (a buffer is refilled two stages after its last read).
+constexpr int kThinRows = 64;
+constexpr int kThinStage = 20 * 1024;
+constexpr int kThinRing = kLds / kThinStage;  // 8
+constexpr int kThinAhead = kThinRing - 2;     // stages in flight
+
+__device__ __forceinline__ void thin_issue(const WaveCtx& c, uint32_t a_off_thin, int kt, int buf) {
+  unsigned char* st = c.lds + buf * kThinStage;
+  if (c.wave < 4)
+    __builtin_amdgcn_global_load_lds(c.a_base + (a_off_thin + static_cast<uint32_t>(kt) * c.a_kstride),
+                                     st + c.wave * 1024, 16, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    __builtin_amdgcn_global_load_lds(c.b_base[j] + (static_cast<uint32_t>(kt) * 1024 + c.b_lane),
+                                     st + 4096 + (c.wave * 2 + j) * 1024, 16, 0, 0);
+}
+
+template <int NSETS>
+__device__ __forceinline__ void thin_k_loop(const WaveCtx& c, uint32_t a_off_thin, int rows, f32x4_t (&acc)[8][4]) {
+  const int KT = c.KT;
+  const bool active = c.wm * 16 < rows;  // this wave pair's row group holds rows
+  for (int kt = 0; kt < kThinAhead && kt < KT; ++kt) thin_issue(c, a_off_thin, kt, kt);
+  for (int kt = 0; kt < KT; ++kt) {
+    // Refill the buffer read two stages ago, then wait for stage kt (loads
+    // per stage: 3 for waves 0-3, 2 for the others).
+    if (kt + kThinAhead < KT) {
+      thin_issue(c, a_off_thin, kt + kThinAhead, (kt + kThinAhead) % kThinRing);
+      if (c.wave < 4)
+        __builtin_amdgcn_s_waitcnt(wait_vm(3 * kThinAhead, false));
+      else
+        __builtin_amdgcn_s_waitcnt(wait_vm(2 * kThinAhead, false));
+    } else {
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    }
+    asm volatile("s_barrier" ::: "memory");
+    if (active) {
+      const unsigned char* st = c.lds + (kt % kThinRing) * kThinStage;
+      const u32x4_t fa = *reinterpret_cast<const u32x4_t*>(st + c.wm * 1024 + c.a_lane);
+      u32x4_t fb[8];
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const int rb = NSETS == 2 ? ((n >> 2) * 8 + c.wn * 4 + (n & 3)) : (c.wn * 8 + n);
+        fb[n] = *reinterpret_cast<const u32x4_t*>(st + 4096 + rb * 1024 + c.b_lane);
+      }
+#pragma unroll
+      for (int n = 0; n < 8; ++n) acc[n][0] = mfma16(fb[n], fa, acc[n][0]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
 }
 
 // The bf16 / fp8-activation K loop of a tile with `rows` rows, after its
@@ -817,8 +885,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
       }
     }
   } else {
-    k_issue_range<NSETS>(c, 0, 4);
-    run_k_body<NSETS, A8>(c, acc, ti.rows);
+    if (!A8 && kThin && ti.rows <= kThinRows) {
+      const int64_t kb_first = split_boundary(static_cast<int>(g.K / 32), g.ksplit, split);
+      thin_k_loop<NSETS>(c, a_group_offset(g, ti, wave & 3, lane, kb_first), ti.rows, acc);
+    } else {
+      k_issue_range<NSETS>(c, 0, 4);
+      run_k_body<NSETS, A8>(c, acc, ti.rows);
+    }
   }
   epi_rows_second<EPI>(g, ti, er);
 
