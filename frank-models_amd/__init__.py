@@ -103,4 +103,18 @@ __all__ = [
     "quantize_fp8",
     "FmoeError",
     "NoDeviceError",
+    "hip_runtimes_loaded",
+    "lowlevel",
+    "params",
+    "attention_block_decode",
+    "AttentionBlockDecode",
+    "PackedLinearWeights",
+    "pack_linear_weights",
+    "kvcache_gather",
+    "kvcache_scatter_decode",
+    "kvcache_scatter_prefill",
+    "ATTN_HPARAMS",
+    "AttentionHParams",
+    "AttentionLayer",
+    "load_attention_layers",
 ]

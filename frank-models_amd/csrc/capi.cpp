@@ -1,7 +1,8 @@
 // C ABI of libfmoe.so: argument validation, workspace layout and the launch
 // sequence of each entry point.  Declarations and reference citations are in
-// include/fmoe.h.
+// include/fmoe.h (the kernel-path override for tests in include/fmoe_diag.h).
 #include "fmoe.h"
+#include "fmoe_diag.h"
 
 #include <hip/hip_runtime_api.h>
 

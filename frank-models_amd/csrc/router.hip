@@ -255,6 +255,19 @@ __global__ __launch_bounds__(kThreads) void router_simt_kernel(
 constexpr int kMfmaWaves = 16;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 
+// NCH: 16-expert chunks the kernel is built for (1, 2, or 8 for up to 128
+// experts, then only the first ceil(E / 16) are used).  Each wave loads
+// kRouterDepth trips (32-wide hidden chunks kMfmaWaves * 32 apart) before
+// its first MFMA: at 4096 hidden columns and up to 32 experts that is all
+// of its 8 trips in one round trip.  With more experts the operands of one
+// trip already fill the register budget (more would spill), so it loads one
+// trip at a time; that case only serves inputs the tile router cannot take.
+template <int NCH>
+constexpr int router_depth() {
+  return NCH <= 2 ? 8 : 1;
+}
+
+template <int NCH>
 __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, int n_tokens, int n_embd,
     int n_expert, int k, int normalize, int* __restrict__ ids, float* __restrict__ weights) {
@@ -266,9 +279,9 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
   const int tok0 = blockIdx.x * kTok;
   const int n_chunks = (n_expert + 15) / 16;
 
-  f32x4_t acc[kMfmaMaxExpert / 16];
+  f32x4_t acc[NCH];
 #pragma unroll
-  for (int c = 0; c < kMfmaMaxExpert / 16; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < NCH; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int row = lane & 15;         // token (A) / expert-in-chunk (B)
   const int kofs = (lane >> 4) * 8;  // 8 consecutive hidden elements
@@ -276,43 +289,39 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
   const bool t_ok = t < n_tokens;
   const bf16_t* xrow = x + static_cast<int64_t>(t_ok ? t : 0) * n_embd + kofs;
   // Operands of one 32-wide chunk of the hidden axis: the token fragment and
-  // one router fragment per 16 experts.  Loaded a trip ahead (two sets of
-  // registers), so each wave keeps a trip's loads in flight while it
-  // multiplies the previous one.
+  // one router fragment per 16 experts; chunks past the hidden axis load
+  // zeros (their MFMAs add exact zeros).  The trips accumulate in hidden
+  // order, as one trip at a time would.
   const u32x4_t zero{0u, 0u, 0u, 0u};
-  auto load = [&](int h0, u32x4_t& av, u32x4_t (&bv)[kMfmaMaxExpert / 16]) __attribute__((always_inline)) {
-    const bool in = h0 < n_embd;
-    av = (t_ok && in) ? *reinterpret_cast<const u32x4_t*>(xrow + h0) : zero;
-#pragma unroll
-    for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
-      const int e = c * 16 + row;
-      bv[c] = (c < n_chunks && e < n_expert && in)
-                  ? *reinterpret_cast<const u32x4_t*>(wr + static_cast<int64_t>(e) * n_embd + h0 + kofs)
-                  : zero;
-    }
-  };
-  auto multiply = [&](const u32x4_t& av, const u32x4_t (&bv)[kMfmaMaxExpert / 16]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int c = 0; c < kMfmaMaxExpert / 16; ++c)
-      if (c < n_chunks)
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                         __builtin_bit_cast(bf16x8_t, bv[c]), acc[c], 0, 0, 0);
-  };
   constexpr int kStep = kMfmaWaves * 32;
-  u32x4_t a0, b0[kMfmaMaxExpert / 16], a1, b1[kMfmaMaxExpert / 16];
-  int h0 = wave * 32;
-  load(h0, a0, b0);
-  for (; h0 < n_embd; h0 += 2 * kStep) {
-    load(h0 + kStep, a1, b1);
-    multiply(a0, b0);
-    if (h0 + kStep >= n_embd) break;
-    load(h0 + 2 * kStep, a0, b0);
-    multiply(a1, b1);
+  constexpr int D = router_depth<NCH>();
+  for (int h0 = wave * 32; h0 < n_embd; h0 += D * kStep) {
+    u32x4_t av[D], bv[D][NCH];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int h = h0 + d * kStep;
+      const bool in = h < n_embd;
+      av[d] = (t_ok && in) ? *reinterpret_cast<const u32x4_t*>(xrow + h) : zero;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int e = c * 16 + row;
+        bv[d][c] = (c < n_chunks && e < n_expert && in)
+                       ? *reinterpret_cast<const u32x4_t*>(wr + static_cast<int64_t>(e) * n_embd + h + kofs)
+                       : zero;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        if (c < n_chunks)
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[d]),
+                                                           __builtin_bit_cast(bf16x8_t, bv[d][c]), acc[c], 0, 0, 0);
   }
   // D[token][expert]: lane holds expert (lane & 15), tokens 4*(lane>>4)+i.
   float* mine = part + wave * kTok * ld;
 #pragma unroll
-  for (int c = 0; c < kMfmaMaxExpert / 16; ++c) {
+  for (int c = 0; c < NCH; ++c) {
     if (c < n_chunks) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) mine[((lane >> 4) * 4 + i) * ld + c * 16 + (lane & 15)] = acc[c][i];
@@ -576,6 +585,17 @@ hipError_t launch_topk_permute(const float* part, int n_split, int n_tokens, int
   return hipGetLastError();
 }
 
+template <int NCH>
+void launch_router_mfma(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k, bool normalize,
+                        int* ids, float* weights, size_t lds, hipStream_t stream) {
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(router_mfma_bf16_kernel<NCH>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  (void)attr;
+  hipLaunchKernelGGL((router_mfma_bf16_kernel<NCH>), dim3((n_tokens + kTok - 1) / kTok), dim3(kMfmaThreads), lds,
+                     stream, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd,
+                     n_expert, k, normalize ? 1 : 0, ids, weights);
+}
+
 template <int NCP>
 void launch_router_tile(const bf16_t* x, const bf16_t* wr, int n_tokens, int n_embd, int n_expert, int k,
                         bool normalize, int* ids, float* weights, hipStream_t stream) {
@@ -608,16 +628,14 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
   } else if (dtype == DT_BF16 && n_embd % 32 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
     const int ld = ((n_expert + 15) / 16) * 16 + 1;
     const size_t lds = static_cast<size_t>(kMfmaWaves + 1) * kTok * ld * sizeof(float);
-    static const bool configured = [] {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(router_mfma_bf16_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      (void)hipGetLastError();
-      return true;
-    }();
-    (void)configured;
-    hipLaunchKernelGGL(router_mfma_bf16_kernel, grid, dim3(kMfmaThreads), lds, stream,
-                       static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens,
-                       n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
+    const int n_chunks = (n_expert + 15) / 16;
+    if (n_chunks == 1)
+      launch_router_mfma<1>(x, wr, n_tokens, n_embd, n_expert, k, normalize, ids, weights, lds, stream);
+    else if (n_chunks == 2)
+      launch_router_mfma<2>(x, wr, n_tokens, n_embd, n_expert, k, normalize, ids, weights, lds, stream);
+    else
+      launch_router_mfma<kMfmaMaxExpert / 16>(x, wr, n_tokens, n_embd, n_expert, k, normalize, ids, weights, lds,
+                                              stream);
   } else {
     const size_t lds = static_cast<size_t>(kTok) * (n_expert + 1) * sizeof(float);
     if (dtype == DT_BF16) {

@@ -66,15 +66,6 @@ typedef enum fmoe_dtype {
                         Mixtral shapes) to the FMOE_F8E4M3FN result. */
 } fmoe_dtype;
 
-/* Kernel-path override for tests and tuning (process-wide; default AUTO). */
-typedef enum fmoe_gemm_path {
-  FMOE_PATH_AUTO = 0,
-  FMOE_PATH_GENERIC = 1, /* SIMT grouped GEMM, any shape and dtype */
-  FMOE_PATH_TILED = 2,   /* MFMA tiled grouped GEMM, 128-row tiles */
-  FMOE_PATH_STREAM = 3,  /* MFMA weight-streaming grouped GEMM (decode) */
-  FMOE_PATH_TILED_LARGE = 4 /* MFMA tiled grouped GEMM, 256x256 tiles (prefill) */
-} fmoe_gemm_path;
-
 /* Message describing the last failure on this thread ("" if none). */
 const char *fmoe_last_error(void);
 
@@ -85,14 +76,6 @@ int fmoe_abi_version(void);
 /* Checks that the current HIP device is a gfx950; writes its ordinal and
  * architecture name (arch may be NULL).  FMOE_ERR_NO_DEVICE otherwise. */
 int fmoe_device_check(int *device, char *arch, size_t arch_len);
-
-/* Selects the grouped-GEMM kernel family (fmoe_gemm_path).  A forced family
- * that cannot run a given GEMM (dtype, shape, alignment) falls back to the
- * AUTO choice for that GEMM. */
-int fmoe_set_gemm_path(int path);
-int fmoe_get_gemm_path(void);
-/* The family used by the last grouped GEMM launched on this thread. */
-int fmoe_last_gemm_path(void);
 
 /* Kernel timing (no counterpart in the reference, which has no profiling
  * beyond dumping linked IR, tests/conftest.py:24-30).  While enabled, each

@@ -1,0 +1,39 @@
+/*
+ * fmoe_diag.h -- kernel-path override of libfmoe.so, for tests and tuning.
+ *
+ * No counterpart in the reference: IREE picks its kernels at compile time
+ * (components/moe/mul_mat_id.mlir:22-120 is lowered once).  These calls are
+ * kept out of fmoe.h because the override is process-wide: it changes the
+ * kernel family of every grouped GEMM any caller launches afterwards, so a
+ * production caller has no use for it.  The parity tests force each family
+ * in turn with it and compare them with the oracle.
+ */
+#ifndef FMOE_DIAG_H_
+#define FMOE_DIAG_H_
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fmoe_gemm_path {
+  FMOE_PATH_AUTO = 0,
+  FMOE_PATH_GENERIC = 1, /* SIMT grouped GEMM, any shape and dtype */
+  FMOE_PATH_TILED = 2,   /* MFMA tiled grouped GEMM, 128-row tiles */
+  FMOE_PATH_STREAM = 3,  /* MFMA weight-streaming grouped GEMM (decode) */
+  FMOE_PATH_TILED_LARGE = 4 /* MFMA tiled grouped GEMM, 256x256 tiles (prefill) */
+} fmoe_gemm_path;
+
+/* Selects the grouped-GEMM kernel family (fmoe_gemm_path) for the whole
+ * process (default AUTO).  A forced family that cannot run a given GEMM
+ * (dtype, shape, alignment) falls back to the AUTO choice for that GEMM.
+ * FMOE_ERR_INVALID_ARGUMENT for an unknown value. */
+int fmoe_set_gemm_path(int path);
+int fmoe_get_gemm_path(void);
+/* The family used by the last grouped GEMM launched on this thread. */
+int fmoe_last_gemm_path(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FMOE_DIAG_H_ */

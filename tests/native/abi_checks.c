@@ -1,4 +1,4 @@
-/* Host-side checks of the C ABI (include/fmoe.h) on a machine without a GPU.
+/* Host-side checks of the C ABI (include/fmoe.h, include/fmoe_diag.h) on a machine without a GPU.
  *
  * Built by tests/test_sanitizers.py with AddressSanitizer and
  * UndefinedBehaviorSanitizer on the host code of capi.cpp, then run: every
@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include "fmoe.h"
+#include "fmoe_diag.h"
 
 static int failures = 0;
 

@@ -1,5 +1,5 @@
 """The C ABI boundary, checked without a GPU: the library loads, exports
-every symbol include/fmoe.h declares, and turns bad arguments into status
+every symbol the headers under include/ declare, and turns bad arguments into status
 codes (never a crash) before it touches a device."""
 
 import ctypes
@@ -11,14 +11,23 @@ import pytest
 import torch
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "fmoe.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 NO_GPU = not torch.cuda.is_available()
 
 
-def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(fmoe_[a-z0-9_]+)\s*\(", text)))
+def declared_functions(headers=None):
+    names = set()
+    for h in headers or HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(fmoe_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+def test_path_override_is_outside_the_product_header():
+    product = declared_functions([ROOT / "include" / "fmoe.h"])
+    assert not [n for n in product if "gemm_path" in n]
+    assert "fmoe_set_gemm_path" in declared_functions([ROOT / "include" / "fmoe_diag.h"])
 
 
 def test_header_declares_the_drop_in_entry_points():
