@@ -252,7 +252,7 @@ struct BlockLayout {
   // fp8 activations (FMOE_F8E4M3FN_A8, prefill-sized batches): e4m3 token
   // rows and SwiGLU rows, K-blocked, with their per-row scales (0 bytes otherwise)
   size_t xq, xs, hq, hs, hmax, xmax, a8_bytes;
-  size_t rpart;          // decode router's split logits (0 bytes when the shape takes the general router)
+  size_t rpart;          // split router logits, decode or prefill (0 bytes when the shape takes the one-kernel router)
   size_t rpart_bytes;
   int h_dtype, y_dtype;
   int y_parts;           // fp32 partial buffers reserved for a K-split down GEMM
@@ -292,8 +292,10 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   L.perm = permute_layout(n, E, off);
   off = L.perm.total;
   L.rpart = off;
-  L.rpart_bytes = router_decode_scratch_bytes(static_cast<int>(T), static_cast<int>(H), static_cast<int>(E),
-                                              static_cast<int>(k), act);
+  L.rpart_bytes = std::max(router_decode_scratch_bytes(static_cast<int>(T), static_cast<int>(H),
+                                                       static_cast<int>(E), static_cast<int>(k), act),
+                           router_prefill_scratch_bytes(static_cast<int>(T), static_cast<int>(H),
+                                                        static_cast<int>(E), static_cast<int>(k), act));
   off += align_up(L.rpart_bytes);
   L.h_dtype = act;
   L.h = off;
@@ -446,8 +448,13 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128),
   // then the slot-major assignments grouped by expert (replaces the gather,
   // mul_mat_id.mlir:50-61).  Decode-sized batches run both as two launches.
-  const bool decode_router = L.rpart_bytes > 0 && reinterpret_cast<uintptr_t>(c.input) % 16 == 0 &&
-                             reinterpret_cast<uintptr_t>(c.w_router) % 16 == 0;
+  const bool router16 = reinterpret_cast<uintptr_t>(c.input) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(c.w_router) % 16 == 0;
+  const int H32 = static_cast<int>(n_embd), E32 = static_cast<int>(n_expert), k32 = static_cast<int>(n_expert_used);
+  const bool decode_router = router16 && router_decode_scratch_bytes(T, H32, E32, k32, act_dtype) > 0 &&
+                             L.rpart_bytes >= router_decode_scratch_bytes(T, H32, E32, k32, act_dtype);
+  const bool split_router = router16 && !decode_router && router_prefill_scratch_bytes(T, H32, E32, k32, act_dtype) > 0 &&
+                            L.rpart_bytes >= router_prefill_scratch_bytes(T, H32, E32, k32, act_dtype);
   if (decode_router) {
     ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
     FMOE_HIP(launch_router_decode(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
@@ -456,8 +463,12 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   } else {
     {
       ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
-      FMOE_HIP(launch_router(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
-                             static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype, ids, rw, s));
+      if (split_router)
+        FMOE_HIP(launch_router_prefill(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype,
+                                       at<float>(workspace, L.rpart), ids, rw, s));
+      else
+        FMOE_HIP(launch_router(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype, ids, rw,
+                               s));
     }
     ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
     FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err,

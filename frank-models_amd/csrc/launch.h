@@ -168,6 +168,17 @@ hipError_t launch_router_decode(const void* x, const void* wr, int n_tokens, int
                                 bool normalize, int dtype, float* part, int* ids, float* weights, int* order,
                                 int* offsets, int* err_count, hipStream_t stream);
 
+// Prefill batches (bf16, n_tokens > kDecodeMaxTokens, 32 < n_expert <= 128,
+// n_embd % 128 == 0, k <= 16): router logits over 64-token tiles and
+// ranges of the hidden axis into `part` (router_prefill_scratch_bytes, 0
+// when the shape does not qualify), then softmax + top-k summing the ranges
+// in order (ids, weights as launch_router writes them).
+// hipErrorNotSupported when the inputs do not qualify.
+size_t router_prefill_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k, int dtype);
+hipError_t launch_router_prefill(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k,
+                                 bool normalize, int dtype, float* part, int* ids, float* weights,
+                                 hipStream_t stream);
+
 // Batches above kPermuteChunk assignments run chunked, with a histogram
 // scratch of permute_scratch_bytes() (0 for smaller batches).
 constexpr int kPermuteChunk = 2048;

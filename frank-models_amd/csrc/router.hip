@@ -341,85 +341,95 @@ __global__ __launch_bounds__(kMfmaThreads) void router_mfma_bf16_kernel(
 }
 
 // ---- Prefill logits for 32 < n_expert <= 128 (bf16, n_embd % 128 == 0,
-// k <= 16): one 512-thread block per kTileTok = 32 tokens.  The block reads
-// its token rows and the router matrix once each, staged through LDS by
-// global_load_lds in stages of 128 hidden columns (a 3-deep ring, two stages
-// in flight): 2 token tiles x 4 steps of 32 and NCP expert chunks x 4 steps,
-// each a 1 KiB block in MFMA lane order (lane l: row l % 16, columns
-// 8 (l / 16) .. +8 of the step).  Wave w owns expert chunk w % NCP and
-// 2 NCP / 8 token tiles, so no partial logits cross waves.  The 16-token
-// kernel above reads the whole router matrix per 16 tokens (at 128 experts
-// and 2048 columns, 512 KiB for 64 KiB of token rows).
-constexpr int kTileTok = 32;
+// k <= 16): one 512-thread block per TT 16-token tiles (32 or 64 tokens) and
+// per range of the hidden axis.  The block stages its token rows and the
+// router rows through an LDS ring by global_load_lds, in stages of 128
+// hidden columns (a 3-deep ring, two stages in flight): TT * 16 token rows
+// then NCP * 16 router rows, 256 bytes each.  Each load instruction moves
+// four whole 256-byte row segments (16 lanes per row), which a CU streams
+// about 1.6x faster than 16-row x 64-byte MFMA-shaped gathers.  The row's
+// 16-byte chunks sit at chunk ^ (row & 15), so the MFMA operand reads
+// (lane l: row l % 16, inputs 8 (l / 16) .. +8 of a 32-input step) hit 16
+// distinct bank groups.  Wave w owns expert chunk w % NCP and TT * NCP / 8
+// token tiles, so no partial logits cross waves.
+//   part == nullptr (one range over the whole hidden axis): softmax + top-k
+//   in the block.  Otherwise range blockIdx.y writes its partial logits to
+//   part[(blockIdx.y * T + t) * E + e] for router_part_topk_kernel.
 constexpr int kTileCols = 128;
 constexpr int kTileRing = 3;
 
-template <int NCP>
+template <int NCP, int TT>
 constexpr int tile_stage_bytes() {
-  return (kTileTok / 16 + NCP) * 4 * 1024;
+  return (TT + NCP) * 16 * 256;
 }
 
-// One wave's loads of stage st: its blocks wave, wave + 8, ... into the
-// stage's ring buffer.
+// One wave's loads of stage st: its 1 KiB blocks wave, wave + 8, ... (four
+// rows each) into the stage's ring buffer.
 template <int NPW>
-__device__ __forceinline__ void tile_issue(const bf16_t* const (&src)[NPW], unsigned char* smem, int st, int wave,
-                                           int stage_bytes) {
-  unsigned char* dst = smem + (st % kTileRing) * stage_bytes;
+__device__ __forceinline__ void tile_issue(const bf16_t* const (&src)[NPW], unsigned char* smem, int st, int buf,
+                                           int wave, int stage_bytes) {
+  unsigned char* dst = smem + buf * stage_bytes;
 #pragma unroll
   for (int j = 0; j < NPW; ++j)
     __builtin_amdgcn_global_load_lds(src[j] + st * kTileCols, dst + (wave + 8 * j) * 1024, 16, 0, 0);
 }
 
-template <int NCP>
+template <int NCP, int TT>
 __global__ __launch_bounds__(512) void router_tile_bf16_kernel(const bf16_t* __restrict__ x,
                                                                const bf16_t* __restrict__ wr, int n_tokens,
                                                                int n_embd, int n_expert, int k, int normalize,
-                                                               int* __restrict__ ids, float* __restrict__ weights) {
-  static_assert(NCP == 4 || NCP == 8, "8 waves over NCP expert chunks x 2 token tiles");
+                                                               int stages_per_range, int* __restrict__ ids,
+                                                               float* __restrict__ weights, float* __restrict__ part) {
+  static_assert(NCP == 4 || NCP == 8, "8 waves over NCP expert chunks");
+  static_assert((TT == 2 || TT == 4) && (TT * NCP) % 8 == 0, "whole token tiles per wave");
   extern __shared__ __align__(16) unsigned char smem[];
-  constexpr int kTT = kTileTok / 16;          // token tiles
-  constexpr int kTTW = kTT * NCP / 8;         // token tiles per wave
-  constexpr int kStage = tile_stage_bytes<NCP>();
-  constexpr int kBlocks = (kTT + NCP) * 4;    // 1 KiB blocks per stage
+  constexpr int kTok = TT * 16;
+  constexpr int kTTW = TT * NCP / 8;          // token tiles per wave
+  constexpr int kStage = tile_stage_bytes<NCP, TT>();
+  constexpr int kBlocks = kStage / 1024;      // 1 KiB blocks (four rows) per stage
   constexpr int kPerWave = kBlocks / 8;       // loads per wave per stage
   static_assert(kBlocks % 8 == 0, "stage blocks split evenly over 8 waves");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int tok0 = blockIdx.x * kTileTok;
+  const int tok0 = blockIdx.x * kTok;
   const int chunk = wave % NCP;
   const int tt0 = (wave / NCP) * kTTW;
   const int r16 = lane & 15;
-  const int kofs = 8 * (lane >> 4);
 
-  // This wave's share of a stage: blocks wave, wave + 8, ...  Block b < 4 kTT
-  // is token tile b / 4, step b % 4; the rest are expert chunk (b - 4 kTT) / 4.
-  // Rows past the batch or the expert count read the last valid row (their
-  // logits are never used).
+  // Block b holds stage rows 4 b .. 4 b + 3 (token rows first, then router
+  // rows); lane l loads row 4 b + l / 16, physical chunk l % 16, i.e. the
+  // logical chunk (l % 16) ^ (row & 15).  Rows past the batch or the expert
+  // count read the last valid row (their logits are never used).
   const bf16_t* src[kPerWave];
 #pragma unroll
   for (int j = 0; j < kPerWave; ++j) {
-    const int b = wave + 8 * j;
-    if (b < 4 * kTT) {
-      const int t = min(tok0 + (b >> 2) * 16 + r16, n_tokens - 1);
-      src[j] = x + static_cast<int64_t>(t) * n_embd + (b & 3) * 32 + kofs;
+    const int r = 4 * (wave + 8 * j) + (lane >> 4);
+    const int c = r16 ^ (r & 15);
+    if (r < kTok) {
+      const int t = min(tok0 + r, n_tokens - 1);
+      src[j] = x + static_cast<int64_t>(t) * n_embd + c * 8;
     } else {
-      const int bb = b - 4 * kTT;
-      const int e = min((bb >> 2) * 16 + r16, n_expert - 1);
-      src[j] = wr + static_cast<int64_t>(e) * n_embd + (bb & 3) * 32 + kofs;
+      const int e = min(r - kTok, n_expert - 1);
+      src[j] = wr + static_cast<int64_t>(e) * n_embd + c * 8;
     }
   }
 
   f32x4_t acc[kTTW];
 #pragma unroll
   for (int q = 0; q < kTTW; ++q) acc[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int n_st = n_embd / kTileCols;
-  tile_issue<kPerWave>(src, smem, 0, wave, kStage);
-  if (n_st > 1) tile_issue<kPerWave>(src, smem, 1, wave, kStage);
+  const int n_st_all = n_embd / kTileCols;
+  const int st0 = blockIdx.y * stages_per_range;
+  const int n_st = min(stages_per_range, n_st_all - st0);
+  tile_issue<kPerWave>(src, smem, st0, 0, wave, kStage);
+  if (n_st > 1) tile_issue<kPerWave>(src, smem, st0 + 1, 1, wave, kStage);
+  // Operand reads: row (lane & 15) of a 16-row tile, logical chunk
+  // 4 s + lane / 16 of step s, stored at that chunk ^ (lane & 15).
+  const int rd_lane = r16 * 256;
   for (int st = 0; st < n_st; ++st) {
     // Stage st + 2 refills the buffer of stage st - 1, released by the
     // barrier that ended the last iteration.
     if (st + 2 < n_st) {
-      tile_issue<kPerWave>(src, smem, st + 2, wave, kStage);
+      tile_issue<kPerWave>(src, smem, st0 + st + 2, (st + 2) % kTileRing, wave, kStage);
       __builtin_amdgcn_s_waitcnt(wait_vm(2 * kPerWave, false));
     } else if (st + 1 < n_st) {
       __builtin_amdgcn_s_waitcnt(wait_vm(kPerWave, false));
@@ -430,10 +440,11 @@ __global__ __launch_bounds__(512) void router_tile_bf16_kernel(const bf16_t* __r
     const unsigned char* cur = smem + (st % kTileRing) * kStage;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4_t b = *reinterpret_cast<const u32x4_t*>(cur + ((4 * kTT + chunk * 4 + s) * 1024) + lane * 16);
+      const int off = rd_lane + (((4 * s + (lane >> 4)) ^ r16) << 4);
+      const u32x4_t b = *reinterpret_cast<const u32x4_t*>(cur + (kTok + chunk * 16) * 256 + off);
 #pragma unroll
       for (int q = 0; q < kTTW; ++q) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(cur + (((tt0 + q) * 4 + s) * 1024) + lane * 16);
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(cur + (tt0 + q) * 16 * 256 + off);
         acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                          __builtin_bit_cast(bf16x8_t, b), acc[q], 0, 0, 0);
       }
@@ -445,18 +456,90 @@ __global__ __launch_bounds__(512) void router_tile_bf16_kernel(const bf16_t* __r
   }
   __builtin_amdgcn_s_waitcnt(wait_vm(0, true));
   // D[token][expert]: the lane holds expert r16 of its chunk, tokens
-  // 4 (lane / 16) + i of each of its tiles.  The logits overwrite the ring.
+  // 4 (lane / 16) + i of each of its tiles.
+  const int e = chunk * 16 + r16;
+  if (part) {
+    float* dst = part + static_cast<int64_t>(blockIdx.y) * n_tokens * n_expert;
+#pragma unroll
+    for (int q = 0; q < kTTW; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = tok0 + (tt0 + q) * 16 + 4 * (lane >> 4) + i;
+        if (t < n_tokens && e < n_expert) dst[static_cast<int64_t>(t) * n_expert + e] = acc[q][i];
+      }
+    return;
+  }
+  // The logits overwrite the ring.
   constexpr int ld = NCP * 16 + 1;
   float* logits = reinterpret_cast<float*>(smem);
 #pragma unroll
   for (int q = 0; q < kTTW; ++q)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) logits[((tt0 + q) * 16 + 4 * (lane >> 4) + i) * ld + chunk * 16 + r16] = acc[q][i];
+    for (int i = 0; i < 4; ++i) logits[((tt0 + q) * 16 + 4 * (lane >> 4) + i) * ld + e] = acc[q][i];
   __syncthreads();
-  for (int g = wave; g < kTileTok / 4; g += 8) {
+  for (int g = wave; g < kTok / 4; g += 8) {
     if (tok0 + 4 * g >= n_tokens) break;
     softmax_topk4<NCP>(logits + 4 * g * ld, ld, tok0 + 4 * g, n_tokens, n_expert, k, normalize != 0, ids, weights);
   }
+}
+
+// Softmax + top-k of prefill logits split over hidden ranges: each wave
+// takes four tokens, sums their n_split partial logits in range order
+// (four ranges' loads in flight at a time) into its LDS rows, then runs the
+// four-token top-k.  n_expert <= 16 NV <= 128.
+constexpr int kPartWaves = 4;
+
+template <int NV>
+__global__ __launch_bounds__(kPartWaves * kWave) void router_part_topk_kernel(
+    const float* __restrict__ part, int n_split, int n_tokens, int n_expert, int k, int normalize,
+    int* __restrict__ ids, float* __restrict__ weights) {
+  constexpr int ld = 16 * NV + 1;
+  __shared__ float lg[kPartWaves][4 * ld];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int t0 = (static_cast<int>(blockIdx.x) * kPartWaves + wave) * 4;
+  if (t0 >= n_tokens) return;
+  const int g = lane >> 4, j = lane & 15;
+  const int t = min(t0 + g, n_tokens - 1);
+  const int64_t plane = static_cast<int64_t>(n_tokens) * n_expert;
+  const float* src = part + static_cast<int64_t>(t) * n_expert;
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = 0.f;
+  for (int s0 = 0; s0 < n_split; s0 += 4) {
+    float pv[4][NV];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = j + 16 * i;
+        pv[q][i] = s0 + q < n_split && e < n_expert ? src[(s0 + q) * plane + e] : 0.f;
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (s0 + q < n_split) v[i] += pv[q][i];
+  }
+  float* row = lg[wave];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) row[g * ld + j + 16 * i] = v[i];
+  // softmax_topk4 reads back only this lane's own values
+  softmax_topk4<NV>(row, ld, t0, n_tokens, n_expert, k, normalize != 0, ids, weights);
+}
+
+// Hidden ranges of the split prefill router: at least one block per CU over
+// the 64-token tiles, whole 128-column stages per range.
+struct PrefillSplit {
+  int n_split, stages_per_range;
+};
+
+PrefillSplit prefill_split(int n_tokens, int n_embd) {
+  const int n_tt = (n_tokens + 63) / 64;
+  const int n_st = n_embd / kTileCols;
+  const int want = std::min(n_st, std::max(1, (256 + n_tt - 1) / n_tt));
+  const int sps = (n_st + want - 1) / want;
+  return {(n_st + sps - 1) / sps, sps};
 }
 
 // ---- Decode-sized batches (T <= kDecodeMaxTokens, bf16, k <= 16,
@@ -596,15 +679,17 @@ void launch_router_mfma(const void* x, const void* wr, int n_tokens, int n_embd,
                      n_expert, k, normalize ? 1 : 0, ids, weights);
 }
 
-template <int NCP>
+template <int NCP, int TT>
 void launch_router_tile(const bf16_t* x, const bf16_t* wr, int n_tokens, int n_embd, int n_expert, int k,
-                        bool normalize, int* ids, float* weights, hipStream_t stream) {
-  constexpr int lds = kTileRing * tile_stage_bytes<NCP>();
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(router_tile_bf16_kernel<NCP>),
+                        bool normalize, int n_split, int stages_per_range, int* ids, float* weights, float* part,
+                        hipStream_t stream) {
+  constexpr int lds = kTileRing * tile_stage_bytes<NCP, TT>();
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(router_tile_bf16_kernel<NCP, TT>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)attr;
-  hipLaunchKernelGGL((router_tile_bf16_kernel<NCP>), dim3((n_tokens + kTileTok - 1) / kTileTok), dim3(512), lds,
-                     stream, x, wr, n_tokens, n_embd, n_expert, k, normalize ? 1 : 0, ids, weights);
+  hipLaunchKernelGGL((router_tile_bf16_kernel<NCP, TT>), dim3((n_tokens + TT * 16 - 1) / (TT * 16), n_split),
+                     dim3(512), lds, stream, x, wr, n_tokens, n_embd, n_expert, k, normalize ? 1 : 0,
+                     stages_per_range, ids, weights, part);
 }
 
 }  // namespace
@@ -619,12 +704,13 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
                        (reinterpret_cast<uintptr_t>(wr) % 16 == 0);
   if (dtype == DT_BF16 && n_embd % kTileCols == 0 && n_expert > 32 && n_expert <= kMfmaMaxExpert && k <= 16 &&
       aligned) {
+    const int n_st = n_embd / kTileCols;
     if (n_expert <= 64)
-      launch_router_tile<4>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd, n_expert,
-                            k, normalize, ids, weights, stream);
+      launch_router_tile<4, 2>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd,
+                               n_expert, k, normalize, 1, n_st, ids, weights, nullptr, stream);
     else
-      launch_router_tile<8>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd, n_expert,
-                            k, normalize, ids, weights, stream);
+      launch_router_tile<8, 2>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(wr), n_tokens, n_embd,
+                               n_expert, k, normalize, 1, n_st, ids, weights, nullptr, stream);
   } else if (dtype == DT_BF16 && n_embd % 32 == 0 && n_expert <= kMfmaMaxExpert && aligned) {
     const int ld = ((n_expert + 15) / 16) * 16 + 1;
     const size_t lds = static_cast<size_t>(kMfmaWaves + 1) * kTok * ld * sizeof(float);
@@ -654,6 +740,40 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
 }  // namespace fmoe
 
 namespace fmoe {
+
+size_t router_prefill_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k, int dtype) {
+  if (dtype != DT_BF16 || n_tokens <= kDecodeMaxTokens || n_embd % kTileCols || n_expert <= 32 ||
+      n_expert > kMfmaMaxExpert || k <= 0 || k > 16 || k > n_expert)
+    return 0;
+  return static_cast<size_t>(prefill_split(n_tokens, n_embd).n_split) * n_tokens * n_expert * sizeof(float);
+}
+
+hipError_t launch_router_prefill(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k,
+                                 bool normalize, int dtype, float* part, int* ids, float* weights,
+                                 hipStream_t stream) {
+  if (!part || router_prefill_scratch_bytes(n_tokens, n_embd, n_expert, k, dtype) == 0 ||
+      reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(wr) % 16)
+    return hipErrorNotSupported;
+  const PrefillSplit ps = prefill_split(n_tokens, n_embd);
+  const bf16_t* xb = static_cast<const bf16_t*>(x);
+  const bf16_t* wb = static_cast<const bf16_t*>(wr);
+  if (n_expert <= 64)
+    launch_router_tile<4, 4>(xb, wb, n_tokens, n_embd, n_expert, k, normalize, ps.n_split, ps.stages_per_range, ids,
+                             weights, part, stream);
+  else
+    launch_router_tile<8, 4>(xb, wb, n_tokens, n_embd, n_expert, k, normalize, ps.n_split, ps.stages_per_range, ids,
+                             weights, part, stream);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 grid((n_tokens + 4 * kPartWaves - 1) / (4 * kPartWaves));
+  if (n_expert <= 64)
+    hipLaunchKernelGGL(router_part_topk_kernel<4>, grid, dim3(kPartWaves * kWave), 0, stream, part, ps.n_split,
+                       n_tokens, n_expert, k, normalize ? 1 : 0, ids, weights);
+  else
+    hipLaunchKernelGGL(router_part_topk_kernel<8>, grid, dim3(kPartWaves * kWave), 0, stream, part, ps.n_split,
+                       n_tokens, n_expert, k, normalize ? 1 : 0, ids, weights);
+  return hipGetLastError();
+}
 
 size_t router_decode_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k, int dtype) {
   if (dtype != DT_BF16 || n_tokens <= 0 || n_tokens > kDecodeMaxTokens || n_embd % 32 || n_expert <= 0 ||

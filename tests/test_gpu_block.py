@@ -144,6 +144,25 @@ def test_decode_router_shapes(fm, wl, name, H, F, T, E, k):
     assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
 
 
+# Prefill batches with 33-128 experts (bf16, H % 128 == 0) take the router
+# that splits the hidden axis into ranges of 128-column stages and sums the
+# ranges' partial logits in order; these shapes cover one stage per range, a
+# shorter last range (7 stages as 3 + 3 + 1), 16-expert chunks of 4 and 8,
+# expert counts that are not a multiple of 16, k = 16 and a last token tile
+# holding one token.
+@pytest.mark.parametrize("name,H,F,T,E,k", [
+    ("C3", 896, 64, 5500, 100, 6), ("C3", 640, 64, 100, 40, 16), ("C4", 256, 64, 65, 64, 6),
+    ("C3", 384, 64, 1000, 128, 8),
+])
+def test_prefill_split_router_shapes(fm, wl, name, H, F, T, E, k):
+    cfg = _scaled(wl, name, H, F, n_expert=E, n_expert_used=k, margin=1e-4)
+    case = Case(fm, wl, cfg, T)
+    out = case.run()
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
+
+
 @pytest.mark.parametrize("name,T", [("C2", 16), ("C4", 1), ("C4", 4), ("C4", 16), ("C4", 64), ("C3", 64),
                                     ("C5", 16)])
 def test_full_size_decode(fm, wl, name, T):
