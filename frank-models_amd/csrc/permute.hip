@@ -51,10 +51,19 @@ __global__ __launch_bounds__(kHistThreads) void chunk_hist_kernel(const int* __r
   __syncthreads();
   const int f0 = blockIdx.x * kPermuteChunk;
   const int f1 = min(n, f0 + kPermuteChunk);
-  for (int f = f0 + threadIdx.x; f < f1; f += kHistThreads) {
-    const int e = ids[f];
-    atomicAdd(&h[(e >= 0 && e < n_expert) ? e : n_expert], 1);
+  // All of a thread's ids are loaded before the first count (one memory
+  // round trip per chunk, not one per id).
+  constexpr int kPer = kPermuteChunk / kHistThreads;
+  int ev[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int f = f0 + q * kHistThreads + static_cast<int>(threadIdx.x);
+    ev[q] = f < f1 ? ids[f] : 0;
   }
+#pragma unroll
+  for (int q = 0; q < kPer; ++q)
+    if (f0 + q * kHistThreads + static_cast<int>(threadIdx.x) < f1)
+      atomicAdd(&h[(ev[q] >= 0 && ev[q] < n_expert) ? ev[q] : n_expert], 1);
   __syncthreads();
   for (int e = threadIdx.x; e <= n_expert; e += kHistThreads)
     counts[static_cast<int64_t>(blockIdx.x) * (n_expert + 1) + e] = h[e];
@@ -75,11 +84,17 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __re
   const int stride = n_expert + 1;
 
   for (int e = tid; e < n_expert; e += kThreads) {
+    // eight chunks' counts in flight at a time
     int tot = 0, pre = 0;
-    for (int c = 0; c < n_chunks; ++c) {
-      const int v = counts[c * stride + e];
-      tot += v;
-      pre += c < chunk ? v : 0;
+    for (int c0 = 0; c0 < n_chunks; c0 += 8) {
+      int v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = c0 + q < n_chunks ? counts[(c0 + q) * stride + e] : 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        tot += v[q];
+        pre += c0 + q < chunk ? v[q] : 0;
+      }
     }
     total[e] = tot;
     base[e] = pre;
