@@ -254,6 +254,7 @@ struct BlockLayout {
   size_t xq, xs, hq, hs, hmax, xmax, a8_bytes;
   size_t rpart;          // split router logits, decode or prefill (0 bytes when the shape takes the one-kernel router)
   size_t rpart_bytes;
+  size_t ttab, ttab_bytes;  // tile schedule of the prefill GEMMs (256-tile kernel), shared by gate/up and down
   int h_dtype, y_dtype;
   int y_parts;           // fp32 partial buffers reserved for a K-split down GEMM
   int64_t y_part_elems;  // elements per partial
@@ -311,6 +312,18 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   const bool a8 = prefill && block_wdt == FMOE_F8E4M3FN_A8 && H % 128 == 0 && F % 128 == 0 && H <= 16384 &&
                   F <= 16384;
   const bool kb_candidate = prefill && !a8 && H % 64 == 0 && F % 64 == 0 && (F + 127) / 128 >= 16;
+  L.ttab = off;
+  L.ttab_bytes = 0;
+  if (prefill) {
+    GroupedGemmArgs gs = down_shape(T, E, k, H, F, act, wdt);
+    const size_t down_bytes = gemm_tiled256_table_bytes(gs);
+    gs.epi = EPI_SWIGLU;
+    gs.N = F;
+    gs.K = H;
+    gs.split_stride = 0;
+    L.ttab_bytes = std::max(down_bytes, gemm_tiled256_table_bytes(gs));
+  }
+  off += align_up(L.ttab_bytes);
   L.xkb = off;
   L.xkb_bytes = kb_candidate ? static_cast<size_t>(n) * H * 2 : 0;
   off += align_up(L.xkb_bytes);
@@ -427,6 +440,9 @@ int validate_block(const BlockCall& c) {
     return fail(FMOE_ERR_INVALID_ARGUMENT, "misaligned pointer");
   return FMOE_OK;
 }
+
+// Prefill GEMMs on the 256-tile kernel take a per-launch tile schedule.
+constexpr bool kTileTable = true;
 
 // The MoE FFN block's kernel sequence (moe_ffn_block.mlir:47-208) on a
 // validated call whose workspace holds layout L.
@@ -582,6 +598,14 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
         d = dk;
         y_dtype = FMOE_BF16;
       }
+    }
+    // The 256-tile GEMMs deal their tiles from a per-launch schedule table
+    // (ignored by the other kernel families).
+    if (kTileTable) {
+      int* ttab = at<int>(workspace, L.ttab);
+      if (L.ttab_bytes && L.ttab_bytes >= gemm_tiled256_table_bytes(g)) g.tile_table = ttab;
+      if (L.ttab_bytes && L.ttab_bytes >= gemm_tiled256_table_bytes(d)) d.tile_table = ttab;
+      if (L.ttab_bytes && L.ttab_bytes >= gemm_tiled256_table_bytes(dq)) dq.tile_table = ttab;
     }
   }
   {

@@ -137,6 +137,10 @@ struct GroupedGemmArgs {
   // the bit patterns of |h| (h rounded to bf16, so non-negative floats order
   // as unsigned integers) into row_amax[p], which starts at zero.
   unsigned* row_amax = nullptr;
+  // 256-tile kernel: workspace of gemm_tiled256_table_bytes(g) bytes for a
+  // per-launch tile schedule (built by a one-block kernel before the GEMM);
+  // nullptr, or a shape the table does not cover, keeps the in-kernel one.
+  int* tile_table = nullptr;
   ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
 };
 
@@ -207,6 +211,7 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g);
 hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t stream);
 // K split the 256-tile kernel would use for g (1 when it does not apply).
 int gemm_tiled256_ksplit(const GroupedGemmArgs& g);
+size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g);
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
                          int dtype, hipStream_t stream);

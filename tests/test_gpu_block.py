@@ -163,6 +163,21 @@ def test_prefill_split_router_shapes(fm, wl, name, H, F, T, E, k):
     assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
 
 
+# Gate/up GEMMs with at least 32 column tiles (n_ff >= 4096) take their tiles
+# from the per-launch schedule table: uniform and Zipf-skewed routing, a ragged
+# batch, and (C5) fp8 weights.
+@pytest.mark.parametrize("name,H,F,T,E,k", [
+    ("C2", 256, 4096, 700, 8, 2), ("C3", 256, 4096, 1500, 64, 6), ("C5", 256, 4096, 333, 8, 2),
+])
+def test_tile_table_shapes(fm, wl, name, H, F, T, E, k):
+    cfg = _scaled(wl, name, H, F, n_expert=E, n_expert_used=k, margin=1e-4)
+    case = Case(fm, wl, cfg, T)
+    out = case.run()
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} F={F} T={T} E={E} k={k}")
+
+
 @pytest.mark.parametrize("name,T", [("C2", 16), ("C4", 1), ("C4", 4), ("C4", 16), ("C4", 64), ("C3", 64),
                                     ("C5", 16)])
 def test_full_size_decode(fm, wl, name, T):
