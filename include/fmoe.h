@@ -208,7 +208,7 @@ int fmoe_moe_ffn_block(const void *input, const void *w_router, const void *pack
  * The call allocates nothing (no hipMalloc, no library allocation; kernel
  * timing is not recorded for it).  A call whose
  * fmoe_moe_ffn_block_workspace_bytes exceed FMOE_NOALLOC_SCRATCH_BYTES
- * (Mixtral shapes: about 500 tokens) fails with FMOE_ERR_WORKSPACE before
+ * (Mixtral shapes: about 480 tokens) fails with FMOE_ERR_WORKSPACE before
  * any device work.  Every call on one GPU shares that GPU's array and
  * leaves its contents behind: calls that overlap on one GPU (two streams,
  * two host threads) race, so the caller serialises them.
