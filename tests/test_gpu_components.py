@@ -246,8 +246,9 @@ def test_permute_device_ids_out_of_range(fm):
     host = np.random.default_rng(5).integers(0, 8, (2, 3000)).astype(np.int32)
     host[0, 10] = 8
     host[1, 2900] = -3
+    host[1, 100] = 513  # one past the largest expert count any kernel takes
     d = torch.from_numpy(host).cuda()
-    with pytest.raises(IndexError, match="2 expert id"):
+    with pytest.raises(IndexError, match="3 expert id"):
         fm.permute(d, 8)
     order = torch.empty(6000, dtype=torch.int32, device="cuda")
     offsets = torch.empty(9, dtype=torch.int32, device="cuda")
