@@ -18,7 +18,12 @@
 // from global memory (global_load_lds_dwordx4, no staging registers).  The
 // two waves of each SIMD take turns: one multiplies two stages while the
 // other reads its next fragments and issues the loads of a stage two to
-// three stages ahead (k_loop).
+// three stages ahead (k_body).  Tiles of at most 64 rows take a loop of
+// their own (thin_k_loop); fp8 weights take k_loop_f8.
+//
+// Tile order: each XCD works through a contiguous range of the tiles
+// (sched_tile), or, for wide gate/up GEMMs, through the list a one-block
+// kernel deals before the launch (tile_table_kernel).
 //
 // LDS layouts: weight blocks are copied as packed (lane-ordered 1 KiB blocks,
 // conflict-free 16-byte reads); token rows are 64 B with the 16-byte chunk

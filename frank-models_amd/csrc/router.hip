@@ -6,8 +6,19 @@
 // linalg.softmax dimension(0), iree_linalg_ext.topk with `ogt`, scf.if
 // renormalisation); oracles/moe.py:86-105.
 //
-// One block handles kTok = 16 tokens.  Logits for those tokens land in LDS,
-// then softmax + top-k runs four tokens per wave (16 lanes each, DPP row
+// Kernels by shape (launch_router, launch_router_prefill, launch_router_decode):
+//   * router_mfma_bf16_kernel: bf16, up to 128 experts (the prefill choice up
+//     to 32), one block per kTok = 16 tokens, 16 waves splitting the hidden
+//     axis;
+//   * router_tile_bf16_kernel: bf16, 33-128 experts, token rows and router
+//     rows staged as whole 256-byte row segments through an LDS ring; at
+//     prefill sizes split over hidden-axis ranges, with router_part_topk_kernel
+//     summing the ranges' partial logits;
+//   * router_split_logits_kernel + router_topk_permute_kernel: decode-sized
+//     batches (logits split over many blocks, one block for top-k and the
+//     permutation);
+//   * router_simt_kernel: fp32 and the shapes above that none takes.
+// Softmax + top-k run four tokens per wave (16 lanes each, DPP row
 // reductions) for k <= 16, or one token per wave over its 64 lanes.
 #include "common.h"
 #include "launch.h"
