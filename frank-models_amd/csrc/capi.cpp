@@ -602,10 +602,12 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
     // The 256-tile GEMMs deal their tiles from a per-launch schedule table
     // (ignored by the other kernel families).
     if (kTileTable) {
+      // only GEMMs the table applies to (nonzero size) and that fit the reserved room
       int* ttab = at<int>(workspace, L.ttab);
-      if (L.ttab_bytes && L.ttab_bytes >= gemm_tiled256_table_bytes(g)) g.tile_table = ttab;
-      if (L.ttab_bytes && L.ttab_bytes >= gemm_tiled256_table_bytes(d)) d.tile_table = ttab;
-      if (L.ttab_bytes && L.ttab_bytes >= gemm_tiled256_table_bytes(dq)) dq.tile_table = ttab;
+      for (GroupedGemmArgs* x : {&g, &d, &dq}) {
+        const size_t need = gemm_tiled256_table_bytes(*x);
+        if (need > 0 && need <= L.ttab_bytes) x->tile_table = ttab;
+      }
     }
   }
   {

@@ -1026,7 +1026,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 }
 
 template <int EPI, int NSETS, bool F8, bool A8>
-hipError_t launch_t(const GroupedGemmArgs& g, hipStream_t s) {
+hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
+  // a table pointer on a GEMM the table does not cover is ignored
+  GroupedGemmArgs g = g_in;
+  if (g.tile_table && gemm_tiled256_table_bytes(g) == 0) g.tile_table = nullptr;
   constexpr int lds_bytes = F8 && !A8 ? kLdsF8 : kLds;
   static const bool configured = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS, F8, A8>),
