@@ -254,7 +254,8 @@ struct BlockLayout {
   size_t xq, xs, hq, hs, hmax, xmax, a8_bytes;
   size_t rpart;          // split router logits, decode or prefill (0 bytes when the shape takes the one-kernel router)
   size_t rpart_bytes;
-  size_t ttab, ttab_bytes;  // tile schedule of the prefill GEMMs (256-tile kernel), shared by gate/up and down
+  // tile schedules of the prefill GEMMs (256-tile kernel; 0 bytes when the shape takes none)
+  size_t ttab_g, ttab_g_bytes, ttab_d, ttab_d_bytes;
   int h_dtype, y_dtype;
   int y_parts;           // fp32 partial buffers reserved for a K-split down GEMM
   int64_t y_part_elems;  // elements per partial
@@ -312,18 +313,21 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   const bool a8 = prefill && block_wdt == FMOE_F8E4M3FN_A8 && H % 128 == 0 && F % 128 == 0 && H <= 16384 &&
                   F <= 16384;
   const bool kb_candidate = prefill && !a8 && H % 64 == 0 && F % 64 == 0 && (F + 127) / 128 >= 16;
-  L.ttab = off;
-  L.ttab_bytes = 0;
+  L.ttab_g_bytes = 0;
+  L.ttab_d_bytes = 0;
   if (prefill) {
     GroupedGemmArgs gs = down_shape(T, E, k, H, F, act, wdt);
-    const size_t down_bytes = gemm_tiled256_table_bytes(gs);
+    L.ttab_d_bytes = gemm_tiled256_table_bytes(gs);
     gs.epi = EPI_SWIGLU;
     gs.N = F;
     gs.K = H;
     gs.split_stride = 0;
-    L.ttab_bytes = std::max(down_bytes, gemm_tiled256_table_bytes(gs));
+    L.ttab_g_bytes = gemm_tiled256_table_bytes(gs);
   }
-  off += align_up(L.ttab_bytes);
+  L.ttab_g = off;
+  off += align_up(L.ttab_g_bytes);
+  L.ttab_d = off;
+  off += align_up(L.ttab_d_bytes);
   L.xkb = off;
   L.xkb_bytes = kb_candidate ? static_cast<size_t>(n) * H * 2 : 0;
   off += align_up(L.xkb_bytes);
@@ -477,18 +481,13 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
                                   static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype,
                                   at<float>(workspace, L.rpart), ids, rw, order, offsets, err, s));
   } else {
-    {
-      ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
-      if (split_router)
-        FMOE_HIP(launch_router_prefill(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype,
-                                       at<float>(workspace, L.rpart), ids, rw, s));
-      else
-        FMOE_HIP(launch_router(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype, ids, rw,
-                               s));
-    }
-    ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
-    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err,
-                            at<int>(workspace, L.perm.scratch), s));
+    ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
+    if (split_router)
+      FMOE_HIP(launch_router_prefill(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype,
+                                     at<float>(workspace, L.rpart), ids, rw, s));
+    else
+      FMOE_HIP(launch_router(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype, ids, rw,
+                             s));
   }
 
   // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
@@ -538,7 +537,8 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   // The 256-tile down GEMM stores its weighted per-slot rows (and K-split
   // partials) in bf16, the activation type, halving the traffic of its
   // epilogue and of combine; the other paths keep fp32.
-  bool h_quant = false;
+  // Only decisions here: the launches that read the permutation follow it.
+  bool h_quant = false, gather_x = false;
   int y_dtype = L.y_dtype;
   GroupedGemmArgs dq = d;
   if (n > 8 * n_expert && act_dtype == FMOE_BF16) {
@@ -561,15 +561,6 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
       dk.act_dtype = DT_F8;
       dk.a_scale = at<float>(workspace, L.hs);
       if (both256 && gemm_tiled256_supported(gk) && gemm_tiled256_supported(dk)) {
-        ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
-        // max |x| per token (that pass also clears the per-row max the
-        // gate/up epilogue accumulates for h), then the token rows gathered
-        // into expert order and quantised.
-        FMOE_HIP(launch_row_absmax(c.input, T, static_cast<int>(n_embd), at<unsigned>(workspace, L.xmax),
-                                   at<unsigned>(workspace, L.hmax), n, s));
-        FMOE_HIP(launch_quantize_rows_kb(c.input, order, n, T, static_cast<int>(n_embd),
-                                         at<unsigned>(workspace, L.xmax), at<char>(workspace, L.xq),
-                                         at<float>(workspace, L.xs), nullptr, s));
         g = gk;
         dq = dk;
         h_quant = true;
@@ -580,35 +571,69 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
       // when many column tiles of the gate/up GEMM re-read them (measured:
       // Mixtral's 112 tiles gain 77 us for a 19 us gather, Qwen3's 6 tiles
       // lose 74 us at 8192 tokens).
-      const bool gather_x = (n_ff + 127) / 128 >= 16;
+      const bool want_gather = (n_ff + 127) / 128 >= 16;
       GroupedGemmArgs gh = g;  // gate/up reading the token rows in place
       gh.out_kb_rows = n;
-      if (gather_x) {
+      if (want_gather) {
         gk.a = at<char>(workspace, L.xkb);
         gk.out_kb_rows = n;
       }
-      GroupedGemmArgs& gsel = gather_x ? gk : gh;
+      GroupedGemmArgs& gsel = want_gather ? gk : gh;
       if (both256 && gemm_tiled256_supported(gsel) && gemm_tiled256_supported(dk)) {
-        if (gather_x) {
-          ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
-          FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd),
-                                         at<char>(workspace, L.xkb), s));
-        }
+        gather_x = want_gather;
         g = gsel;
         d = dk;
         y_dtype = FMOE_BF16;
       }
     }
     // The 256-tile GEMMs deal their tiles from a per-launch schedule table
-    // (ignored by the other kernel families).
+    // (ignored by the other kernel families), each in its reserved room,
+    // built by the permutation below where there is one.
     if (kTileTable) {
-      // only GEMMs the table applies to (nonzero size) and that fit the reserved room
-      int* ttab = at<int>(workspace, L.ttab);
-      for (GroupedGemmArgs* x : {&g, &d, &dq}) {
-        const size_t need = gemm_tiled256_table_bytes(*x);
-        if (need > 0 && need <= L.ttab_bytes) x->tile_table = ttab;
+      GroupedGemmArgs* dn = h_quant ? &dq : &d;
+      const struct {
+        GroupedGemmArgs* x;
+        size_t at, bytes;
+      } tabs[2] = {{&g, L.ttab_g, L.ttab_g_bytes}, {dn, L.ttab_d, L.ttab_d_bytes}};
+      for (const auto& tb : tabs) {
+        const size_t need = gemm_tiled256_table_bytes(*tb.x);
+        if (need > 0 && need <= tb.bytes) tb.x->tile_table = at<int>(workspace, tb.at);
       }
     }
+  }
+
+  if (!decode_router) {
+    // Tile schedules the permutation builds beside its scatter: those of the
+    // 256-tile GEMMs that will run.
+    TileTableReq reqs[kPermuteMaxTables];
+    int n_req = 0;
+    GroupedGemmArgs* dn = h_quant ? &dq : &d;
+    for (GroupedGemmArgs* x : {&g, dn}) {
+      if (!x->tile_table || !gemm_tiled256_table_request(*x, &reqs[n_req])) continue;
+      int v = 0;
+      const int path = pick_path(*x, &v);
+      if ((path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE) && v == TILED_256) {
+        x->tile_table_ready = true;
+        ++n_req;
+      }
+    }
+    ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
+    FMOE_HIP(launch_permute(ids, n, static_cast<int>(n_expert), order, offsets, err,
+                            at<int>(workspace, L.perm.scratch), s, reqs, n_req));
+  }
+  if (h_quant) {
+    ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
+    // max |x| per token (that pass also clears the per-row max the gate/up
+    // epilogue accumulates for h), then the token rows gathered into expert
+    // order and quantised.
+    FMOE_HIP(launch_row_absmax(c.input, T, static_cast<int>(n_embd), at<unsigned>(workspace, L.xmax),
+                               at<unsigned>(workspace, L.hmax), n, s));
+    FMOE_HIP(launch_quantize_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<unsigned>(workspace, L.xmax),
+                                     at<char>(workspace, L.xq), at<float>(workspace, L.xs), nullptr, s));
+  }
+  if (gather_x) {
+    ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
+    FMOE_HIP(launch_gather_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<char>(workspace, L.xkb), s));
   }
   {
     ScopedTimer t(FMOE_TIMER_GATE_UP, s, c.timers);

@@ -22,8 +22,9 @@
 // their own (thin_k_loop); fp8 weights take k_loop_f8.
 //
 // Tile order: each XCD works through a contiguous range of the tiles
-// (sched_tile), or, for wide gate/up GEMMs, through the list a one-block
-// kernel deals before the launch (tile_table_kernel).
+// (sched_tile), or, for GEMMs of 16 or more column tiles, through a list
+// dealt before the launch (tile_table.h) by the permutation or by a
+// one-block kernel (tile_table_kernel).
 //
 // LDS layouts: weight blocks are copied as packed (lane-ordered 1 KiB blocks,
 // conflict-free 16-byte reads); token rows are 64 B with the 16-byte chunk
@@ -32,6 +33,7 @@
 #include "common.h"
 #include "launch.h"
 #include "permute_block.h"
+#include "tile_table.h"
 
 namespace fmoe {
 namespace {
@@ -220,110 +222,23 @@ __device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, 
   return true;
 }
 
-// ---- Per-launch tile schedule (the block's prefill GEMMs).  The equal-count
-// XCD ranges above leave whole XCDs short of work when the experts' row
-// counts are skewed, and each XCD's last round partly empty.  This one-block
-// kernel deals the work longest first instead: a chunk is one (K split,
-// column group of kGroupN tiles, expert) with all the expert's row tiles,
-// costed per row tile as 375 + rows (a full tile 631: fixed setup, prologue,
-// epilogue and weight stream, plus its rows' MFMAs).  Chunks are sorted by
-// cost into 255 buckets (a stable counting sort, largest first; empty
-// chunks last) and dealt to the XCDs in snake order (0..7, 7..0, ...); each
-// XCD runs its chunks in that order, a chunk's tiles row tile by row tile
-// over its columns, so tiles sharing token rows or a weight slab stay on one
-// L2.  Entry b of the table is hardware block b's tile (XCD b % 8, position
-// b / 8 in that XCD's list): {expert, first row, rows, column | split << 16},
-// expert -1 for no tile.  If an XCD's list outgrows the grid, every entry
-// reads -2 and the kernel falls back to the in-kernel ranges.
-constexpr int kTabChunks = 2048;   // chunks a table covers (permute_block's limit)
-constexpr int kTableMinCols = 32;  // GEMMs with fewer column tiles keep the in-kernel ranges
-constexpr int kTabBuckets = 256;
-
-__host__ __device__ inline int table_blocks_per_xcd(int row_tiles_bound, int n_col, int ksplit) {
-  const int per = (row_tiles_bound * n_col * ksplit + 7) / 8;
-  return per + per / 4 + 1;
-}
-
-__device__ __forceinline__ int tile_cost(int rows) { return 375 + rows; }
-
-// Position in the sorted chunk order of the m-th chunk XCD x receives.
-__device__ __forceinline__ int snake_pos(int x, int m) { return m * 8 + ((m & 1) ? 7 - x : x); }
+// ---- Per-launch tile schedule (the block's prefill GEMMs), dealt longest
+// first over the XCDs (tile_table.h).  The permutation builds it beside its
+// scatter when the caller asks (GroupedGemmArgs::tile_table_ready); this
+// one-block kernel builds it otherwise.
+// GEMMs with fewer column tiles keep the in-kernel ranges: one with a table
+// the permutation built, and one with a table this launcher builds first.
+constexpr int kTableMinCols = 16;
+constexpr int kTableMinColsOwn = 32;
+static_assert(kBM == ttab::kBM && kGroupN == ttab::kGroupN, "the table deals this kernel's tiles");
 
 __global__ __launch_bounds__(perm::kThreads) void tile_table_kernel(const int* __restrict__ offsets, int n_expert,
                                                                      int n_col, int ksplit, int bpx,
                                                                      int4* __restrict__ table) {
-  __shared__ int e_off[kSchedExperts], e_rows[kSchedExperts], e_cost[kSchedExperts];
-  __shared__ int bucket[kTabChunks], srt[kTabChunks], boff[kTabBuckets + 1], berr;
-  __shared__ int pref[8][kTabChunks / 8 + 1];
-  __shared__ int max_cost;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1), wave = tid / kWave;
-  const int n_groups = (n_col + kGroupN - 1) / kGroupN;
-  const int n_chunks = ksplit * n_groups * n_expert;
-  if (tid == 0) max_cost = 0;
-  for (int e = tid; e < n_expert; e += perm::kThreads) {
-    const int o = offsets[e], r = offsets[e + 1] - o;
-    const int nt = (r + kBM - 1) / kBM;
-    e_off[e] = o;
-    e_rows[e] = r;
-    e_cost[e] = nt == 0 ? 0 : (nt - 1) * tile_cost(kBM) + tile_cost(r - (nt - 1) * kBM);
-  }
+  __shared__ int rows[ttab::kMaxExperts];
+  for (int e = threadIdx.x; e < n_expert; e += perm::kThreads) rows[e] = offsets[e + 1] - offsets[e];
   __syncthreads();
-  for (int e = tid; e < n_expert; e += perm::kThreads) atomicMax(&max_cost, e_cost[e] * kGroupN);
-  __syncthreads();
-  // bucket 0 = the most expensive chunks, 254 the cheapest, 255 empty
-  for (int c = tid; c < n_chunks; c += perm::kThreads) {
-    const int e = c % n_expert, g = (c / n_expert) % n_groups;
-    const int cost = e_cost[e] * min(kGroupN, n_col - g * kGroupN);
-    bucket[c] = cost == 0 ? kTabBuckets - 1
-                          : kTabBuckets - 2 - static_cast<int>(static_cast<int64_t>(cost) * (kTabBuckets - 2) /
-                                                               (max_cost + 1));
-  }
-  __syncthreads();
-  perm::permute_block(bucket, n_chunks, kTabBuckets, srt, boff, &berr);
-  __syncthreads();
-  // pref[x][m]: tiles of XCD x's chunks before its m-th (one wave per XCD)
-  const int per_x = (n_chunks + 7) / 8;
-  if (wave < 8) {
-    const int x = wave;
-    int running = 0;
-    for (int m0 = 0; m0 < per_x; m0 += kWave) {
-      const int m = m0 + lane;
-      const int q = snake_pos(x, m);
-      int nt = 0;
-      if (m < per_x && q < n_chunks) {
-        const int c = srt[q];
-        const int e = c % n_expert, g = (c / n_expert) % n_groups;
-        nt = (e_rows[e] + kBM - 1) / kBM * min(kGroupN, n_col - g * kGroupN);
-      }
-      const int incl = wave_inclusive_scan(nt);
-      if (m < per_x) pref[x][m] = running + incl - nt;
-      running += __shfl(incl, kWave - 1, kWave);
-    }
-    if (lane == 0) pref[x][per_x] = running;
-  }
-  __syncthreads();
-  bool fits = true;
-#pragma unroll
-  for (int x = 0; x < 8; ++x) fits = fits && pref[x][per_x] <= bpx;
-  for (int b = tid; b < 8 * bpx; b += perm::kThreads) {
-    const int x = b % 8, p = b / 8;
-    int4 ent = make_int4(fits ? -1 : -2, 0, 0, 0);
-    if (fits && p < pref[x][per_x]) {
-      int lo = 0, hi = per_x - 1;  // the last m with pref[x][m] <= p
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if (pref[x][mid] <= p) lo = mid; else hi = mid - 1;
-      }
-      const int c = srt[snake_pos(x, lo)];
-      const int e = c % n_expert, g = (c / n_expert) % n_groups, sp = c / (n_expert * n_groups);
-      const int cig = min(kGroupN, n_col - g * kGroupN);
-      const int t = p - pref[x][lo];
-      const int r = t / cig;
-      ent = make_int4(e, e_off[e] + r * kBM, min(kBM, e_rows[e] - r * kBM), (g * kGroupN + t % cig) | (sp << 16));
-    }
-    table[b] = ent;
-  }
+  ttab::build(rows, n_expert, n_col, ksplit, bpx, table);
 }
 
 // The epilogue, staged through LDS so that every global store writes whole
@@ -1027,7 +942,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 
 template <int EPI, int NSETS, bool F8, bool A8>
 hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
-  // a table pointer on a GEMM the table does not cover is ignored
+  // A table pointer on a GEMM the table does not cover is ignored, and so is
+  // one this launcher would have to build itself for a narrow GEMM (its
+  // kernel costs about as much as the table gains there).
   GroupedGemmArgs g = g_in;
   if (g.tile_table && gemm_tiled256_table_bytes(g) == 0) g.tile_table = nullptr;
   constexpr int lds_bytes = F8 && !A8 ? kLdsF8 : kLds;
@@ -1042,10 +959,12 @@ hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
   const int col_tiles = static_cast<int>((g.N + kBN / NSETS - 1) / (kBN / NSETS));
   const int64_t total = static_cast<int64_t>(row_tiles) * col_tiles * g.ksplit;
   unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
+  if (g.tile_table && !g.tile_table_ready && col_tiles < kTableMinColsOwn) g.tile_table = nullptr;
   if (g.tile_table) {
-    const int bpx = table_blocks_per_xcd(row_tiles, col_tiles, g.ksplit);
-    hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(perm::kThreads), 0, s, g.offsets, g.n_expert, col_tiles,
-                       g.ksplit, bpx, reinterpret_cast<int4*>(g.tile_table));
+    const int bpx = ttab::blocks_per_xcd(row_tiles, col_tiles, g.ksplit);
+    if (!g.tile_table_ready)
+      hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(perm::kThreads), 0, s, g.offsets, g.n_expert, col_tiles,
+                         g.ksplit, bpx, reinterpret_cast<int4*>(g.tile_table));
     blocks = static_cast<unsigned>(8 * bpx);
   }
   hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8, A8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
@@ -1068,19 +987,33 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g) {
   return 1;
 }
 
-size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g) {
+bool gemm_tiled256_table_request(const GroupedGemmArgs& g, TileTableReq* r) {
   const int nsets = g.epi == EPI_SWIGLU ? 2 : 1;
   const int col_tiles = static_cast<int>((g.N + kBN / nsets - 1) / (kBN / nsets));
   const int ksplit = gemm_tiled256_ksplit(g);
   const int64_t chunks = static_cast<int64_t>(ksplit) * ((col_tiles + kGroupN - 1) / kGroupN) * g.n_expert;
   // Measured: with many column tiles (Mixtral's gate/up, 112) the table
-  // deals the work better (gate/up 1.47-1.48 -> 1.45 ms at T=4096); with few
-  // (Mixtral's down, 16: no change; Qwen3's 6 and 8: 4-13% slower) the
-  // equal-count ranges in the kernel are kept.
-  if (col_tiles < kTableMinCols) return 0;
-  if (g.n_expert <= 0 || g.n_expert > kSchedExperts || chunks > kTabChunks || col_tiles >= (1 << 16)) return 0;
+  // deals the work better (gate/up 1.47-1.48 -> 1.45 ms at T=4096); with
+  // Qwen3's 6 and 8 it was 4-13% slower and the equal-count ranges in the
+  // kernel are kept.
+  if (col_tiles < kTableMinCols || g.n_assign <= 0) return false;
+  if (g.n_expert <= 0 || g.n_expert > kSchedExperts || g.n_expert > ttab::kMaxExperts || chunks > ttab::kChunks ||
+      col_tiles >= (1 << 16))
+    return false;
   const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
-  return static_cast<size_t>(8) * table_blocks_per_xcd(row_tiles, col_tiles, ksplit) * 16;
+  if (r) {
+    r->table = g.tile_table;
+    r->n_col = col_tiles;
+    r->ksplit = ksplit;
+    r->bpx = ttab::blocks_per_xcd(row_tiles, col_tiles, ksplit);
+  }
+  return true;
+}
+
+size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g) {
+  TileTableReq r;
+  if (!gemm_tiled256_table_request(g, &r)) return 0;
+  return static_cast<size_t>(8) * r.bpx * 16;
 }
 
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {

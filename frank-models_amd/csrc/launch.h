@@ -138,9 +138,12 @@ struct GroupedGemmArgs {
   // as unsigned integers) into row_amax[p], which starts at zero.
   unsigned* row_amax = nullptr;
   // 256-tile kernel: workspace of gemm_tiled256_table_bytes(g) bytes for a
-  // per-launch tile schedule (built by a one-block kernel before the GEMM);
-  // nullptr, or a shape the table does not cover, keeps the in-kernel one.
+  // per-launch tile schedule; nullptr, or a shape the table does not cover,
+  // keeps the in-kernel one.  tile_table_ready: the permutation that wrote
+  // the offsets built the table too (launch_permute's tables); otherwise the
+  // launcher builds it with a one-block kernel first (wide GEMMs only).
   int* tile_table = nullptr;
+  bool tile_table_ready = false;
   ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
 };
 
@@ -183,12 +186,23 @@ hipError_t launch_router_prefill(const void* x, const void* wr, int n_tokens, in
                                  bool normalize, int dtype, float* part, int* ids, float* weights,
                                  hipStream_t stream);
 
+// A 256-tile GEMM's tile schedule for the permutation to build beside its
+// scatter (gemm_tiled256_table_request fills it; table: 8 * bpx int4 entries).
+struct TileTableReq {
+  int* table = nullptr;
+  int n_col = 0, ksplit = 1, bpx = 0;
+};
+constexpr int kPermuteMaxTables = 2;
+
 // Batches above kPermuteChunk assignments run chunked, with a histogram
-// scratch of permute_scratch_bytes() (0 for smaller batches).
+// scratch of permute_scratch_bytes() (0 for smaller batches).  Up to
+// kPermuteMaxTables tile schedules over the resulting offsets are built by
+// extra blocks of the same launch.
 constexpr int kPermuteChunk = 2048;
 size_t permute_scratch_bytes(int n_assign, int n_expert);
 hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order,
-                          int* offsets, int* err_count, int* scratch, hipStream_t stream);
+                          int* offsets, int* err_count, int* scratch, hipStream_t stream,
+                          const TileTableReq* tables = nullptr, int n_tables = 0);
 
 hipError_t launch_pack(const void* src, int src_dtype, const float* src_scales,
                        int n_out, int n_in, int n_expert, int dst_dtype, void* dst,
@@ -211,6 +225,9 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g);
 hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t stream);
 // K split the 256-tile kernel would use for g (1 when it does not apply).
 int gemm_tiled256_ksplit(const GroupedGemmArgs& g);
+// The tile schedule g would use (false: none; the shape keeps the in-kernel
+// one), with r->table = g.tile_table; and its size in bytes (0: none).
+bool gemm_tiled256_table_request(const GroupedGemmArgs& g, TileTableReq* r);
 size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g);
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,

@@ -22,9 +22,14 @@
 //   b. each chunk's block sums the histograms into the expert offsets and
 //      its own per-expert base (offset + the counts of earlier chunks), then
 //      runs step 3 over its chunk.  Chunk 0 writes the offsets.
+// A caller may also ask for the tile schedules of 256-tile GEMMs over the
+// resulting offsets (tile_table.h): one extra block per schedule in the same
+// launch counts the rows per expert itself and builds it while the scatter
+// runs.
 #include "common.h"
 #include "launch.h"
 #include "permute_block.h"
+#include "tile_table.h"
 
 namespace fmoe {
 namespace {
@@ -35,10 +40,29 @@ using perm::kMaxExpert;
 using perm::scatter_range;
 constexpr int kHistThreads = 256;
 
+struct TileTables {
+  TileTableReq r[kPermuteMaxTables];
+};
+
+// Blocks 1.. of the launch: the tile schedule over the counts of the valid
+// ids per expert (the offsets block 0 writes).
 __global__ __launch_bounds__(kThreads) void permute_kernel(const int* __restrict__ ids, int n,
                                                            int n_expert, int* __restrict__ order,
                                                            int* __restrict__ offsets,
-                                                           int* __restrict__ err_count) {
+                                                           int* __restrict__ err_count, TileTables tt) {
+  if (blockIdx.x > 0) {
+    __shared__ int rows[ttab::kMaxExperts];
+    for (int e = threadIdx.x; e < n_expert; e += kThreads) rows[e] = 0;
+    __syncthreads();
+    for (int f = threadIdx.x; f < n; f += kThreads) {
+      const int e = ids[f];
+      if (e >= 0 && e < n_expert) atomicAdd(&rows[e], 1);
+    }
+    __syncthreads();
+    const TileTableReq r = tt.r[blockIdx.x - 1];
+    ttab::build(rows, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table));
+    return;
+  }
   perm::permute_block(ids, n, n_expert, order, offsets, err_count);
 }
 
@@ -73,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __re
                                                                  int n_expert, const int* __restrict__ counts,
                                                                  int n_chunks, int* __restrict__ order,
                                                                  int* __restrict__ offsets,
-                                                                 int* __restrict__ err_count) {
+                                                                 int* __restrict__ err_count, TileTables tt) {
   __shared__ int base[kMaxExpert];
   __shared__ int total[kMaxExpert];
   __shared__ int wcnt[kWaves][kMaxExpert];
@@ -83,6 +107,24 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __re
   const int chunk = blockIdx.x;
   const int stride = n_expert + 1;
 
+  if (chunk >= n_chunks) {
+    // a tile schedule over the per-expert totals of the histograms
+    for (int e = tid; e < n_expert; e += kThreads) {
+      int tot = 0;
+      for (int c0 = 0; c0 < n_chunks; c0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = c0 + q < n_chunks ? counts[(c0 + q) * stride + e] : 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) tot += v[q];
+      }
+      total[e] = tot;
+    }
+    __syncthreads();
+    const TileTableReq r = tt.r[chunk - n_chunks];
+    ttab::build(total, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table));
+    return;
+  }
   for (int e = tid; e < n_expert; e += kThreads) {
     // eight chunks' counts in flight at a time
     int tot = 0, pre = 0;
@@ -139,19 +181,31 @@ size_t permute_scratch_bytes(int n_assign, int n_expert) {
 }
 
 hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order, int* offsets,
-                          int* err_count, int* scratch, hipStream_t stream) {
+                          int* err_count, int* scratch, hipStream_t stream, const TileTableReq* tables,
+                          int n_tables) {
   if (n_expert > kMaxExpert || n_expert <= 0) return hipErrorInvalidValue;
+  if (n_tables < 0 || n_tables > kPermuteMaxTables || (n_tables > 0 && !tables)) return hipErrorInvalidValue;
+  TileTables tt;
+  for (int i = 0; i < n_tables; ++i) {
+    const TileTableReq& r = tables[i];
+    const int64_t chunks = static_cast<int64_t>(r.ksplit) * ((r.n_col + ttab::kGroupN - 1) / ttab::kGroupN) * n_expert;
+    if (!r.table || r.n_col <= 0 || r.n_col >= (1 << 16) || r.ksplit <= 0 || r.bpx <= 0 ||
+        n_expert > ttab::kMaxExperts || chunks > ttab::kChunks ||
+        r.bpx != ttab::blocks_per_xcd(max_row_tiles(n_assign, n_expert, ttab::kBM), r.n_col, r.ksplit))
+      return hipErrorInvalidValue;
+    tt.r[i] = r;
+  }
   if (n_assign <= kPermuteChunk) {
-    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
-                       order, offsets, err_count);
+    hipLaunchKernelGGL(permute_kernel, dim3(1 + n_tables), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
+                       order, offsets, err_count, tt);
     return hipGetLastError();
   }
   if (!scratch) return hipErrorInvalidValue;
   const int chunks = (n_assign + kPermuteChunk - 1) / kPermuteChunk;
   hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks), dim3(kHistThreads), 0, stream, ids, n_assign, n_expert,
                      scratch);
-  hipLaunchKernelGGL(chunk_scatter_kernel, dim3(chunks), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
-                     scratch, chunks, order, offsets, err_count);
+  hipLaunchKernelGGL(chunk_scatter_kernel, dim3(chunks + n_tables), dim3(kThreads), 0, stream, ids, n_assign,
+                     n_expert, scratch, chunks, order, offsets, err_count, tt);
   return hipGetLastError();
 }
 

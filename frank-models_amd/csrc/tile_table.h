@@ -1,0 +1,139 @@
+// Device code of the per-launch tile schedule of the 256x256-tile grouped
+// GEMM (gemm_tiled256.hip), shared by the GEMM's own one-block table kernel
+// and the permutation kernels, which build it beside their scatter
+// (permute.hip) so that it costs no launch of its own.
+//
+// The GEMM's in-kernel schedule gives each XCD an equal count of row tiles;
+// with skewed expert row counts that leaves whole XCDs short of work and
+// each XCD's last round partly empty.  The table deals the work longest
+// first instead: a chunk is one (K split, column group of kGroupN tiles,
+// expert) with all the expert's row tiles, costed per row tile as
+// 375 + rows (a full tile 631: fixed setup, prologue, epilogue and weight
+// stream, plus its rows' MFMAs).  Chunks are sorted by cost into 255
+// buckets (a stable counting sort, largest first; empty chunks last) and
+// dealt to the XCDs in snake order (0..7, 7..0, ...); each XCD runs its
+// chunks in that order, a chunk's tiles row tile by row tile over its
+// columns, so tiles sharing token rows or a weight slab stay on one L2.
+// Entry b of the table is hardware block b's tile (XCD b % 8, position
+// b / 8 in that XCD's list): {expert, first row, rows, column | split << 16},
+// expert -1 for no tile.  If an XCD's list outgrows the grid, every entry
+// reads -2 and the GEMM falls back to its in-kernel schedule.
+#pragma once
+#include "common.h"
+#include "launch.h"
+#include "permute_block.h"
+
+namespace fmoe {
+namespace {
+namespace ttab {
+
+constexpr int kBM = 256;        // assignment rows per tile
+constexpr int kGroupN = 4;      // column tiles per chunk
+constexpr int kChunks = 2048;   // chunks a table covers (permute_block's limit)
+constexpr int kBuckets = 256;
+constexpr int kMaxExperts = 256;
+static_assert(kMaxExperts <= perm::kThreads, "one thread per expert");
+
+__host__ __device__ inline int blocks_per_xcd(int row_tiles_bound, int n_col, int ksplit) {
+  const int per = (row_tiles_bound * n_col * ksplit + 7) / 8;
+  return per + per / 4 + 1;
+}
+
+__device__ __forceinline__ int tile_cost(int rows) { return 375 + rows; }
+
+// Position in the sorted chunk order of the m-th chunk XCD x receives.
+__device__ __forceinline__ int snake_pos(int x, int m) { return m * 8 + ((m & 1) ? 7 - x : x); }
+
+// The table of a GEMM over n_col column tiles and ksplit K splits whose
+// experts hold e_rows[e] rows (LDS, n_expert <= kMaxExperts entries, visible
+// to the whole block), in expert order; 8 * bpx entries.  Called by every
+// thread of a perm::kThreads block.
+__device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_col, int ksplit, int bpx,
+                                      int4* __restrict__ table) {
+  __shared__ int e_off[kMaxExperts], e_rows[kMaxExperts], e_cost[kMaxExperts];
+  __shared__ int bucket[kChunks], srt[kChunks], boff[kBuckets + 1], berr;
+  __shared__ int pref[8][kChunks / 8 + 1];
+  __shared__ int max_cost;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const int n_groups = (n_col + kGroupN - 1) / kGroupN;
+  const int n_chunks = ksplit * n_groups * n_expert;
+  if (wave == 0) {
+    // e_off: exclusive scan of the row counts; max_cost: the largest chunk's cost
+    int running = 0, mc = 0;
+    for (int c = 0; c < n_expert; c += kWave) {
+      const int e = c + lane;
+      const int r = e < n_expert ? e_rows_in[e] : 0;
+      const int incl = wave_inclusive_scan(r);
+      const int nt = (r + kBM - 1) / kBM;
+      const int cost = nt == 0 ? 0 : (nt - 1) * tile_cost(kBM) + tile_cost(r - (nt - 1) * kBM);
+      if (e < n_expert) {
+        e_off[e] = running + incl - r;
+        e_rows[e] = r;
+        e_cost[e] = cost;
+      }
+      mc = max(mc, cost);
+      running += __shfl(incl, kWave - 1, kWave);
+    }
+    for (int o = kWave / 2; o > 0; o >>= 1) mc = max(mc, __shfl_xor(mc, o, kWave));
+    if (lane == 0) max_cost = mc * kGroupN;
+  }
+  __syncthreads();
+  // bucket 0 = the most expensive chunks, kBuckets - 2 the cheapest, kBuckets - 1 empty
+  for (int c = tid; c < n_chunks; c += perm::kThreads) {
+    const int e = c % n_expert, g = (c / n_expert) % n_groups;
+    const int cost = e_cost[e] * min(kGroupN, n_col - g * kGroupN);
+    bucket[c] = cost == 0 ? kBuckets - 1
+                          : kBuckets - 2 - static_cast<int>(static_cast<int64_t>(cost) * (kBuckets - 2) /
+                                                            (max_cost + 1));
+  }
+  __syncthreads();
+  perm::permute_block(bucket, n_chunks, kBuckets, srt, boff, &berr);
+  __syncthreads();
+  // pref[x][m]: tiles of XCD x's chunks before its m-th (one wave per XCD)
+  const int per_x = (n_chunks + 7) / 8;
+  if (wave < 8) {
+    const int x = wave;
+    int running = 0;
+    for (int m0 = 0; m0 < per_x; m0 += kWave) {
+      const int m = m0 + lane;
+      const int q = snake_pos(x, m);
+      int nt = 0;
+      if (m < per_x && q < n_chunks) {
+        const int c = srt[q];
+        const int e = c % n_expert, g = (c / n_expert) % n_groups;
+        nt = (e_rows[e] + kBM - 1) / kBM * min(kGroupN, n_col - g * kGroupN);
+      }
+      const int incl = wave_inclusive_scan(nt);
+      if (m < per_x) pref[x][m] = running + incl - nt;
+      running += __shfl(incl, kWave - 1, kWave);
+    }
+    if (lane == 0) pref[x][per_x] = running;
+  }
+  __syncthreads();
+  bool fits = true;
+#pragma unroll
+  for (int x = 0; x < 8; ++x) fits = fits && pref[x][per_x] <= bpx;
+  for (int b = tid; b < 8 * bpx; b += perm::kThreads) {
+    const int x = b % 8, p = b / 8;
+    int4 ent = make_int4(fits ? -1 : -2, 0, 0, 0);
+    if (fits && p < pref[x][per_x]) {
+      int lo = 0, hi = per_x - 1;  // the last m with pref[x][m] <= p
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (pref[x][mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      const int c = srt[snake_pos(x, lo)];
+      const int e = c % n_expert, g = (c / n_expert) % n_groups, sp = c / (n_expert * n_groups);
+      const int cig = min(kGroupN, n_col - g * kGroupN);
+      const int t = p - pref[x][lo];
+      const int r = t / cig;
+      ent = make_int4(e, e_off[e] + r * kBM, min(kBM, e_rows[e] - r * kBM), (g * kGroupN + t % cig) | (sp << 16));
+    }
+    table[b] = ent;
+  }
+}
+
+}  // namespace ttab
+}  // namespace
+}  // namespace fmoe

@@ -163,11 +163,14 @@ def test_prefill_split_router_shapes(fm, wl, name, H, F, T, E, k):
     assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
 
 
-# Gate/up GEMMs with at least 32 column tiles (n_ff >= 4096) take their tiles
-# from the per-launch schedule table: uniform and Zipf-skewed routing, a ragged
-# batch, and (C5) fp8 weights.
+# Prefill GEMMs with at least 16 column tiles (gate/up: n_ff >= 2048; down:
+# n_embd >= 4096) take their tiles from a per-launch schedule table that the
+# permutation builds: uniform and Zipf-skewed routing, a ragged batch, (C5)
+# fp8 weights, one table from the one-block permutation (T=700) and from the
+# chunked one (T=1500), and a down-only table (n_ff 256, n_embd 4096).
 @pytest.mark.parametrize("name,H,F,T,E,k", [
     ("C2", 256, 4096, 700, 8, 2), ("C3", 256, 4096, 1500, 64, 6), ("C5", 256, 4096, 333, 8, 2),
+    ("C2", 4096, 256, 300, 8, 2),
 ])
 def test_tile_table_shapes(fm, wl, name, H, F, T, E, k):
     cfg = _scaled(wl, name, H, F, n_expert=E, n_expert_used=k, margin=1e-4)
