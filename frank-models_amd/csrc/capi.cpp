@@ -646,6 +646,24 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
     d = dq;
   }
 
+  // Decode batches of at most 16 assignments on the streaming kernel (the
+  // automatic kernel choice): steps 9-11 in one launch.
+  if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && n <= 16) {
+    int vd = 0;
+    if (pick_path(d, &vd) == FMOE_PATH_STREAM) {
+      hipError_t e;
+      {
+        ScopedTimer t(FMOE_TIMER_DOWN, s, c.timers);
+        e = launch_down_combine_small(d, c.residual, c.out, act_dtype, T, static_cast<int>(n_expert_used), s);
+      }
+      if (e == hipSuccess) {
+        g_last_path = FMOE_PATH_STREAM;
+        return ok();
+      }
+      if (e != hipErrorNotSupported) return fail(FMOE_ERR_HIP, "down + combine launch: %s", hipGetErrorString(e));
+    }
+  }
+
   // Steps 9-10: down projection, routing weight applied per assignment (mlir:158-177).
   int down_split = 1;
   {

@@ -498,6 +498,168 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   }
 }
 
+// ============================================================ down + combine
+// Decode batches whose n_assign = n_tokens * k assignments fit one 16-row
+// MFMA tile (n_assign <= 16): the down projection and the slot-ordered
+// combine (moe_ffn_block.mlir:158-206) in one launch.  Block = 16 output
+// columns; its 16 waves take (active expert, K quarter) items, each the
+// arithmetic of one wave of gemm_stream_kernel (same quarters, same steps,
+// same MFMA sequence: the B tile holds all assignment rows, those of other
+// experts zeroed).  Then, through LDS, each assignment's quarters are added
+// in order, scaled and weighted as gemm_stream_kernel's epilogue does, and
+// the slots of each token are summed in slot order (plus the residual) as
+// combine_kernel does, with one rounding to bf16: the result is the
+// two-launch path's, bit for bit.  Every weight byte of the active experts'
+// 16-row slabs is read once; a block streams n_active slabs, so the
+// launcher takes this path only while that stays small.
+constexpr int kFcThreads = 1024;
+constexpr int kFcWaves = kFcThreads / kWave;
+constexpr int kFcRows = 16;                 // assignment rows (one MFMA tile)
+constexpr int kFcItems = 4 * kFcRows;       // (active expert, K quarter) items, at most
+constexpr int kFcUnroll = 12;               // 32-input steps per trip (a K quarter of 1408 inputs in one)
+// Weight bytes one block may stream, for a grid that fills the 256 CUs; a
+// smaller grid (n_embd / 16 blocks) takes proportionally less.  Measured
+// (whole block calls, cold, medians against the two launches): C2 T=1 127
+// against 136 us (917 KiB per block, 256 blocks), C5 T=1 80.2 against 84.8
+// us (458 KiB, 256), C3 T=1 38.8 against 41.1 us (196 KiB, 128), C4 T=1
+// 39.9 against 41.2 us (270 KiB, 128), C3 T=2 44.3 against 45.0 us (393 KiB,
+// 128); C4 T=2 (540 KiB, 128) 51.7 against 49.3 us, hence the scaling.
+constexpr int64_t kFcMaxBlockBytes = 1 << 20;
+
+template <bool F8>
+__global__ __launch_bounds__(kFcThreads) void down_combine_small_kernel(GroupedGemmArgs g, const bf16_t* residual,
+                                                                        bf16_t* out, int n_tokens, int k) {
+  __shared__ f32x4_t part[kFcItems][kWave];
+  __shared__ float ys[kFcRows][kStreamRows];  // weighted y of flat assignment f, the block's columns
+  __shared__ int act_e[kFcRows], act_off[kFcRows], act_cnt[kFcRows], row_act[kFcRows], n_act_s;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t N = g.N, K = g.K;
+  const int64_t nblocks = N / 16, nb = blockIdx.x;
+  const int64_t n_base = nb * kStreamRows;
+
+  // Active experts in ascending order (wave ballots over the offsets); rows
+  // of no expert (none, for valid ids) keep row_act = -1.
+  if (tid < kFcRows) {
+    row_act[tid] = -1;
+    for (int c = 0; c < kStreamRows; ++c) ys[tid][c] = 0.f;
+  }
+  if (wave == 0) {
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+    int n = 0;
+    for (int e0 = 0; e0 < g.n_expert; e0 += kWave) {
+      const int e = e0 + lane;
+      const int o = e < g.n_expert ? g.offsets[e] : 0;
+      const int c = e < g.n_expert ? g.offsets[e + 1] - o : 0;
+      const bool has = c > 0 && o >= 0 && o + c <= g.n_assign;
+      const uint64_t m = __ballot(has);
+      const int idx = n + __popcll(m & lt_mask);
+      if (has && idx < kFcRows) {
+        act_e[idx] = e;
+        act_off[idx] = o;
+        act_cnt[idx] = c;
+      }
+      n += __popcll(m);
+    }
+    if (lane == 0) n_act_s = min(n, kFcRows);
+  }
+  __syncthreads();
+  const int n_act = n_act_s;
+  if (tid < n_act)
+    for (int r = act_off[tid]; r < act_off[tid] + act_cnt[tid]; ++r) row_act[r] = tid;
+
+  const int64_t kblocks = F8 ? K / 64 : K / 32;
+  const int ksteps = static_cast<int>(K / 32);
+  const int unit = F8 ? 2 : 1;
+  const int units = ksteps / unit;
+  const int kq = (lane >> 4) * 8;
+  const int j = lane & 15;  // this lane's B row: assignment row j
+  const u32x4_t zero{0u, 0u, 0u, 0u};
+  for (int it = wave; it < 4 * n_act; it += kFcWaves) {
+    const int a = it >> 2, q = it & 3;
+    const int e = act_e[a];
+    const int ks_begin = (q * units / kStreamWaves) * unit;
+    const int ks_end = ((q + 1) * units / kStreamWaves) * unit;
+    const bool mine = j >= act_off[a] && j < act_off[a] + act_cnt[a];
+    const bf16_t* arow = static_cast<const bf16_t*>(g.a) + a_source_row(g, mine ? j : act_off[a]) * g.lda + kq;
+    const unsigned char* wsrc =
+        static_cast<const unsigned char*>(g.w0) + ((static_cast<int64_t>(e) * nblocks + nb) * kblocks) * 1024 + lane * 16;
+    f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+    for (int ks = ks_begin; ks < ks_end; ks += kFcUnroll) {
+      u32x4_t wv[kFcUnroll];
+      if (F8) {
+        u32x4_t qv[kFcUnroll / 2];
+#pragma unroll
+        for (int u = 0; u < kFcUnroll; u += 2)
+          qv[u / 2] = ks + u < ks_end
+                          ? stream_load(reinterpret_cast<const u32x4_t*>(wsrc + static_cast<int64_t>((ks + u) / 2) * 1024))
+                          : zero;
+#pragma unroll
+        for (int u = 0; u < kFcUnroll; u += 2) f8x16_to_bf16(qv[u / 2], wv[u], wv[u + 1]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < kFcUnroll; ++u)
+          wv[u] = ks + u < ks_end
+                      ? stream_load(reinterpret_cast<const u32x4_t*>(wsrc + static_cast<int64_t>(ks + u) * 1024))
+                      : zero;
+      }
+      u32x4_t tok[kFcUnroll];
+#pragma unroll
+      for (int u = 0; u < kFcUnroll; ++u)
+        tok[u] = (mine && ks + u < ks_end) ? *reinterpret_cast<const u32x4_t*>(arow + (ks + u) * 32) : zero;
+#pragma unroll
+      for (int u = 0; u < kFcUnroll; ++u)
+        if (ks + u < ks_end) acc = mfma16(wv[u], tok[u], acc);
+    }
+    part[it][lane] = acc;
+  }
+  __syncthreads();
+
+  // Lane L of wave 0: assignment row L % 16, columns 4 (L / 16) .. + 3.
+  if (wave == 0) {
+    const int a = row_act[j];
+    if (a >= 0) {
+      f32x4_t acc = part[4 * a][lane];
+#pragma unroll
+      for (int q = 1; q < 4; ++q) acc += part[4 * a + q][lane];
+      const int c = 4 * (lane >> 4);
+      const int64_t n = n_base + c;
+      float4 sc{1.f, 1.f, 1.f, 1.f};
+      if (F8) sc = *reinterpret_cast<const float4*>(g.s0 + static_cast<int64_t>(act_e[a]) * N + n);
+      const int f = g.order[j];
+      if (f >= 0 && f < g.n_assign) {
+        const float w = g.route_w[f];
+        float v0 = acc[0] * sc.x, v1 = acc[1] * sc.y, v2 = acc[2] * sc.z, v3 = acc[3] * sc.w;
+        v0 *= w, v1 *= w, v2 *= w, v3 *= w;
+        ys[f][c] = v0, ys[f][c + 1] = v1, ys[f][c + 2] = v2, ys[f][c + 3] = v3;
+      }
+    }
+  }
+  __syncthreads();
+  // out[t, 4 columns]: slots in order, then the residual, one rounding
+  if (tid < n_tokens * 4) {
+    const int t = tid >> 2, c = 4 * (tid & 3);
+    float acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = ys[t][c + i];
+    for (int sl = 1; sl < k; ++sl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + ys[sl * n_tokens + t][c + i];
+    const int64_t o = static_cast<int64_t>(t) * N + n_base + c;
+    if (residual) {
+      const u32x2_t r = *reinterpret_cast<const u32x2_t*>(residual + o);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t h = r[i / 2];
+        const float pv = __uint_as_float((i & 1) ? (h & 0xFFFF0000u) : (h << 16));
+        acc[i] = pv + acc[i];
+      }
+    }
+    *reinterpret_cast<u32x2_t*>(out + o) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+  }
+}
+
 // The grouping of assignment rows: order + offsets, or (streaming kernel
 // only, identity_ok) neither, for one expert whose rows are read in order.
 bool grouping_ok(const GroupedGemmArgs& g, bool identity_ok) {
@@ -646,6 +808,30 @@ hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t s) {
   if (!gemm_stream_supported(g)) return hipErrorNotSupported;
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
   return g.w_dtype == DT_F8 ? launch_stream_t<true>(g, s) : launch_stream_t<false>(g, s);
+}
+
+hipError_t launch_down_combine_small(const GroupedGemmArgs& d, const void* residual, void* out, int out_dtype,
+                                     int n_tokens, int k, hipStream_t s) {
+  GroupedGemmArgs g = d;
+  g.ksplit = 1;
+  if (g.epi != EPI_SCATTER_WEIGHTED || g.out_dtype != DT_F32 || out_dtype != DT_BF16 || !g.order || !g.offsets ||
+      !g.route_w || !gemm_stream_supported(g) || g.a_mode != A_DIRECT)
+    return hipErrorNotSupported;
+  if (n_tokens <= 0 || k <= 0 || g.n_assign != n_tokens * k || g.n_assign > kFcRows) return hipErrorNotSupported;
+  if (g.N % 4 || reinterpret_cast<uintptr_t>(out) % 8 || reinterpret_cast<uintptr_t>(residual) % 8)
+    return hipErrorNotSupported;
+  const int64_t slabs = g.n_assign < g.n_expert ? g.n_assign : g.n_expert;
+  const int64_t block_bytes = slabs * kStreamRows * g.K * (g.w_dtype == DT_F8 ? 1 : 2);
+  const int64_t blocks = g.N / kStreamRows;
+  if (block_bytes * 256 > kFcMaxBlockBytes * (blocks < 256 ? blocks : 256)) return hipErrorNotSupported;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (g.w_dtype == DT_F8)
+    hipLaunchKernelGGL(down_combine_small_kernel<true>, grid, dim3(kFcThreads), 0, s, g,
+                       static_cast<const bf16_t*>(residual), static_cast<bf16_t*>(out), n_tokens, k);
+  else
+    hipLaunchKernelGGL(down_combine_small_kernel<false>, grid, dim3(kFcThreads), 0, s, g,
+                       static_cast<const bf16_t*>(residual), static_cast<bf16_t*>(out), n_tokens, k);
+  return hipGetLastError();
 }
 
 }  // namespace fmoe

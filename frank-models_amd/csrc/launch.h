@@ -217,6 +217,14 @@ enum TiledVariant { TILED_AUTO = 0, TILED_128 = 1, TILED_256 = 2 };
 int resolve_tiled_variant(const GroupedGemmArgs& g, int variant);
 hipError_t launch_gemm_tiled(const GroupedGemmArgs& g, hipStream_t stream, int variant);
 hipError_t launch_gemm_stream(const GroupedGemmArgs& g, hipStream_t stream);
+// The block's down projection (d: EPI_SCATTER_WEIGHTED, fp32 per-slot rows,
+// streaming-kernel operands) fused with the combine for decode batches of
+// n_tokens * k <= 16 assignments: out (bf16 [n_tokens, d.N]) = [residual +]
+// the slot-ordered sum, bit-identical to launch_gemm_stream(d) followed by
+// launch_combine.  d.out is not written.  hipErrorNotSupported when the
+// batch or operands do not qualify (the caller then launches the two).
+hipError_t launch_down_combine_small(const GroupedGemmArgs& d, const void* residual, void* out, int out_dtype,
+                                     int n_tokens, int k, hipStream_t stream);
 bool gemm_tiled_supported(const GroupedGemmArgs& g);
 bool gemm_stream_supported(const GroupedGemmArgs& g);
 // 256x256-tile bf16 kernel (gemm_tiled256.hip); launch_gemm_tiled uses it

@@ -256,6 +256,56 @@ def test_fp8_activations_decode_keeps_bf16(fm, wl):
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+# ------------------------------------------------------------------ fused decode down + combine
+# Batches of at most 16 assignments take the down projection and the combine
+# in one launch under the automatic kernel choice; forcing the streaming
+# kernel gives the two-launch path.  The two agree bit for bit (the fused
+# kernel repeats the streaming kernel's K quarters, MFMA sequence and
+# epilogue, and the combine's slot order), and the fused launch is the one
+# that ran (no combine launch recorded).  C2 T=8 (8 Mixtral slabs per block)
+# and C4 T=2 (12 slabs on a grid of 128 blocks) stream more per block than
+# the fused kernel takes: they keep the two launches.
+@pytest.mark.parametrize("name,T,fused", [("C4", 1, True), ("C4", 2, False), ("C3", 2, True), ("C5", 1, True),
+                                          ("C2", 1, True), ("C2", 8, False)])
+def test_decode_down_combine_fused(fm, wl, gemm_path, name, T, fused):
+    cfg = wl.CONFIGS[name]
+    case = Case(fm, wl, cfg, T)
+    ll = gemm_path
+    ll.timing_read()
+    ll.timing_enable(True)
+    try:
+        a = case.run()
+        kern = ll.timing_read()
+    finally:
+        ll.timing_enable(False)
+    assert (kern["combine"][1] == 0) == fused, kern
+    _set_path(gemm_path, "stream")
+    b = case.run()
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(a, ref, cfg.rtol, what=f"{name} T={T}")
+
+
+def test_decode_down_combine_fused_sublayer(fm, wl, gemm_path):
+    """The sub-layer's residual add in the fused epilogue, out of place and in
+    place, against the two-launch path."""
+    cfg = wl.CONFIGS["C4"]
+    case = Case(fm, wl, cfg, 2)
+    nw = torch.ones(cfg.n_embd, dtype=torch.bfloat16, device="cuda")
+    outs = []
+    for p in ("auto", "stream"):
+        _set_path(gemm_path, p)
+        o = case.block.sublayer(case.x, nw, 1e-5)
+        r = case.x.clone()
+        case.block.sublayer(r, nw, 1e-5, out=r)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(o.float().cpu().numpy().view(np.uint32),
+                                      r.float().cpu().numpy().view(np.uint32))
+        outs.append(o.float().cpu().numpy())
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 # ------------------------------------------------------------------ properties
 def test_deterministic_and_token_order_equivariant(fm, wl, gemm_path):
     cfg = _scaled(wl, "C3", 256, 256)
