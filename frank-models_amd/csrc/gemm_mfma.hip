@@ -356,13 +356,16 @@ constexpr int kStreamWaves = kThreads / kWave;
 // keep the occupancy they reach anyway (6 for one tile spills).
 // The RoPE epilogue's double-precision angles need more registers; its
 // projection has one or two blocks per CU anyway.
-template <int EPI, int NSETS, int kStreamTiles>
+// U: 32-input steps per trip (kStreamUnroll, or 16 for the one-tile bf16
+// gate/up kernel, whose wave then loads its whole share of a 2048-input axis
+// in one trip at 2 waves per SIMD).
+template <int EPI, int NSETS, int kStreamTiles, int U>
 constexpr int stream_waves_per_eu() {
-  return EPI == EPI_QKV_ROPE ? 2 : NSETS == 2 ? 3 : kStreamTiles == 1 ? 5 : 4;
+  return EPI == EPI_QKV_ROPE ? 2 : U > kStreamUnroll ? 2 : NSETS == 2 ? 3 : kStreamTiles == 1 ? 5 : 4;
 }
 
-template <int EPI, int NSETS, bool F8, int kStreamTiles>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<EPI, NSETS, kStreamTiles>())))
+template <int EPI, int NSETS, bool F8, int kStreamTiles, int U = kStreamUnroll>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<EPI, NSETS, kStreamTiles, U>())))
 void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   __shared__ f32x4_t partial[kStreamWaves - 1][kStreamTiles][NSETS][kWave];
   const int e = blockIdx.x / col_tiles;
@@ -416,25 +419,25 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
 #pragma unroll
       for (int s = 0; s < NSETS; ++s) acc[mt][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // kStreamUnroll steps per trip, all loads first; a short last trip is
+    // U steps per trip, all loads first; a short last trip is
     // predicated per step (wave-uniform), so it keeps its loads in flight too.
-    for (int ks = ks_begin; ks < ks_end; ks += kStreamUnroll) {
-      u32x4_t wv[NSETS][kStreamUnroll];
+    for (int ks = ks_begin; ks < ks_end; ks += U) {
+      u32x4_t wv[NSETS][U];
 #pragma unroll
       for (int s = 0; s < NSETS; ++s) {
         if (F8) {
           // all loads, then all conversions (a conversion waits for its load)
-          u32x4_t q[kStreamUnroll / 2];
+          u32x4_t q[U / 2];
 #pragma unroll
-          for (int u = 0; u < kStreamUnroll; u += 2)
+          for (int u = 0; u < U; u += 2)
             q[u / 2] = ks + u < ks_end ? stream_load(reinterpret_cast<const u32x4_t*>(
                                              wsrc[s] + static_cast<int64_t>((ks + u) / 2) * 1024))
                                        : zero;
 #pragma unroll
-          for (int u = 0; u < kStreamUnroll; u += 2) f8x16_to_bf16(q[u / 2], wv[s][u], wv[s][u + 1]);
+          for (int u = 0; u < U; u += 2) f8x16_to_bf16(q[u / 2], wv[s][u], wv[s][u + 1]);
         } else {
 #pragma unroll
-          for (int u = 0; u < kStreamUnroll; ++u)
+          for (int u = 0; u < U; ++u)
             wv[s][u] = ks + u < ks_end
                            ? stream_load(reinterpret_cast<const u32x4_t*>(wsrc[s] + static_cast<int64_t>(ks + u) * 1024))
                            : zero;
@@ -443,12 +446,12 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
 #pragma unroll
       for (int mt = 0; mt < kStreamTiles; ++mt) {
         if (mt < nt) {
-          u32x4_t tok[kStreamUnroll];
+          u32x4_t tok[U];
 #pragma unroll
-          for (int u = 0; u < kStreamUnroll; ++u)
+          for (int u = 0; u < U; ++u)
             tok[u] = (r_ok[mt] && ks + u < ks_end) ? *reinterpret_cast<const u32x4_t*>(arow[mt] + (ks + u) * 32) : zero;
 #pragma unroll
-          for (int u = 0; u < kStreamUnroll; ++u)
+          for (int u = 0; u < U; ++u)
             if (ks + u < ks_end)
 #pragma unroll
               for (int s = 0; s < NSETS; ++s) acc[mt][s] = mfma16(wv[s][u], tok[u], acc[mt][s]);
@@ -710,6 +713,18 @@ hipError_t launch_tiled_t(const GroupedGemmArgs& g, hipStream_t s) {
 template <bool F8, int TILES>
 void launch_stream_tiles(const GroupedGemmArgs& g, hipStream_t s, dim3 grid, int col_tiles) {
   grid.y = g.ksplit > 1 ? g.ksplit : 1;
+  // The one-tile bf16 gate/up kernel loads 16 steps per trip (2 waves per
+  // SIMD) unless its blocks with rows (estimated: column tiles x experts
+  // that can have rows) would just overflow one round of 2 blocks per CU
+  // that 3 blocks per CU still hold.  Measured (whole block calls, cold):
+  // C2 T=16 gate/up 287 -> 278 us, C2 T=1 78 -> 75.5 us, C3 T=1 16.6 ->
+  // 15.7 us; C4 T=1 (528 blocks) 18.1 -> 19.5 us.  One-set (down) kernels
+  // were slower with it (C4 T=16 51 -> 61 us).
+  const int64_t active = static_cast<int64_t>(col_tiles) * (g.n_assign < g.n_expert ? g.n_assign : g.n_expert);
+  if (g.epi == EPI_SWIGLU && TILES == 1 && !F8 && !(active > 2 * 256 && active <= 3 * 256)) {
+    hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8, TILES, 16>), grid, dim3(kThreads), 0, s, g, col_tiles);
+    return;
+  }
   if (g.epi == EPI_SWIGLU)
     hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
   else if (g.epi == EPI_LINEAR)
