@@ -87,8 +87,9 @@ typedef enum fmoe_timer {
   FMOE_TIMER_ROUTER = 0,
   FMOE_TIMER_PERMUTE = 1,
   FMOE_TIMER_GATE_UP = 2, /* grouped GEMM: gate + up projections + SwiGLU */
-  FMOE_TIMER_DOWN = 3,    /* grouped GEMM: down projection + routing weight */
-  FMOE_TIMER_COMBINE = 4,
+  FMOE_TIMER_DOWN = 3,    /* grouped GEMM: down projection + routing weight (decode batches of
+                             at most 16 assignments: + the slot-ordered combine, one launch) */
+  FMOE_TIMER_COMBINE = 4, /* slot-ordered sum (+ residual); no launch where DOWN includes it */
   FMOE_TIMER_MUL_MAT_ID = 5,
   FMOE_TIMER_NORM = 6,    /* ffn_norm RMSNorm of the sub-layer */
   FMOE_TIMER_QKV = 7,     /* decode attention: Q/K/V projection + bias + RoPE */
