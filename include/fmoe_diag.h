@@ -26,6 +26,9 @@ typedef enum fmoe_gemm_path {
 /* Selects the grouped-GEMM kernel family (fmoe_gemm_path) for the whole
  * process (default AUTO).  A forced family that cannot run a given GEMM
  * (dtype, shape, alignment) falls back to the AUTO choice for that GEMM.
+ * Any forced family also keeps the block's down projection and combine as
+ * two launches (AUTO fuses them for decode batches of at most 16
+ * assignments, with the same results bit for bit).
  * FMOE_ERR_INVALID_ARGUMENT for an unknown value. */
 int fmoe_set_gemm_path(int path);
 int fmoe_get_gemm_path(void);
