@@ -44,13 +44,15 @@ struct TileTables {
   TileTableReq r[kPermuteMaxTables];
 };
 
-// Blocks 1.. of the launch: the tile schedule over the counts of the valid
-// ids per expert (the offsets block 0 writes).
+// Blocks 1.. of the launch (TABLES): the tile schedule over the counts of
+// the valid ids per expert (the offsets block 0 writes).  Without TABLES the
+// kernel holds none of the schedule's LDS.
+template <bool TABLES>
 __global__ __launch_bounds__(kThreads) void permute_kernel(const int* __restrict__ ids, int n,
                                                            int n_expert, int* __restrict__ order,
                                                            int* __restrict__ offsets,
                                                            int* __restrict__ err_count, TileTables tt) {
-  if (blockIdx.x > 0) {
+  if (TABLES && blockIdx.x > 0) {
     __shared__ int rows[ttab::kMaxExperts];
     for (int e = threadIdx.x; e < n_expert; e += kThreads) rows[e] = 0;
     __syncthreads();
@@ -93,6 +95,7 @@ __global__ __launch_bounds__(kHistThreads) void chunk_hist_kernel(const int* __r
     counts[static_cast<int64_t>(blockIdx.x) * (n_expert + 1) + e] = h[e];
 }
 
+template <bool TABLES>
 __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __restrict__ ids, int n,
                                                                  int n_expert, const int* __restrict__ counts,
                                                                  int n_chunks, int* __restrict__ order,
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __re
   const int chunk = blockIdx.x;
   const int stride = n_expert + 1;
 
-  if (chunk >= n_chunks) {
+  if (TABLES && chunk >= n_chunks) {
     // a tile schedule over the per-expert totals of the histograms
     for (int e = tid; e < n_expert; e += kThreads) {
       int tot = 0;
@@ -196,16 +199,24 @@ hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order
     tt.r[i] = r;
   }
   if (n_assign <= kPermuteChunk) {
-    hipLaunchKernelGGL(permute_kernel, dim3(1 + n_tables), dim3(kThreads), 0, stream, ids, n_assign, n_expert,
-                       order, offsets, err_count, tt);
+    if (n_tables > 0)
+      hipLaunchKernelGGL(permute_kernel<true>, dim3(1 + n_tables), dim3(kThreads), 0, stream, ids, n_assign,
+                         n_expert, order, offsets, err_count, tt);
+    else
+      hipLaunchKernelGGL(permute_kernel<false>, dim3(1), dim3(kThreads), 0, stream, ids, n_assign, n_expert, order,
+                         offsets, err_count, tt);
     return hipGetLastError();
   }
   if (!scratch) return hipErrorInvalidValue;
   const int chunks = (n_assign + kPermuteChunk - 1) / kPermuteChunk;
   hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks), dim3(kHistThreads), 0, stream, ids, n_assign, n_expert,
                      scratch);
-  hipLaunchKernelGGL(chunk_scatter_kernel, dim3(chunks + n_tables), dim3(kThreads), 0, stream, ids, n_assign,
-                     n_expert, scratch, chunks, order, offsets, err_count, tt);
+  if (n_tables > 0)
+    hipLaunchKernelGGL(chunk_scatter_kernel<true>, dim3(chunks + n_tables), dim3(kThreads), 0, stream, ids,
+                       n_assign, n_expert, scratch, chunks, order, offsets, err_count, tt);
+  else
+    hipLaunchKernelGGL(chunk_scatter_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream, ids, n_assign,
+                       n_expert, scratch, chunks, order, offsets, err_count, tt);
   return hipGetLastError();
 }
 
