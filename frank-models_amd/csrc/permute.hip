@@ -23,9 +23,9 @@
 //      its own per-expert base (offset + the counts of earlier chunks), then
 //      runs step 3 over its chunk.  Chunk 0 writes the offsets.
 // A caller may also ask for the tile schedules of 256-tile GEMMs over the
-// resulting offsets (tile_table.h): one extra block per schedule in the same
-// launch counts the rows per expert itself and builds it while the scatter
-// runs.
+// resulting offsets (tile_table.h): kTableParts extra blocks per schedule in
+// the same launch count the rows per expert themselves and build it while the
+// scatter runs, each writing a part of its entries.
 #include "common.h"
 #include "launch.h"
 #include "permute_block.h"
@@ -43,6 +43,8 @@ constexpr int kHistThreads = 256;
 struct TileTables {
   TileTableReq r[kPermuteMaxTables];
 };
+// Blocks per schedule: each sorts the chunks and writes a part of the entries.
+constexpr int kTableParts = 4;
 
 // Blocks 1.. of the launch (TABLES): the tile schedule over the counts of
 // the valid ids per expert (the offsets block 0 writes).  Without TABLES the
@@ -61,8 +63,10 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const int* __restrict
       if (e >= 0 && e < n_expert) atomicAdd(&rows[e], 1);
     }
     __syncthreads();
-    const TileTableReq r = tt.r[blockIdx.x - 1];
-    ttab::build(rows, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table));
+    const int i = static_cast<int>(blockIdx.x) - 1;
+    const TileTableReq r = tt.r[i / kTableParts];
+    ttab::build(rows, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table), i % kTableParts,
+                kTableParts);
     return;
   }
   perm::permute_block(ids, n, n_expert, order, offsets, err_count);
@@ -124,8 +128,10 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __re
       total[e] = tot;
     }
     __syncthreads();
-    const TileTableReq r = tt.r[chunk - n_chunks];
-    ttab::build(total, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table));
+    const int i = chunk - n_chunks;
+    const TileTableReq r = tt.r[i / kTableParts];
+    ttab::build(total, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table), i % kTableParts,
+                kTableParts);
     return;
   }
   for (int e = tid; e < n_expert; e += kThreads) {
@@ -200,7 +206,7 @@ hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order
   }
   if (n_assign <= kPermuteChunk) {
     if (n_tables > 0)
-      hipLaunchKernelGGL(permute_kernel<true>, dim3(1 + n_tables), dim3(kThreads), 0, stream, ids, n_assign,
+      hipLaunchKernelGGL(permute_kernel<true>, dim3(1 + kTableParts * n_tables), dim3(kThreads), 0, stream, ids, n_assign,
                          n_expert, order, offsets, err_count, tt);
     else
       hipLaunchKernelGGL(permute_kernel<false>, dim3(1), dim3(kThreads), 0, stream, ids, n_assign, n_expert, order,
@@ -212,7 +218,7 @@ hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order
   hipLaunchKernelGGL(chunk_hist_kernel, dim3(chunks), dim3(kHistThreads), 0, stream, ids, n_assign, n_expert,
                      scratch);
   if (n_tables > 0)
-    hipLaunchKernelGGL(chunk_scatter_kernel<true>, dim3(chunks + n_tables), dim3(kThreads), 0, stream, ids,
+    hipLaunchKernelGGL(chunk_scatter_kernel<true>, dim3(chunks + kTableParts * n_tables), dim3(kThreads), 0, stream, ids,
                        n_assign, n_expert, scratch, chunks, order, offsets, err_count, tt);
   else
     hipLaunchKernelGGL(chunk_scatter_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream, ids, n_assign,

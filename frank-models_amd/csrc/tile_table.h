@@ -47,9 +47,10 @@ __device__ __forceinline__ int snake_pos(int x, int m) { return m * 8 + ((m & 1)
 // The table of a GEMM over n_col column tiles and ksplit K splits whose
 // experts hold e_rows[e] rows (LDS, n_expert <= kMaxExperts entries, visible
 // to the whole block), in expert order; 8 * bpx entries.  Called by every
-// thread of a perm::kThreads block.
+// thread of a perm::kThreads block; with n_parts blocks on one table, each
+// sorts the chunks and writes part `part` of the entries.
 __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_col, int ksplit, int bpx,
-                                      int4* __restrict__ table) {
+                                      int4* __restrict__ table, int part = 0, int n_parts = 1) {
   __shared__ int e_off[kMaxExperts], e_rows[kMaxExperts], e_cost[kMaxExperts];
   __shared__ int bucket[kChunks], srt[kChunks], boff[kBuckets + 1], berr;
   __shared__ int pref[8][kChunks / 8 + 1];
@@ -114,7 +115,9 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_
   bool fits = true;
 #pragma unroll
   for (int x = 0; x < 8; ++x) fits = fits && pref[x][per_x] <= bpx;
-  for (int b = tid; b < 8 * bpx; b += perm::kThreads) {
+  const int per_part = (8 * bpx + n_parts - 1) / n_parts;
+  const int b_end = min(8 * bpx, (part + 1) * per_part);
+  for (int b = part * per_part + tid; b < b_end; b += perm::kThreads) {
     const int x = b % 8, p = b / 8;
     int4 ent = make_int4(fits ? -1 : -2, 0, 0, 0);
     if (fits && p < pref[x][per_x]) {
