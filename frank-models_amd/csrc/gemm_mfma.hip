@@ -719,7 +719,8 @@ void launch_stream_tiles(const GroupedGemmArgs& g, hipStream_t s, dim3 grid, int
   // that 3 blocks per CU still hold.  Measured (whole block calls, cold):
   // C2 T=16 gate/up 287 -> 278 us, C2 T=1 78 -> 75.5 us, C3 T=1 16.6 ->
   // 15.7 us; C4 T=1 (528 blocks) 18.1 -> 19.5 us.  One-set (down) kernels
-  // were slower with it (C4 T=16 51 -> 61 us).
+  // were slower with it (C4 T=16 51 -> 61 us), and so was the fp8-weight
+  // gate/up kernel (C5 T=16 144 -> 156 us, T=1 42.5 -> 47.8 us).
   const int64_t active = static_cast<int64_t>(col_tiles) * (g.n_assign < g.n_expert ? g.n_assign : g.n_expert);
   if (g.epi == EPI_SWIGLU && TILES == 1 && !F8 && !(active > 2 * 256 && active <= 3 * 256)) {
     hipLaunchKernelGGL((gemm_stream_kernel<EPI_SWIGLU, 2, F8, TILES, 16>), grid, dim3(kThreads), 0, s, g, col_tiles);
