@@ -230,7 +230,7 @@ __device__ __forceinline__ bool sched_tile(const GroupedGemmArgs& g, int n_col, 
 // the permutation built, and one with a table this launcher builds first.
 constexpr int kTableMinCols = 16;
 constexpr int kTableMinColsOwn = 32;
-static_assert(kBM == ttab::kBM && kGroupN == ttab::kGroupN, "the table deals this kernel's tiles");
+static_assert(kBM == ttab::kBM, "the table deals this kernel's tiles");
 
 __global__ __launch_bounds__(perm::kThreads) void tile_table_kernel(const int* __restrict__ offsets, int n_expert,
                                                                      int n_col, int ksplit, int bpx,
@@ -991,7 +991,7 @@ bool gemm_tiled256_table_request(const GroupedGemmArgs& g, TileTableReq* r) {
   const int nsets = g.epi == EPI_SWIGLU ? 2 : 1;
   const int col_tiles = static_cast<int>((g.N + kBN / nsets - 1) / (kBN / nsets));
   const int ksplit = gemm_tiled256_ksplit(g);
-  const int64_t chunks = static_cast<int64_t>(ksplit) * ((col_tiles + kGroupN - 1) / kGroupN) * g.n_expert;
+  const int64_t chunks = ttab::n_chunks(col_tiles, ksplit, g.n_expert);
   // Measured: with many column tiles (Mixtral's gate/up, 112) the table
   // deals the work better (gate/up 1.47-1.48 -> 1.45 ms at T=4096); with
   // Qwen3's 6 and 8 it was 4-13% slower and the equal-count ranges in the

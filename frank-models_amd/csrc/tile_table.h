@@ -6,7 +6,7 @@
 // The GEMM's in-kernel schedule gives each XCD an equal count of row tiles;
 // with skewed expert row counts that leaves whole XCDs short of work and
 // each XCD's last round partly empty.  The table deals the work longest
-// first instead: a chunk is one (K split, column group of kGroupN tiles,
+// first instead: a chunk is one (K split, column group of group_cols tiles,
 // expert) with all the expert's row tiles, costed per row tile as
 // 375 + rows (a full tile 631: fixed setup, prologue, epilogue and weight
 // stream, plus its rows' MFMAs).  Chunks are sorted by cost into 255
@@ -28,7 +28,6 @@ namespace {
 namespace ttab {
 
 constexpr int kBM = 256;        // assignment rows per tile
-constexpr int kGroupN = 4;      // column tiles per chunk
 constexpr int kChunks = 2048;   // chunks a table covers (permute_block's limit)
 constexpr int kBuckets = 256;
 constexpr int kMaxExperts = 256;
@@ -37,6 +36,20 @@ static_assert(kMaxExperts <= perm::kThreads, "one thread per expert");
 __host__ __device__ inline int blocks_per_xcd(int row_tiles_bound, int n_col, int ksplit) {
   const int per = (row_tiles_bound * n_col * ksplit + 7) / 8;
   return per + per / 4 + 1;
+}
+
+// Column tiles per chunk.  A chunk's tiles run side by side on one XCD; 8
+// columns x an expert's ~4 row tiles share more of each stage's token rows
+// and weight slabs in L2 than 4 x 4 (measured at Mixtral's gate/up, 112
+// columns: 5.08 against 6.63 GB fetched per launch, the same time), but on
+// a narrow GEMM the coarser chunks balance the XCDs worse (Mixtral's down,
+// 16 columns: 766 against 754 us).
+__host__ __device__ inline int group_cols(int n_col) { return n_col >= 64 ? 8 : 4; }
+
+// Chunks of a table (K splits x column groups x experts).
+__host__ __device__ inline int64_t n_chunks(int n_col, int ksplit, int n_expert) {
+  const int gc = group_cols(n_col);
+  return static_cast<int64_t>(ksplit) * ((n_col + gc - 1) / gc) * n_expert;
 }
 
 __device__ __forceinline__ int tile_cost(int rows) { return 375 + rows; }
@@ -57,7 +70,8 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_
   __shared__ int max_cost;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wave = tid / kWave;
-  const int n_groups = (n_col + kGroupN - 1) / kGroupN;
+  const int gcols = group_cols(n_col);
+  const int n_groups = (n_col + gcols - 1) / gcols;
   const int n_chunks = ksplit * n_groups * n_expert;
   if (wave == 0) {
     // e_off: exclusive scan of the row counts; max_cost: the largest chunk's cost
@@ -77,13 +91,13 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_
       running += __shfl(incl, kWave - 1, kWave);
     }
     for (int o = kWave / 2; o > 0; o >>= 1) mc = max(mc, __shfl_xor(mc, o, kWave));
-    if (lane == 0) max_cost = mc * kGroupN;
+    if (lane == 0) max_cost = mc * gcols;
   }
   __syncthreads();
   // bucket 0 = the most expensive chunks, kBuckets - 2 the cheapest, kBuckets - 1 empty
   for (int c = tid; c < n_chunks; c += perm::kThreads) {
     const int e = c % n_expert, g = (c / n_expert) % n_groups;
-    const int cost = e_cost[e] * min(kGroupN, n_col - g * kGroupN);
+    const int cost = e_cost[e] * min(gcols, n_col - g * gcols);
     bucket[c] = cost == 0 ? kBuckets - 1
                           : kBuckets - 2 - static_cast<int>(static_cast<int64_t>(cost) * (kBuckets - 2) /
                                                             (max_cost + 1));
@@ -103,7 +117,7 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_
       if (m < per_x && q < n_chunks) {
         const int c = srt[q];
         const int e = c % n_expert, g = (c / n_expert) % n_groups;
-        nt = (e_rows[e] + kBM - 1) / kBM * min(kGroupN, n_col - g * kGroupN);
+        nt = (e_rows[e] + kBM - 1) / kBM * min(gcols, n_col - g * gcols);
       }
       const int incl = wave_inclusive_scan(nt);
       if (m < per_x) pref[x][m] = running + incl - nt;
@@ -128,10 +142,10 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_
       }
       const int c = srt[snake_pos(x, lo)];
       const int e = c % n_expert, g = (c / n_expert) % n_groups, sp = c / (n_expert * n_groups);
-      const int cig = min(kGroupN, n_col - g * kGroupN);
+      const int cig = min(gcols, n_col - g * gcols);
       const int t = p - pref[x][lo];
       const int r = t / cig;
-      ent = make_int4(e, e_off[e] + r * kBM, min(kBM, e_rows[e] - r * kBM), (g * kGroupN + t % cig) | (sp << 16));
+      ent = make_int4(e, e_off[e] + r * kBM, min(kBM, e_rows[e] - r * kBM), (g * gcols + t % cig) | (sp << 16));
     }
     table[b] = ent;
   }
