@@ -807,6 +807,25 @@ hipError_t launch_router_decode(const void* x, const void* wr, int n_tokens, int
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int nv = (n_expert + 15) / 16;
+  if (n_expert > 64 && n_tokens > 32) {
+    // Many experts and tokens: one block's waves would select every token's
+    // experts on one CU's 4 SIMDs (C3 T=64: 14.5 us for the fused kernel).
+    // The prefill top-k (same partial layout, splits summed in the same
+    // order) spreads the tokens over blocks; the one-block permutation
+    // follows as its own launch.  Measured (whole block calls, cold): C3
+    // T=64 123.0 -> 119.4 us; at T=16 the fused kernel is ahead (77.3 against
+    // 78.8 us), its 4 waves one per SIMD.
+    const dim3 grid((n_tokens + 4 * kPartWaves - 1) / (4 * kPartWaves));
+    if (nv <= 8)
+      hipLaunchKernelGGL(router_part_topk_kernel<8>, grid, dim3(kPartWaves * kWave), 0, stream, part, n_split,
+                         n_tokens, n_expert, k, normalize ? 1 : 0, ids, weights);
+    else
+      hipLaunchKernelGGL(router_part_topk_kernel<16>, grid, dim3(kPartWaves * kWave), 0, stream, part, n_split,
+                         n_tokens, n_expert, k, normalize ? 1 : 0, ids, weights);
+    const hipError_t e2 = hipGetLastError();
+    if (e2 != hipSuccess) return e2;
+    return launch_permute(ids, k * n_tokens, n_expert, order, offsets, err_count, nullptr, stream);
+  }
   if (nv <= 1) return launch_topk_permute<1>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
   if (nv <= 2) return launch_topk_permute<2>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
   if (nv <= 4) return launch_topk_permute<4>(part, n_split, n_tokens, n_expert, k, normalize, ids, weights, order, offsets, err_count, stream);
