@@ -167,7 +167,9 @@ hipError_t launch_router(const void* x, const void* wr, int n_tokens, int n_embd
 // k <= 16): router logits split over many blocks into `part`
 // (router_decode_scratch_bytes, 0 when the shape does not qualify), then one
 // block runs softmax + top-k and the permutation (ids, weights, order,
-// offsets, err_count as launch_router + launch_permute write them).
+// offsets, err_count as launch_router + launch_permute write them); above 64
+// experts and 32 tokens the top-k runs over blocks and the permutation as a
+// launch of its own.
 // hipErrorNotSupported when the inputs do not qualify.
 constexpr int kDecodeMaxTokens = 64;
 size_t router_decode_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k, int dtype);

@@ -16,7 +16,8 @@
 //     summing the ranges' partial logits;
 //   * router_split_logits_kernel + router_topk_permute_kernel: decode-sized
 //     batches (logits split over many blocks, one block for top-k and the
-//     permutation);
+//     permutation; above 64 experts and 32 tokens router_part_topk_kernel
+//     over blocks, then the permutation's own launch);
 //   * router_simt_kernel: fp32 and the shapes above that none takes.
 // Softmax + top-k run four tokens per wave (16 lanes each, DPP row
 // reductions) for k <= 16, or one token per wave over its 64 lanes.
