@@ -23,7 +23,10 @@
 //           share weight rows run on the same XCD (same L2).
 //   stream  decode-sized batches: every weight block is read exactly once
 //           straight into MFMA registers (no LDS), 16 assignment rows per
-//           pass, 8 input steps of loads in flight per wave.
+//           pass, 8 input steps of loads in flight per wave (16 for the
+//           one-tile bf16 gate/up kernel).
+// And, for decode batches of at most 16 assignments, the down projection
+// fused with the slot-ordered combine (down_combine_small_kernel).
 #include "common.h"
 #include "launch.h"
 
@@ -344,7 +347,7 @@ constexpr int kStreamWaves = kThreads / kWave;
 // 4 waves split the input axis in four and their partial sums are added in
 // wave order through LDS, so even a handful of active experts keeps many
 // waves streaming.  Each wave streams its weight blocks from HBM straight
-// into MFMA registers (kStreamUnroll 1 KiB blocks per set in flight) and
+// into MFMA registers (U 1 KiB blocks per set in flight, below) and
 // applies each fragment to up to kStreamTiles 16-row tiles of the expert's
 // token rows, so an expert's weights are read once for up to
 // 16 * kStreamTiles rows.  An expert has at most n_tokens rows (top-k picks
