@@ -163,6 +163,21 @@ def test_prefill_split_router_shapes(fm, wl, name, H, F, T, E, k):
     assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
 
 
+# Decode batches of at most 4 tokens take the one-wave top-k + permutation:
+# odd token counts, the widest expert count per lane (up to 256 experts), and
+# k = 16 (64 assignments, one per lane).
+@pytest.mark.parametrize("name,H,F,T,E,k", [
+    ("C3", 256, 64, 1, 256, 8), ("C3", 256, 64, 3, 200, 8), ("C4", 256, 64, 4, 64, 16), ("C2", 256, 64, 2, 8, 2),
+])
+def test_decode_one_wave_router_shapes(fm, wl, name, H, F, T, E, k):
+    cfg = _scaled(wl, name, H, F, n_expert=E, n_expert_used=k, margin=1e-4)
+    case = Case(fm, wl, cfg, T)
+    out = case.run()
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
+
+
 # Prefill GEMMs with at least 16 column tiles (gate/up: n_ff >= 2048; down:
 # n_embd >= 4096) take their tiles from a per-launch schedule table that the
 # permutation builds: uniform and Zipf-skewed routing, a ragged batch, (C5)
