@@ -669,11 +669,12 @@ __global__ __launch_bounds__(perm::kThreads) void router_topk_permute_kernel(
 
 // Batches of at most 4 tokens and 64 assignments: one wave does what
 // router_topk_permute_kernel does with 16 (measured, whole block calls,
-// cold: C4 T=1 39.8 -> 38.85 us, T=4 80.2 -> 79.5 us).  Lane (g, j) sums the partials of
-// token g's experts j, j + 16, ... in split order (the same sums, so the same
-// ids); the permutation ranks each flat id f among the others: its position
-// is the number of ids of lower experts plus those of its expert before f,
-// the stable counting sort's order.
+// cold: C4 T=1 39.8 -> 38.85 us, T=4 80.2 -> 79.5 us).  Lane (g, j) sums
+// the partials of token g's experts j, j + 16, ... in split order (the same
+// sums, so the same ids); the permutation ranks each flat id f among the
+// others: its position is the number of ids of lower experts plus those of
+// its expert before f, the stable counting sort's order.  Top-k ids are
+// always valid experts, so the invalid-id count is zero.
 template <int NV>
 __global__ __launch_bounds__(kWave) void router_topk_permute_wave_kernel(
     const float* __restrict__ part, int n_split, int n_tokens, int n_expert, int k, int normalize,
