@@ -12,7 +12,7 @@ The JSON line carries:
   value / ms_per_step   whole-block throughput (tokens/s) over --steps calls,
                         bracketed by torch.cuda.synchronize()
   roofline              the dominant kernel alone (grouped gate+up GEMM): its
-                        average duration from HIP events recorded by the
+                        duration per call from HIP events recorded by the
                         library on the launch stream, algorithmic FLOPs per
                         launch against the dense bf16 MFMA peak (2.5 PFLOP/s);
                         traffic from the committed rocprofv3 PMC summary named
@@ -30,8 +30,11 @@ The JSON line carries:
   decode                C2 T=16 (the same as its configs row, kept as a field)
   cpu_baseline          the oracle's expert-grouped NumPy restatement (oracle/)
                         timed on this host's cores on a bounded token sample,
-                        all cores and one thread; the literal gather form where
-                        it fits; the CPU model; IREE llvm-cpu (not installed)
+                        all cores and one thread; the literal gather form at
+                        C1, C4 T=1/4/16/64, C3 T=64 and C2 T=16 (where one
+                        projection's gathered weights take at most 8 GB);
+                        medians of 3 runs; the CPU model; IREE llvm-cpu (not
+                        installed)
   attention_decode      the decode step's attention half at Mixtral's attention
                         shape (16 sequences x 4096 cached positions, paged
                         bf16 KV): ms/step, per-phase times, KV-read GB/s;
@@ -71,7 +74,9 @@ def block_bytes(T, H, F, E, k, touched, wbytes=2, abytes=2):
 
 def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=False, fp8_activations=False):
     """Times `steps` block calls at T tokens (and, with `sublayer`, the
-    norm + block + residual sub-layer); returns a dict of measurements."""
+    norm + block + residual sub-layer); returns a dict of measurements
+    (`kernels`: ms per call of each kernel family, from the library's timers
+    over `steps` more calls)."""
     x_np, wr_np, gen = wl.router_inputs(cfg, T)
     x = torch.from_numpy(x_np).to("cuda", torch.bfloat16)
     wr = torch.from_numpy(wr_np).to("cuda", torch.bfloat16)
@@ -100,19 +105,12 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=Fals
         block(x, out=out)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    # Per-kernel durations: HIP events recorded by the library on the launch stream.
-    ll = fm.lowlevel
-    ll.timing_read()
-    ll.timing_enable(True)
-    for _ in range(steps):
-        block(x, out=out)
-    torch.cuda.synchronize()
-    kernels = ll.timing_read()
-    ll.timing_enable(False)
+    # Per-kernel durations: HIP events recorded by the library on the launch
+    # stream, over as many calls again, right after the timed ones.
+    kernels = kernel_pass(fm, torch, lambda: block(x, out=out), steps)
     ids = block.routing(T)[0]
     touched = int(torch.unique(ids).numel())
-    res = dict(T=T, elapsed=elapsed, ms=elapsed / steps * 1e3, tok_s=steps * T / elapsed,
-               kernels={k: (v[0] / v[1] if v[1] else 0.0) for k, v in kernels.items() if v[1]},
+    res = dict(T=T, elapsed=elapsed, ms=elapsed / steps * 1e3, tok_s=steps * T / elapsed, kernels=kernels,
                touched=touched, pack_s=pack_s, gen=gen, x_np=x_np, wr_np=wr_np, weights=weights,
                block=block, x=x, out=out)
     if sublayer:
@@ -128,15 +126,30 @@ def run_config(fm, wl, torch, cfg, T, steps, warmup, weights=None, sublayer=Fals
             block.sublayer(x, nw, 1e-5, out=sub_out)
         torch.cuda.synchronize()
         res["sublayer_ms"] = (time.perf_counter() - t0) / steps * 1e3
-        ll.timing_read()
-        ll.timing_enable(True)
-        for _ in range(steps):
-            block.sublayer(x, nw, 1e-5, out=sub_out)
-        torch.cuda.synchronize()
-        k2 = ll.timing_read()
-        ll.timing_enable(False)
-        res["sublayer_kernels"] = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in k2.items() if v[1]}
+        res["sublayer_kernels"] = kernel_pass(fm, torch, lambda: block.sublayer(x, nw, 1e-5, out=sub_out), steps)
     return res
+
+
+def kernel_pass(fm, torch, fn, calls, flush=None):
+    """{kernel family: ms per call}: `calls` calls of fn() with the library's
+    HIP-event timers on (flush(), untimed, before each), each family's summed
+    time divided by the number of calls.  A family may be timed in more than
+    one region per call (the permutation and the token-row gather; the two
+    e4m3 quantisation passes), so its count of timed regions is not a call
+    count."""
+    ll = fm.lowlevel
+    ll.timing_read()
+    ll.timing_enable(True)
+    try:
+        for _ in range(calls):
+            if flush:
+                flush()
+            fn()
+        torch.cuda.synchronize()
+        t = ll.timing_read()
+    finally:
+        ll.timing_enable(False)
+    return {k: v[0] / calls for k, v in t.items() if v[1]}
 
 
 def percentile(sorted_vals, q):
@@ -198,20 +211,27 @@ def cpu_info():
 
 
 def _time_oracle(fn, runs):
+    """Median wall time of `runs` calls of fn()."""
     times = []
     for _ in range(runs):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
-    return min(times)
+    return sorted(times)[len(times) // 2]
 
 
-def cpu_baseline(torch, wl, cfg, res, sample, sample_1t):
+# The literal form's rows (BASELINE.md's CPU plan): where the gathered weight
+# copies of one projection take at most 8 GB.
+LITERAL_ROWS = [("C1", 32), ("C4", 1), ("C4", 4), ("C4", 16), ("C4", 64), ("C3", 64), ("C2", 16)]
+LITERAL_BUDGET = 8e9
+
+
+def cpu_baseline(torch, wl, cfg, res, sample, sample_1t, literal=True):
     """The oracle's expert-grouped NumPy restatement (oracle/moe.py), fp32
     OpenBLAS, on a bounded sample of the same batch: all cores (the value)
     and one thread; plus the literal gather form (oracle/moe.py
-    mul_mat_id_literal, the reference's own decomposition) where its gathered
-    weight copies fit: the C1 toy block and C4 at one token."""
+    mul_mat_id_literal, the reference's own decomposition) at LITERAL_ROWS.
+    Every time is the median of 3 runs."""
     import numpy as np
     from oracle import moe as om
 
@@ -220,14 +240,14 @@ def cpu_baseline(torch, wl, cfg, res, sample, sample_1t):
     host_w = [w.float().cpu().numpy() for w in dev_w]
     args = (res["wr_np"], *host_w, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff, cfg.normalize)
     xs = res["x_np"][:sample]
-    best = _time_oracle(lambda: om.moe_ffn_block(xs, *args, dtype=np.float32), 3)
+    med = _time_oracle(lambda: om.moe_ffn_block(xs, *args, dtype=np.float32), 3)
     out = {
-        "value": sample / best,
+        "value": sample / med,
         "unit": "tokens/s",
         "cores": info["affinity_cores"],
         "kind": "port",
         "sample": (f"{sample} of the {res['T']} tokens of the C2 batch, fp32 expert-grouped NumPy/OpenBLAS "
-                   f"restatement of oracles/moe.py (oracle/moe.py), best of 3 runs ({best:.2f}s each), "
+                   f"restatement of oracles/moe.py (oracle/moe.py), median of 3 runs ({med:.2f}s), "
                    f"all {info['affinity_cores']} cores"),
         **info,
     }
@@ -236,23 +256,41 @@ def cpu_baseline(torch, wl, cfg, res, sample, sample_1t):
 
         x1 = res["x_np"][:sample_1t]
         with threadpool_limits(limits=1):
-            b1 = _time_oracle(lambda: om.moe_ffn_block(x1, *args, dtype=np.float32), 2)
-        out["single_thread"] = {"value": sample_1t / b1, "unit": "tokens/s", "cores": 1,
-                                "sample": f"{sample_1t} tokens, best of 2 runs ({b1:.2f}s each)"}
+            m1 = _time_oracle(lambda: om.moe_ffn_block(x1, *args, dtype=np.float32), 3)
+        out["single_thread"] = {"value": sample_1t / m1, "unit": "tokens/s", "cores": 1,
+                                "sample": f"{sample_1t} tokens, median of 3 runs ({m1:.2f}s)"}
     except Exception as e:  # pragma: no cover - reporting only
         out["single_thread"] = f"not timed: {e}"
-    # The literal form (per-assignment weight gather + batched mat-vec).
-    literal = []
-    for name, T in (("C1", 32), ("C4", 1)):
+    if not literal:
+        return out
+    # The literal form (per-assignment weight gather + batched mat-vec, one
+    # thread: NumPy's gather and einsum run on the calling thread).  C2 runs
+    # on the headline's weights; the other configurations on N(0, 0.02^2)
+    # weights drawn once per configuration.
+    rows = []
+    weights = {"C2": host_w}
+    for name, T in LITERAL_ROWS:
         c = wl.CONFIGS[name]
+        if name not in weights:
+            weights = {"C2": host_w}
+            g = np.random.default_rng(0)
+            weights[name] = [(g.standard_normal(sh, dtype=np.float32) * np.float32(0.02)) for sh in
+                             ((c.n_ff, c.n_embd, c.n_expert), (c.n_ff, c.n_embd, c.n_expert),
+                              (c.n_embd, c.n_ff, c.n_expert))]
         x, wr, _ = wl.router_inputs(c, T)
-        g = np.random.default_rng(0)
-        ws = [(g.standard_normal(sh, dtype=np.float32) * 0.02) for sh in
-              ((c.n_ff, c.n_embd, c.n_expert), (c.n_ff, c.n_embd, c.n_expert), (c.n_embd, c.n_ff, c.n_expert))]
+        if name == "C2":
+            x, wr = res["x_np"][:T], res["wr_np"]
+        ws = weights[name]
+        gathered = c.n_expert_used * T * c.n_ff * c.n_embd * 4
         t = _time_oracle(lambda: om.moe_ffn_block_literal(x, wr, *ws, c.n_expert, c.n_expert_used, c.n_embd,
-                                                          c.n_ff, c.normalize), 3)
-        literal.append({"config": name, "tokens": T, "tokens_per_s": T / t, "seconds": t})
-    out["literal_form"] = literal
+                                                          c.n_ff, c.normalize, budget_bytes=LITERAL_BUDGET), 3)
+        rows.append({"config": name, "tokens": T, "tokens_per_s": T / t, "median_s": t, "runs": 3,
+                     "gathered_bytes_per_projection": gathered})
+        log(f"cpu literal {name} T={T}: {t:.3f} s (median of 3)")
+    out["literal_form"] = rows
+    out["literal_form_infeasible"] = {
+        f"{n} T={T}": f"would materialise {wl.CONFIGS[n].n_expert_used * T * wl.CONFIGS[n].n_ff * wl.CONFIGS[n].n_embd * 4 / 1e9:.0f} GB per projection"
+        for n, T in (("C2", 512), ("C2", 4096), ("C3", 2048), ("C3", 8192), ("C5", 4096))}
     return out
 
 
@@ -282,9 +320,11 @@ def config_table(fm, wl, torch, steps, warmup, headline=None, rows_spec=None):
     """Every BASELINE configuration and token count (CONFIG_ROWS): per-call
     device time (median / p10 / p90), tokens/s, MFMA fraction (against the
     bf16 peak, or the fp8 peak for e4m3 activations), HBM fraction of the
-    touched experts' weights, per-kernel HIP-event times.  Rows whose touched
-    weights would fit in the MALL are timed cold: a 512 MB buffer is written
-    before every call."""
+    touched experts' weights, and per call the time of each kernel family
+    (kernels_us, from the library's HIP-event timers over as many calls
+    again, right after the timed ones; their sum leaves out the gaps between
+    launches).  Rows whose touched weights would fit in the MALL are timed
+    cold: a 512 MB buffer is written before every call."""
     flush_buf = torch.empty(int(2 * MALL_BYTES), dtype=torch.uint8, device="cuda")
     rows = []
     cache = {}
@@ -296,14 +336,17 @@ def config_table(fm, wl, torch, steps, warmup, headline=None, rows_spec=None):
             torch.cuda.empty_cache()
         cfg = wl.CONFIGS[name]
         H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
-        res = run_config(fm, wl, torch, cfg, T, 3, 2, weights=cache.get(name), fp8_activations=a8)
+        res = run_config(fm, wl, torch, cfg, T, 2, 1, weights=cache.get(name), fp8_activations=a8)
         cache[name] = res["weights"]
         wb = 1 if cfg.weights == "fp8" else 2
         wbytes = res["touched"] * 3.0 * H * F * wb
         cold = wbytes < 2 * MALL_BYTES
         block, x, out = res["block"], res["x"], res["out"]
-        st = timed_calls(torch, lambda: block(x, out=out), warmup, steps,
-                         flush=(lambda: flush_buf.zero_()) if cold else None)
+        flush = (lambda: flush_buf.zero_()) if cold else None
+        st = timed_calls(torch, lambda: block(x, out=out), warmup, steps, flush=flush)
+        # Kernel families over as many calls again, in the same state (the
+        # same flush before every call), straight after the timed calls.
+        kern = kernel_pass(fm, torch, lambda: block(x, out=out), steps, flush=flush)
         ms = st["median_ms"]
         flops = block_flops(T, H, F, E, k)
         nbytes = block_bytes(T, H, F, E, k, res["touched"], wbytes=wb)
@@ -313,7 +356,8 @@ def config_table(fm, wl, torch, steps, warmup, headline=None, rows_spec=None):
                "calls": st["calls"], "warmup": st["warmup"], "tokens_per_s": T / (ms * 1e-3),
                "mfma_frac": flops / (ms * 1e-3) / peak, "mfma_peak_tflops": peak / 1e12,
                "hbm_frac": nbytes / (ms * 1e-3) / PEAK_HBM_BYTES, "experts_touched": res["touched"],
-               "mall_flushed": cold, "kernels_us": {kk: round(v * 1e3, 1) for kk, v in res["kernels"].items()}}
+               "mall_flushed": cold, "kernels_us": {kk: round(v * 1e3, 1) for kk, v in kern.items()},
+               "kernels_sum_us": round(sum(kern.values()) * 1e3, 1)}
         rows.append(row)
         log(f"{name} T={T:5d} act={row['activations']}: median {ms:.4f} ms (p10 {st['p10_ms']:.4f}, "
             f"p90 {st['p90_ms']:.4f}){' cold' if cold else ''}  mfma {row['mfma_frac']:.3f}  "
@@ -373,14 +417,7 @@ def attention_decode(fm, torch, batch, ctx, steps, warmup, block_size=16, cpu_sa
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / steps * 1e3
-    ll = fm.lowlevel
-    ll.timing_read()
-    ll.timing_enable(True)
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    kern = {k: v[0] / v[1] for k, v in ll.timing_read().items() if v[1]}
-    ll.timing_enable(False)
+    kern = kernel_pass(fm, torch, step, steps)
     kv_bytes = 2.0 * batch * ctx * nkv * 2
     qkv_bytes = n_embd * (n_embd + 2 * nkv) * 2.0
     out_bytes = n_embd * n_embd * 2.0
@@ -449,10 +486,10 @@ def attention_cpu_baseline(torch, blk, x, pos, kp, vp, tables, lens, ctx, bi, pi
                                   pi[:sample].cpu().numpy(), *ws, None, None, None, None, False, 32, 8, 4096,
                                   dtype=np.float32)
         times.append(time.perf_counter() - t0)
-    dt = min(times)
+    dt = sorted(times)[len(times) // 2]
     return {"value": sample / dt, "unit": "tokens/s", "cores": len(os.sched_getaffinity(0)), "kind": "port",
             "sample": f"{sample} of the {x.shape[0]} sequences ({ctx} cached positions each), fp32 NumPy gather + "
-                      f"attention_block_decode + scatter (oracle/attention.py), best of {len(times)} runs "
+                      f"attention_block_decode + scatter (oracle/attention.py), median of {len(times)} runs "
                       f"({dt:.2f}s each), random weights of the same shapes"}
 
 
@@ -469,6 +506,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=4096)
     ap.add_argument("--cpu-sample-1t", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-literal", action="store_true", help="skip the literal-form CPU rows")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration table")
     ap.add_argument("--config-rows", default="",
                     help="only these configs rows: comma-separated NAME[:T[:bf16|e4m3]] (default: all)")
@@ -577,7 +615,7 @@ def main():
     if not args.no_cpu_baseline:
         log(f"cpu baseline on {args.cpu_sample} tokens (all cores), {args.cpu_sample_1t} (one thread)")
         result["cpu_baseline"] = cpu_baseline(torch, wl, cfg, pre, min(args.cpu_sample, T),
-                                              min(args.cpu_sample_1t, T))
+                                              min(args.cpu_sample_1t, T), literal=not args.no_cpu_literal)
         log(f"cpu baseline {result['cpu_baseline']['value']:.1f} tok/s")
     else:
         result["cpu_baseline"] = None

@@ -213,8 +213,9 @@ def timing_enable(on: bool = True) -> None:
 
 
 def timing_read():
-    """{kernel family: (total ms, launches)} since the last read (waits for
-    the recorded HIP events)."""
+    """{kernel family: (total ms, timed regions)} since the last read (waits
+    for the recorded HIP events).  A family can be timed in more than one
+    region per call, so per-call times are totals divided by the calls."""
     n = len(TIMERS)
     ms = (ctypes.c_double * n)()
     cnt = (_c_i64 * n)()

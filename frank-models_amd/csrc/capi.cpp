@@ -965,7 +965,7 @@ int fmoe_timing_enable(int on) {
   return ok();
 }
 
-int fmoe_timing_read(double* ms_out, int64_t* launches_out, int n) {
+int fmoe_timing_read(double* ms_out, int64_t* regions_out, int n) {
   std::lock_guard<std::mutex> lk(g_t_mu);
   for (const PendingTiming& p : g_pending) {
     float ms = 0.f;
@@ -979,7 +979,7 @@ int fmoe_timing_read(double* ms_out, int64_t* launches_out, int n) {
   g_pending.clear();
   for (int i = 0; i < n && i < FMOE_TIMER_COUNT; ++i) {
     if (ms_out) ms_out[i] = g_t_ms[i];
-    if (launches_out) launches_out[i] = g_t_calls[i];
+    if (regions_out) regions_out[i] = g_t_calls[i];
   }
   for (int i = 0; i < FMOE_TIMER_COUNT; ++i) {
     g_t_ms[i] = 0;

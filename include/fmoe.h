@@ -69,9 +69,13 @@ typedef enum fmoe_dtype {
 /* Message describing the last failure on this thread ("" if none). */
 const char *fmoe_last_error(void);
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any change to the declarations).
+ * 2: the kernel-path override (fmoe_set_gemm_path and its enum) moved to
+ *    fmoe_diag.h; FMOE_TIMER_QUANT added (FMOE_TIMER_COUNT 10 -> 11); dtype
+ *    FMOE_F8E4M3FN_A8 (3); fmoe_moe_ffn_block_noalloc.  Packed-weight
+ *    artifacts record the version they were written under. */
 int fmoe_abi_version(void);
-#define FMOE_ABI_VERSION 1
+#define FMOE_ABI_VERSION 2
 
 /* Checks that the current HIP device is a gfx950; writes its ordinal and
  * architecture name (arch may be NULL).  FMOE_ERR_NO_DEVICE otherwise. */
@@ -81,8 +85,12 @@ int fmoe_device_check(int *device, char *arch, size_t arch_len);
  * beyond dumping linked IR, tests/conftest.py:24-30).  While enabled, each
  * kernel that fmoe_moe_ffn_block / fmoe_mul_mat_id launch is bracketed by
  * HIP events recorded on the caller's stream.  fmoe_timing_read waits for
- * the recorded events, writes the summed milliseconds and launch counts per
- * kernel family (index fmoe_timer, up to n entries) and clears them. */
+ * the recorded events, writes the summed milliseconds and the number of
+ * timed regions per kernel family (index fmoe_timer, up to n entries) and
+ * clears them.  A family can be timed in more than one region per call (the
+ * permutation and the token-row gather under FMOE_TIMER_PERMUTE; the two
+ * e4m3 quantisation passes under FMOE_TIMER_QUANT), so per-call times are
+ * the sums divided by the number of calls, not by the region counts. */
 typedef enum fmoe_timer {
   FMOE_TIMER_ROUTER = 0,
   FMOE_TIMER_PERMUTE = 1,
@@ -99,7 +107,7 @@ typedef enum fmoe_timer {
   FMOE_TIMER_COUNT = 11
 } fmoe_timer;
 int fmoe_timing_enable(int on);
-int fmoe_timing_read(double *ms_out, int64_t *launches_out, int n);
+int fmoe_timing_read(double *ms_out, int64_t *regions_out, int n);
 
 /* ---------------------------------------------------------------------- */
 /* SwiGLU: out[i] = gate[i] * up[i] / (1 + exp(-up[i])), silu on `up`.

@@ -93,13 +93,15 @@ def permute(ids: np.ndarray, n_expert: int):
     return order, offsets
 
 
-def mul_mat_id_literal(weights: np.ndarray, input: np.ndarray, ids: np.ndarray) -> np.ndarray:
+def mul_mat_id_literal(weights: np.ndarray, input: np.ndarray, ids: np.ndarray,
+                       budget_bytes: int = LITERAL_BUDGET_BYTES) -> np.ndarray:
     """The reference's gather + batched mat-vec, step for step
-    (mul_mat_id.mlir:37-117; oracles/moe.py:29-48).  Small shapes only."""
+    (mul_mat_id.mlir:37-117; oracles/moe.py:29-48).  Small shapes only: the
+    gathered weights may take at most ``budget_bytes``."""
     n_out, n_in, n_expert = weights.shape
     k, T = ids.shape
     need = k * T * n_out * n_in * weights.dtype.itemsize
-    if need > LITERAL_BUDGET_BYTES:
+    if need > budget_bytes:
         raise MemoryError(f"literal mul_mat_id would materialise {need / 1e9:.1f} GB")
     weights_t = weights.transpose(2, 0, 1)  # [E, n_out, n_in]
     gathered = weights_t[ids]  # [k, T, n_out, n_in]
@@ -155,6 +157,7 @@ def moe_ffn_block_literal(
     n_ff,
     normalize_weights,
     dtype=np.float32,
+    budget_bytes=LITERAL_BUDGET_BYTES,
 ):
     """The reference block step for step (moe_ffn_block.mlir:46-208;
     oracles/moe.py:84-132): replicate the input per slot, three literal
@@ -164,10 +167,10 @@ def moe_ffn_block_literal(
     T = x.shape[0]
     k = int(n_expert_used)
     xr = np.broadcast_to(x.T[:, None, :], (n_embd, k, T)).copy()
-    up = mul_mat_id_literal(np.asarray(up_exps_w, dtype), xr, ids)
-    gate = mul_mat_id_literal(np.asarray(gate_exps_w, dtype), xr, ids)
+    up = mul_mat_id_literal(np.asarray(up_exps_w, dtype), xr, ids, budget_bytes)
+    gate = mul_mat_id_literal(np.asarray(gate_exps_w, dtype), xr, ids, budget_bytes)
     act = swiglu(gate, up)
-    y = mul_mat_id_literal(np.asarray(down_exps_w, dtype), act, ids)
+    y = mul_mat_id_literal(np.asarray(down_exps_w, dtype), act, ids, budget_bytes)
     y = y * w[None, :, :].astype(dtype)
     return y.sum(axis=1).T
 

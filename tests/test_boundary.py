@@ -46,7 +46,10 @@ def test_library_exports_every_declared_symbol(fm):
 
 
 def test_abi_version(fm):
-    assert fm.lowlevel.lib().fmoe_abi_version() == 1
+    text = (Path(__file__).resolve().parents[1] / "include" / "fmoe.h").read_text()
+    declared = int(re.search(r"#define FMOE_ABI_VERSION (\d+)", text).group(1))
+    assert declared == 2
+    assert fm.lowlevel.lib().fmoe_abi_version() == declared
 
 
 def test_single_hip_runtime(fm):

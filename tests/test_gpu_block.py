@@ -302,16 +302,28 @@ def test_decode_down_combine_fused(fm, wl, gemm_path, name, T, fused):
     assert_close_rms(a, ref, cfg.rtol, what=f"{name} T={T}")
 
 
-def test_decode_down_combine_fused_sublayer(fm, wl, gemm_path):
+@pytest.mark.parametrize("name,T", [("C4", 1), ("C3", 2), ("C2", 1)])
+def test_decode_down_combine_fused_sublayer(fm, wl, gemm_path, name, T):
     """The sub-layer's residual add in the fused epilogue, out of place and in
-    place, against the two-launch path."""
-    cfg = wl.CONFIGS["C4"]
-    case = Case(fm, wl, cfg, 2)
+    place, against the two-launch path, at shapes whose automatic choice is
+    the fused launch (no combine launch recorded; the forced streaming
+    kernel records one)."""
+    cfg = wl.CONFIGS[name]
+    case = Case(fm, wl, cfg, T)
     nw = torch.ones(cfg.n_embd, dtype=torch.bfloat16, device="cuda")
+    ll = gemm_path
     outs = []
     for p in ("auto", "stream"):
         _set_path(gemm_path, p)
-        o = case.block.sublayer(case.x, nw, 1e-5)
+        ll.timing_read()
+        ll.timing_enable(True)
+        try:
+            o = case.block.sublayer(case.x, nw, 1e-5)
+            torch.cuda.synchronize()
+            kern = ll.timing_read()
+        finally:
+            ll.timing_enable(False)
+        assert (kern["combine"][1] == 0) == (p == "auto"), (p, kern)
         r = case.x.clone()
         case.block.sublayer(r, nw, 1e-5, out=r)
         torch.cuda.synchronize()

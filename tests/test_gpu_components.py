@@ -167,10 +167,10 @@ def test_router_ties_lower_index(fm):
 
 
 # Logits one ulp apart have one fp32 probability: the selection runs on the
-# probabilities (lower expert index first), on every router kernel: the SIMT
-# kernel (fp32), the MFMA kernels (bf16, T > 64: 16 tokens per block, or 32
-# for 33..128 experts with n_embd % 128 == 0), the decode pair (bf16,
-# T <= 64), and the one-token-per-wave top-k (k > 16).
+# probabilities (lower expert index first), on every kernel fmoe_router runs:
+# the SIMT kernel (fp32), the MFMA kernels (bf16: 16 tokens per block, or 32
+# for 33..128 experts with n_embd % 128 == 0), and the one-token-per-wave
+# top-k (k > 16).  The block's own routers are covered below.
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("T", [1, 16, 100])
 @pytest.mark.parametrize("E,k,H", [(8, 3, 64), (40, 18, 64), (40, 3, 128), (128, 8, 256)])
@@ -182,6 +182,32 @@ def test_router_ulp_apart_logits(fm, dt, T, E, k, H):
         ids, w = fm.router(torch.from_numpy(x).to("cuda", dt), torch.from_numpy(wr).to("cuda", dt), k, norm)
         ids, w = ids.cpu().numpy(), w.cpu().numpy()
         np.testing.assert_array_equal(ids, want)
+        assert np.array_equal(w[0], w[1])  # the tied pair has one weight
+
+
+# The same ties through the block, whose routing runs other kernels: the
+# decode split-logits router (bf16, T <= 64) with its one-wave finish (up to
+# 4 tokens), its one-block finish, and its top-k over blocks (above 64
+# experts and 32 tokens); and the split prefill router (33..128 experts,
+# n_embd % 128 == 0, T > 64), which sums partial logits over hidden-axis
+# ranges.
+@pytest.mark.parametrize("E,k,H,T", [(128, 8, 256, 1), (128, 8, 256, 3), (64, 6, 256, 16), (128, 8, 256, 40),
+                                     (40, 3, 128, 100)])
+def test_block_router_ulp_apart_logits(fm, wl, E, k, H, T):
+    F = 64
+    cfg = wl.scaled(wl.CONFIGS["C3"], H, F, n_expert=E, n_expert_used=k)
+    x, wr = ulp_tie_router_inputs(E, H, T)
+    want, _ = om.router(x, wr, k, False, dtype=np.float32)
+    up, gate, down = wl.expert_weights(cfg, "cuda", dtype=torch.bfloat16)
+    packed = [fm.pack_expert_weights(w) for w in (up, gate, down)]
+    for norm in (False, True):
+        blk = fm.MoEFFNBlock(torch.from_numpy(wr).to("cuda", torch.bfloat16), *packed, E, k, H, F, norm,
+                             act_dtype=torch.bfloat16)
+        blk(torch.from_numpy(x).to("cuda", torch.bfloat16))
+        torch.cuda.synchronize()
+        ids, w, _, _ = blk.routing(T)
+        np.testing.assert_array_equal(ids.cpu().numpy(), want, err_msg=f"normalize={norm}")
+        w = w.cpu().numpy()
         assert np.array_equal(w[0], w[1])  # the tied pair has one weight
 
 

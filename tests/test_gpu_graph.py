@@ -36,8 +36,12 @@ def _replays_match(make_inputs, static_inputs, run, outputs, n=3):
             assert torch.equal(a, b), f"replay {i} differs from the eager call"
 
 
+@pytest.mark.parametrize("noalloc", [False, True])
 @pytest.mark.parametrize("T", [1, 16, 300])
-def test_moe_ffn_block_graph_replay(fm, wl, T):
+def test_moe_ffn_block_graph_replay(fm, wl, T, noalloc):
+    """Also the allocation-free entry point (the library's fixed scratch in
+    place of the block's workspace): its launches hold no allocation, copy or
+    memset either."""
     cfg = wl.scaled(wl.CONFIGS["C3"], 256, 384)
     up, gate, down = wl.expert_weights(cfg, "cuda", dtype=torch.bfloat16)
     packed = [fm.pack_expert_weights(w) for w in (up, gate, down)]
@@ -51,7 +55,7 @@ def test_moe_ffn_block_graph_replay(fm, wl, T):
                          cfg.n_embd, cfg.n_ff, cfg.normalize)
     x = torch.from_numpy(x0).to("cuda", torch.bfloat16)
     out = torch.empty((T, cfg.n_embd), dtype=torch.bfloat16, device="cuda")
-    _replays_match(make, [x], lambda: blk(x, out=out), [out])
+    _replays_match(make, [x], lambda: blk(x, out=out, noalloc=noalloc), [out])
 
 
 def test_paged_attention_graph_replay(fm):

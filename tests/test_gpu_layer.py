@@ -66,9 +66,9 @@ RES_SCALE = {"C1": (0.25, 4.0), "C2": (0.1, 1.5), "C3": (0.25, 4.0), "C4": (0.02
 
 
 class SubCase:
-    def __init__(self, fm, wl, cfg, T):
+    def __init__(self, fm, wl, cfg, T, scale_range=None):
         self.cfg, self.T = cfg, T
-        res, nw, wr, eps, _ = wl.sublayer_inputs(cfg, T, scale_range=RES_SCALE[cfg.name[:2]])
+        res, nw, wr, eps, _ = wl.sublayer_inputs(cfg, T, scale_range=scale_range or RES_SCALE[cfg.name[:2]])
         act = torch.bfloat16 if cfg.act == "bf16" else torch.float32
         self.res_np, self.nw_np, self.wr_np, self.eps = res, nw, wr, eps
         self.res = torch.from_numpy(res).to("cuda", act)
@@ -142,6 +142,28 @@ def test_sublayer_full_size(fm, wl, name, T, sample):
     out = case.run()
     tok = None if sample is None else np.sort(np.random.default_rng(T).choice(T, sample, replace=False))
     case.check(out, tok)
+
+
+# One decode token at full size: at most 16 assignments, so the down
+# projection, the slot-ordered combine and the residual add run in one launch
+# (no combine launch recorded).  Residual scales at the low end of each
+# configuration's range keep the block a large part of a single row's output.
+@pytest.mark.parametrize("name,scale", [("C4", (0.02, 0.03)), ("C2", (0.1, 0.15)), ("C5", (0.1, 0.15))])
+def test_sublayer_one_token_fused(fm, wl, name, scale):
+    case = SubCase(fm, wl, wl.CONFIGS[name], 1, scale_range=scale)
+    ll = fm.lowlevel
+    ll.timing_read()
+    ll.timing_enable(True)
+    try:
+        out = case.run()
+        kern = ll.timing_read()
+    finally:
+        ll.timing_enable(False)
+    assert kern["combine"][1] == 0 and kern["down"][1] > 0, kern
+    case.check(out)
+    buf = case.res.clone()
+    again = case.run(out=buf)
+    np.testing.assert_array_equal(out.view(np.uint32), again.view(np.uint32))
 
 
 def test_sublayer_in_place_equals_out_of_place(fm, wl):
