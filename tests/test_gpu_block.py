@@ -333,6 +333,47 @@ def test_decode_down_combine_fused_sublayer(fm, wl, gemm_path, name, T):
     np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+# ------------------------------------------------------------------ degenerate routings
+# Any 1 <= n_expert_used <= n_expert is a valid block (moe_ffn_block.mlir:77-89
+# takes k from the call): one expert (every token to expert 0, weight 1),
+# every expert selected, and k = 1 with renormalisation (weight exactly 1).
+@pytest.mark.parametrize("base", ["C1", "C2"])
+@pytest.mark.parametrize("E,k,normalize,T", [(1, 1, False, 37), (1, 1, True, 300), (4, 4, False, 50),
+                                             (4, 4, True, 700), (16, 1, True, 129), (6, 6, True, 5)])
+def test_degenerate_routings(fm, wl, gemm_path, base, E, k, normalize, T):
+    cfg = _scaled(wl, base, 128, 192, n_expert=E, n_expert_used=k, normalize=normalize)
+    case = Case(fm, wl, cfg, T)
+    ref, ids, w = case.oracle()
+    for p in PATHS:
+        _set_path(gemm_path, p)
+        out = case.run()
+        _check_routing(case, ids)
+        assert_close_rms(out, ref, cfg.rtol, what=f"{cfg.name} E={E} k={k} T={T} path={p}")
+        dev_w = case.block.routing(T)[1].cpu().numpy()
+        if k == 1 and (normalize or E == 1):
+            assert np.all(dev_w == 1.0)
+        np.testing.assert_allclose(dev_w, w, rtol=1e-5)
+
+
+def test_block_without_tokens(fm, wl):
+    """A batch of no tokens returns an empty output, for the block and the
+    sub-layer, bf16 and fp32."""
+    for base in ("C1", "C2"):
+        cfg = _scaled(wl, base, 128, 192)
+        case = Case(fm, wl, cfg, 4)
+        empty = case.x[:0]
+        out = case.block(empty)
+        torch.cuda.synchronize()
+        assert out.shape == (0, cfg.n_embd) and out.dtype == case.x.dtype
+        nw = torch.ones(cfg.n_embd, dtype=case.x.dtype, device="cuda")
+        sub = case.block.sublayer(empty, nw, 1e-5)
+        torch.cuda.synchronize()
+        assert sub.shape == (0, cfg.n_embd)
+        # the block still works on a real batch afterwards
+        ref, ids, _ = case.oracle()
+        assert_close_rms(case.run(), ref, cfg.rtol, what=f"{base} after an empty call")
+
+
 # ------------------------------------------------------------------ properties
 def test_deterministic_and_token_order_equivariant(fm, wl, gemm_path):
     cfg = _scaled(wl, "C3", 256, 256)
