@@ -85,8 +85,13 @@ __device__ __forceinline__ f32x4_t mfma_f8x2(const u32x4_t a0, const u32x4_t a1,
 constexpr int kWaitLgkm0 = 0xC07F;                  // lgkmcnt(0)
 constexpr int kWaitVm0 = 0x0F70;                    // vmcnt(0)
 
-__host__ __device__ __forceinline__ int split_boundary(int kblocks, int ksplit, int s) {
-  return s >= ksplit ? kblocks : (s * kblocks / ksplit) & ~1;
+// First K stage of piece s of a tile split ksplit ways: equal pieces rounded
+// down to even stages, except that a two-way split may put its boundary at
+// first64 / 64 of the stages (gemm_tiled256_split_first64).
+__host__ __device__ __forceinline__ int split_boundary(int kblocks, int ksplit, int s, int first64 = 32) {
+  if (s >= ksplit) return kblocks;
+  if (ksplit == 2 && s == 1) return (kblocks * first64 / 64) & ~1;
+  return (s * kblocks / ksplit) & ~1;
 }
 
 __device__ __forceinline__ int64_t source_row(const GroupedGemmArgs& g, int p) {
@@ -233,12 +238,11 @@ constexpr int kTableMinColsOwn = 32;
 static_assert(kBM == ttab::kBM, "the table deals this kernel's tiles");
 
 __global__ __launch_bounds__(perm::kThreads) void tile_table_kernel(const int* __restrict__ offsets, int n_expert,
-                                                                     int n_col, int ksplit, int bpx,
-                                                                     int4* __restrict__ table) {
+                                                                     TileTableReq r) {
   __shared__ int rows[ttab::kMaxExperts];
   for (int e = threadIdx.x; e < n_expert; e += perm::kThreads) rows[e] = offsets[e + 1] - offsets[e];
   __syncthreads();
-  ttab::build(rows, n_expert, n_col, ksplit, bpx, table);
+  ttab::build(rows, n_expert, r, reinterpret_cast<int4*>(r.table));
 }
 
 // The epilogue, staged through LDS so that every global store writes whole
@@ -737,11 +741,11 @@ __device__ __forceinline__ WaveCtx tile_ctx(const GroupedGemmArgs& g, const Tile
   const int64_t nblocks = N / 16;
   constexpr int kStageInputs = F8 ? 64 : 32;  // one packed weight block
   const int64_t kblocks = K / kStageInputs;
-  // This block's share of K: stages [k_first, k_first + KT).
-  // Split s covers stages [b(s), b(s+1)), b(s) = s * kblocks / ksplit rounded
-  // down to even (the bf16 loop runs two stages per trip).
-  const int k_first = split_boundary(static_cast<int>(kblocks), g.ksplit, split);
-  const int KT = split_boundary(static_cast<int>(kblocks), g.ksplit, split + 1) - k_first;
+  // This block's share of K: stages [k_first, k_first + KT), piece s covering
+  // [b(s), b(s+1)) with b = split_boundary, a multiple of two stages (the bf16
+  // loop runs two stages per trip).
+  const int k_first = split_boundary(static_cast<int>(kblocks), g.ksplit, split, g.ksplit_first64);
+  const int KT = split_boundary(static_cast<int>(kblocks), g.ksplit, split + 1, g.ksplit_first64) - k_first;
   WaveCtx c;
   c.lds = lds;
   c.a_base = static_cast<const unsigned char*>(g.a);
@@ -923,7 +927,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     }
   } else {
     if (!A8 && kThin && ti.rows <= kThinRows) {
-      const int64_t kb_first = split_boundary(static_cast<int>(g.K / 32), g.ksplit, split);
+      const int64_t kb_first = split_boundary(static_cast<int>(g.K / 32), g.ksplit, split, g.ksplit_first64);
       thin_k_loop<NSETS>(c, a_group_offset(g, ti, wave & 3, lane, kb_first), ti.rows, acc);
     } else {
       k_issue_range<NSETS>(c, 0, 4);
@@ -946,6 +950,7 @@ hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
   // one this launcher would have to build itself for a narrow GEMM (its
   // kernel costs about as much as the table gains there).
   GroupedGemmArgs g = g_in;
+  g.ksplit_first64 = gemm_tiled256_split_first64(g);
   if (g.tile_table && gemm_tiled256_table_bytes(g) == 0) g.tile_table = nullptr;
   constexpr int lds_bytes = F8 && !A8 ? kLdsF8 : kLds;
   static const bool configured = [] {
@@ -961,11 +966,11 @@ hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
   unsigned blocks = static_cast<unsigned>((total + 7) / 8 * 8);
   if (g.tile_table && !g.tile_table_ready && col_tiles < kTableMinColsOwn) g.tile_table = nullptr;
   if (g.tile_table) {
-    const int bpx = ttab::blocks_per_xcd(row_tiles, col_tiles, g.ksplit);
+    TileTableReq r;
+    gemm_tiled256_table_request(g, &r);
     if (!g.tile_table_ready)
-      hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(perm::kThreads), 0, s, g.offsets, g.n_expert, col_tiles,
-                         g.ksplit, bpx, reinterpret_cast<int4*>(g.tile_table));
-    blocks = static_cast<unsigned>(8 * bpx);
+      hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(perm::kThreads), 0, s, g.offsets, g.n_expert, r);
+    blocks = static_cast<unsigned>(8 * r.bpx);
   }
   hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8, A8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
                      row_tiles, col_tiles);
@@ -1006,8 +1011,27 @@ bool gemm_tiled256_table_request(const GroupedGemmArgs& g, TileTableReq* r) {
     r->n_col = col_tiles;
     r->ksplit = ksplit;
     r->bpx = ttab::blocks_per_xcd(row_tiles, col_tiles, ksplit);
+    r->kblocks = static_cast<int>(g.K / (g.w_dtype == DT_F8 ? 64 : 32));
+    r->ksplit_first64 = gemm_tiled256_split_first64(g);
   }
   return true;
+}
+
+// The two pieces of a K-split tile are dealt as separate blocks.  When the
+// launch runs many rounds of blocks per CU (at least 4.5: Mixtral's down
+// projection at 4096 tokens, 35 row tiles x 16 columns x 2 pieces over 256
+// CUs), a short first piece (12/64 of K) and a long second one leave short
+// blocks to fill the last round: measured C2 T=4096 down 731 -> 711 us, C5
+// T=4096 707 -> 700 us (e4m3 activations 372 -> 359 us), medians of three
+// interleaved rounds.  A list-scheduling replay of the measured tile costs
+// gave the same optimum (8.9% -> 4.1% idle CU time).  With fewer rounds the
+// split is there to fill the CUs, and equal pieces keep the longest block
+// short (C2 T=512: 170 us against 229 us with 12/64).
+int gemm_tiled256_split_first64(const GroupedGemmArgs& g) {
+  if (gemm_tiled256_ksplit(g) != 2) return 32;
+  const int row_tiles = max_row_tiles(g.n_assign, g.n_expert, kBM);
+  const int64_t blocks = static_cast<int64_t>(row_tiles) * ((g.N + kBN - 1) / kBN) * 2;
+  return blocks * 2 >= 9 * 256 ? 12 : 32;
 }
 
 size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g) {

@@ -116,6 +116,9 @@ struct GroupedGemmArgs {
   // ksplit (one weight set, fp32 scatter output).
   int ksplit = 1;
   int64_t split_stride = 0;
+  // 256-tile kernel with ksplit == 2: the first piece covers this many 64ths
+  // of the K stages (set by its launcher).
+  int ksplit_first64 = 32;
   // Upper bound on any expert's row count when the caller knows one (the
   // block: n_tokens, since top-k picks distinct experts per token); 0 =
   // unknown.  A tuning hint: kernels are correct for any count.
@@ -193,6 +196,8 @@ hipError_t launch_router_prefill(const void* x, const void* wr, int n_tokens, in
 struct TileTableReq {
   int* table = nullptr;
   int n_col = 0, ksplit = 1, bpx = 0;
+  int kblocks = 0;          // K stages of a whole tile
+  int ksplit_first64 = 32;  // with ksplit == 2: the first piece's share in 64ths
 };
 constexpr int kPermuteMaxTables = 2;
 
@@ -239,6 +244,8 @@ int gemm_tiled256_ksplit(const GroupedGemmArgs& g);
 // one), with r->table = g.tile_table; and its size in bytes (0: none).
 bool gemm_tiled256_table_request(const GroupedGemmArgs& g, TileTableReq* r);
 size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g);
+// With a two-way K split: the first piece's share of the K stages, in 64ths.
+int gemm_tiled256_split_first64(const GroupedGemmArgs& g);
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n,
                          int dtype, hipStream_t stream);

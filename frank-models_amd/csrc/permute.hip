@@ -65,8 +65,7 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const int* __restrict
     __syncthreads();
     const int i = static_cast<int>(blockIdx.x) - 1;
     const TileTableReq r = tt.r[i / kTableParts];
-    ttab::build(rows, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table), i % kTableParts,
-                kTableParts);
+    ttab::build(rows, n_expert, r, reinterpret_cast<int4*>(r.table), i % kTableParts, kTableParts);
     return;
   }
   perm::permute_block(ids, n, n_expert, order, offsets, err_count);
@@ -130,8 +129,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(const int* __re
     __syncthreads();
     const int i = chunk - n_chunks;
     const TileTableReq r = tt.r[i / kTableParts];
-    ttab::build(total, n_expert, r.n_col, r.ksplit, r.bpx, reinterpret_cast<int4*>(r.table), i % kTableParts,
-                kTableParts);
+    ttab::build(total, n_expert, r, reinterpret_cast<int4*>(r.table), i % kTableParts, kTableParts);
     return;
   }
   for (int e = tid; e < n_expert; e += kThreads) {

@@ -6,10 +6,11 @@
 // The GEMM's in-kernel schedule gives each XCD an equal count of row tiles;
 // with skewed expert row counts that leaves whole XCDs short of work and
 // each XCD's last round partly empty.  The table deals the work longest
-// first instead: a chunk is one (K split, column group of group_cols tiles,
+// first instead: a chunk is one (K piece, column group of group_cols tiles,
 // expert) with all the expert's row tiles, costed per row tile as
 // 375 + rows (a full tile 631: fixed setup, prologue, epilogue and weight
-// stream, plus its rows' MFMAs).  Chunks are sorted by cost into 255
+// stream, plus its rows' MFMAs), scaled by the piece's share of the K
+// stages (the two pieces of a split may differ).  Chunks are sorted by cost into 255
 // buckets (a stable counting sort, largest first; empty chunks last) and
 // dealt to the XCDs in snake order (0..7, 7..0, ...); each XCD runs its
 // chunks in that order, a chunk's tiles row tile by row tile over its
@@ -54,6 +55,18 @@ __host__ __device__ inline int64_t n_chunks(int n_col, int ksplit, int n_expert)
 
 __device__ __forceinline__ int tile_cost(int rows) { return 375 + rows; }
 
+// K stages of piece sp of a tile split ksplit ways (the 256-tile kernel's
+// split_boundary: a two-way split at first64 / 64 of the stages, rounded down
+// to even; otherwise equal pieces).
+__device__ __forceinline__ int piece_stages(int kblocks, int ksplit, int first64, int sp) {
+  auto bound = [&](int s) {
+    if (s >= ksplit) return kblocks;
+    if (ksplit == 2 && s == 1) return (kblocks * first64 / 64) & ~1;
+    return (s * kblocks / ksplit) & ~1;
+  };
+  return bound(sp + 1) - bound(sp);
+}
+
 // Position in the sorted chunk order of the m-th chunk XCD x receives.
 __device__ __forceinline__ int snake_pos(int x, int m) { return m * 8 + ((m & 1) ? 7 - x : x); }
 
@@ -62,8 +75,13 @@ __device__ __forceinline__ int snake_pos(int x, int m) { return m * 8 + ((m & 1)
 // to the whole block), in expert order; 8 * bpx entries.  Called by every
 // thread of a perm::kThreads block; with n_parts blocks on one table, each
 // sorts the chunks and writes part `part` of the entries.
-__device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_col, int ksplit, int bpx,
+__device__ __forceinline__ void build(const int* e_rows_in, int n_expert, const TileTableReq& req,
                                       int4* __restrict__ table, int part = 0, int n_parts = 1) {
+  const int n_col = req.n_col, ksplit = req.ksplit, bpx = req.bpx;
+  const int kblocks = req.kblocks > 0 ? req.kblocks : ksplit;
+  // a chunk's cost scales with its K piece (the pieces of a two-way split may differ)
+  int max_piece = 0;
+  for (int sp = 0; sp < ksplit; ++sp) max_piece = max(max_piece, piece_stages(kblocks, ksplit, req.ksplit_first64, sp));
   __shared__ int e_off[kMaxExperts], e_rows[kMaxExperts], e_cost[kMaxExperts];
   __shared__ int bucket[kChunks], srt[kChunks], boff[kBuckets + 1], berr;
   __shared__ int pref[8][kChunks / 8 + 1];
@@ -91,13 +109,14 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, int n_
       running += __shfl(incl, kWave - 1, kWave);
     }
     for (int o = kWave / 2; o > 0; o >>= 1) mc = max(mc, __shfl_xor(mc, o, kWave));
-    if (lane == 0) max_cost = mc * gcols;
+    if (lane == 0) max_cost = static_cast<int>(static_cast<int64_t>(mc) * gcols * max_piece / kblocks);
   }
   __syncthreads();
   // bucket 0 = the most expensive chunks, kBuckets - 2 the cheapest, kBuckets - 1 empty
   for (int c = tid; c < n_chunks; c += perm::kThreads) {
-    const int e = c % n_expert, g = (c / n_expert) % n_groups;
-    const int cost = e_cost[e] * min(gcols, n_col - g * gcols);
+    const int e = c % n_expert, g = (c / n_expert) % n_groups, sp = c / (n_expert * n_groups);
+    const int cost = static_cast<int>(static_cast<int64_t>(e_cost[e]) * min(gcols, n_col - g * gcols) *
+                                      piece_stages(kblocks, ksplit, req.ksplit_first64, sp) / kblocks);
     bucket[c] = cost == 0 ? kBuckets - 1
                           : kBuckets - 2 - static_cast<int>(static_cast<int64_t>(cost) * (kBuckets - 2) /
                                                             (max_cost + 1));
