@@ -24,7 +24,8 @@
 //   stream  decode-sized batches: every weight block is read exactly once
 //           straight into MFMA registers (no LDS), 16 assignment rows per
 //           pass, 8 input steps of loads in flight per wave (16 for the
-//           one-tile bf16 gate/up kernel).
+//           one-tile bf16 gate/up kernel); one-weight projections of at most
+//           16 rows stream through a ring in LDS instead (gemm_stream_lds_kernel).
 // And, for decode batches of at most 16 assignments, the down projection
 // fused with the slot-ordered combine (down_combine_small_kernel).
 #include "common.h"
@@ -504,6 +505,90 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
   }
 }
 
+// ===================================================== stream through LDS
+// One-weight projections of at most 16 rows (the decode attention's Q/K/V
+// and output projections): a column slab per block and four K quarters per
+// wave, as gemm_stream_kernel, but each wave keeps D input steps of loads in
+// flight by loading them straight into a ring of its own in LDS
+// (global_load_lds, no staging registers): per step the 1 KiB weight block
+// and the 1 KiB token fragment block, in the lane order the MFMA reads them.
+// gemm_stream_kernel holds one trip of 8 steps per wave in registers and
+// waits for it before loading the next, so a slab of a 4096-input weight
+// (4 trips per wave) costs four round trips to HBM; here the wave waits only
+// for the oldest step.  The arithmetic is gemm_stream_kernel's (the same
+// quarters, MFMA chains, wave-order sum and epilogue), so the results are
+// bit for bit the same.  Token rows past the batch load row 0 (their output
+// rows are not stored).
+// Cache policy of the weight loads: non-temporal (each weight byte is read
+// once per launch), as gemm_stream_kernel's, so the weights do not push the
+// token rows and the next kernel's data out of the caches.
+constexpr int kNonTemporal = 2;
+
+template <int D>
+constexpr int stream_lds_bytes() {
+  return kStreamWaves * D * 2048 + (kStreamWaves - 1) * kWave * 16;
+}
+
+template <int EPI, int D>
+__global__ __launch_bounds__(kThreads) void gemm_stream_lds_kernel(GroupedGemmArgs g) {
+  static_assert(EPI == EPI_LINEAR || EPI == EPI_QKV_ROPE, "fused one-weight projection epilogues");
+  static_assert((D & (D - 1)) == 0 && 2 * D <= 62, "ring slots: a power of two, loads within the vmcnt range");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  f32x4_t* partial = reinterpret_cast<f32x4_t*>(lds + kStreamWaves * D * 2048);  // [kStreamWaves - 1][kWave]
+  const int ct = blockIdx.x;
+  const int count = g.n_assign;  // <= 16 rows, in order (one expert, no grouping arrays)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop control
+  const int64_t N = g.N;
+  const int ksteps = static_cast<int>(g.K / 32);
+  const int ks_begin = wave * ksteps / kStreamWaves;
+  const int n = (wave + 1) * ksteps / kStreamWaves - ks_begin;
+  const int r = lane & 15;
+  const unsigned char* wsrc =
+      static_cast<const unsigned char*>(g.w0) + (static_cast<int64_t>(ct) * ksteps + ks_begin) * 1024 + lane * 16;
+  const unsigned char* tsrc = reinterpret_cast<const unsigned char*>(
+      static_cast<const bf16_t*>(g.a) + static_cast<int64_t>(r < count ? r : 0) * g.lda + (lane >> 4) * 8 +
+      static_cast<int64_t>(ks_begin) * 32);
+  unsigned char* ring = lds + wave * D * 2048;
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    unsigned char* slot = ring + (i & (D - 1)) * 2048;
+    __builtin_amdgcn_global_load_lds(wsrc + static_cast<int64_t>(i) * 1024, slot, 16, 0, kNonTemporal);
+    __builtin_amdgcn_global_load_lds(tsrc + static_cast<int64_t>(i) * 64, slot + 1024, 16, 0, 0);
+  };
+  const int pre = n < D ? n : D;
+  for (int i = 0; i < pre; ++i) issue(i);
+  f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < n; ++i) {
+    // step i's two loads are done once at most 2 (D - 1) younger ones are
+    // in flight (loads complete in order); near the end, all of them
+    if (i + D <= n)
+      __builtin_amdgcn_s_waitcnt(wait_vm(2 * D - 2, false));
+    else
+      __builtin_amdgcn_s_waitcnt(wait_vm(0, false));
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    const unsigned char* slot = ring + (i & (D - 1)) * 2048;
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(slot + lane * 16);
+    const u32x4_t t = *reinterpret_cast<const u32x4_t*>(slot + 1024 + lane * 16);
+    acc = mfma16(w, t, acc);
+    // the slot is refilled only after its reads have returned (the MFMA
+    // above waits for them)
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + D < n) issue(i + D);
+  }
+
+  // Partial sums of waves 1..3 -> LDS; wave 0 adds them in wave order.
+  if (wave > 0) partial[(wave - 1) * kWave + lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 1; w < kStreamWaves; ++w) acc += partial[(w - 1) * kWave + lane];
+    const int64_t col = static_cast<int64_t>(ct) * kStreamRows + 4 * (lane >> 4);
+    if (r < count && col < N) store4<EPI>(g, r, col, acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
 // ============================================================ down + combine
 // Decode batches whose n_assign = n_tokens * k assignments fit one 16-row
 // MFMA tile (n_assign <= 16): the down projection and the slot-ordered
@@ -748,6 +833,31 @@ hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(col_tiles * g.n_expert));
   // Rows one pass must cover to read each expert's weights once.
   const int rows = g.max_rows_per_expert > 0 ? g.max_rows_per_expert : g.n_assign;
+  if (!F8 && (g.epi == EPI_LINEAR || g.epi == EPI_QKV_ROPE) && g.n_expert == 1 && !g.offsets && !g.order &&
+      g.n_assign <= 16 && g.ksplit <= 1) {
+    // 8 ring steps per wave (67 KiB of LDS per block, two blocks per CU): measured
+    // against 16 (one block per CU) on the Mixtral attention shape, Q/K/V
+    // 19.0 against 22.3 us and the output projection 11.4 against 12.4 us at
+    // 16 rows, and ahead at 1 and 4 rows too.
+    constexpr int kDepth = 8;
+    static const bool configured = [] {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_lds_kernel<EPI_LINEAR, kDepth>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes<kDepth>());
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_lds_kernel<EPI_QKV_ROPE, kDepth>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes<kDepth>());
+      (void)hipGetLastError();
+      return true;
+    }();
+    (void)configured;
+    const dim3 lgrid(static_cast<unsigned>(col_tiles));
+    if (g.epi == EPI_LINEAR)
+      hipLaunchKernelGGL((gemm_stream_lds_kernel<EPI_LINEAR, kDepth>), lgrid, dim3(kThreads),
+                         stream_lds_bytes<kDepth>(), s, g);
+    else
+      hipLaunchKernelGGL((gemm_stream_lds_kernel<EPI_QKV_ROPE, kDepth>), lgrid, dim3(kThreads),
+                         stream_lds_bytes<kDepth>(), s, g);
+    return hipGetLastError();
+  }
   if (rows <= 16)
     launch_stream_tiles<F8, 1>(g, s, grid, col_tiles);
   else if (rows <= 32)

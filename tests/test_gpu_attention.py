@@ -392,3 +392,58 @@ def test_attention_sublayer_decode_paged(fm, dt, B):
     torch.cuda.synchronize()
     assert out2.data_ptr() == r2.data_ptr()
     assert torch.equal(out2, out)
+
+
+# Shapes for the projections' LDS-ring kernel: the Mixtral attention shape,
+# and small input axes whose four K quarters are short (n_embd 544: 17 input
+# steps, quarters of 4, 4, 4 and 5 steps, each below the 8-step ring) or
+# single steps (n_embd 160: 5 steps).
+RING = [
+    # B, n_embd, H, Hkv
+    (16, 4096, 32, 8),
+    (1, 4096, 32, 8),
+    (7, 544, 17, 17),
+    (3, 160, 5, 5),
+]
+
+
+@pytest.mark.parametrize("B,n_embd,H,Hkv", RING)
+def test_projection_ring_matches_register_stream(fm, gemm_path, B, n_embd, H, Hkv):
+    """Up to 16 rows, bf16 weights: the automatic choice runs the Q/K/V and
+    output projections on the LDS-ring streaming kernel with bias + RoPE and
+    bias + residual in its epilogue; the forced streaming path runs the same
+    products on the register-staged streaming kernel (fp32 out) with the
+    bias, RoPE and residual in separate launches.  Same K quarters, MFMA
+    chains and epilogue arithmetic: equal bit for bit, out of place (block)
+    and with the residual (sub-layer)."""
+    rng = np.random.default_rng(B * 1000 + n_embd)
+    tdt = torch.bfloat16
+    D = n_embd // H
+    bs, max_ctx = 16, 40
+    n_blocks = B * 4 + 4
+    tables = rng.permutation(n_blocks)[: B * 4].reshape(1, B, 4).astype(np.int32)
+    lens = rng.integers(1, max_ctx + 1, (1, B)).astype(np.int32)
+    kp = _round(rng.standard_normal((n_blocks, bs, Hkv, D)), tdt)
+    vp = _round(rng.standard_normal((n_blocks, bs, Hkv, D)), tdt)
+    bi = np.array([tables[0, b, 3] for b in range(B)], np.int32)
+    pi = np.full(B, 15, np.int32)
+    w, b, _ = _weights(rng, n_embd, Hkv * D, tdt)
+    x = _round(rng.standard_normal((B, n_embd)), tdt)
+    nw = _round(rng.standard_normal(n_embd) * 0.5 + 1.0, tdt)
+    pos = torch.from_numpy(lens[0].astype(np.int64)).cuda()
+    blk = fm.AttentionBlockDecode(*(_dev(w[k], tdt) for k in ("wq", "wk", "wv", "wo")),
+                                  *(torch.from_numpy(b[k]).cuda() for k in ("bq", "bk", "bv", "bo")),
+                                  use_bias=True, n_head=H, n_head_kv=Hkv, n_embd=n_embd, act_dtype=tdt)
+    ll = gemm_path
+    got = {}
+    for path in (ll.PATH_AUTO, ll.PATH_STREAM):
+        ll.check(ll.lib().fmoe_set_gemm_path(path))
+        kd, vd = _dev(kp, tdt), _dev(vp, tdt)
+        o = blk.paged(_dev(x, tdt), pos, kd, vd, 0, tables, lens, max_ctx, bi, pi)
+        kd2, vd2 = _dev(kp, tdt), _dev(vp, tdt)
+        s = blk.paged_sublayer(_dev(x, tdt), _dev(nw, tdt), 1e-5, pos, kd2, vd2, 0, tables, lens, max_ctx, bi, pi)
+        torch.cuda.synchronize()
+        got[path] = [t.view(torch.int16).cpu().numpy() for t in (*o, *s, kd, vd)]
+    for name, a, c in zip(("out", "k_new", "v_new", "sub out", "sub k_new", "sub v_new", "k pool", "v pool"),
+                          got[ll.PATH_AUTO], got[ll.PATH_STREAM]):
+        np.testing.assert_array_equal(a, c, err_msg=f"B={B} n_embd={n_embd}: {name}")
