@@ -875,7 +875,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
   int col_tile, split;
   TileInfo ti;
   int4 ent = make_int4(-2, 0, 0, 0);
-  if (g.tile_table) ent = reinterpret_cast<const int4*>(g.tile_table)[blockIdx.x];
+  if (g.tile_table) {
+    const int4* tab = reinterpret_cast<const int4*>(g.tile_table);
+    ent = tab[1 + blockIdx.x];
+    if (ent.x == ttab::kTakeFromPool) {
+      // the next tile of the shared pool, or none once it is empty (one
+      // device-scope atomic per block past its XCD's own tiles), passed to
+      // the block through the first word of the LDS ring before any stage
+      // is loaded into it
+      int* claim = reinterpret_cast<int*>(lds);
+      if (threadIdx.x == 0) *claim = atomicAdd(const_cast<int*>(&tab[0].y), 1);
+      __syncthreads();
+      const int j = *claim;
+      __syncthreads();
+      ent = j < tab[0].x ? tab[1 + gridDim.x + j] : make_int4(-1, 0, 0, 0);
+    }
+  }
   if (ent.x >= 0) {
     ti.expert = __builtin_amdgcn_readfirstlane(ent.x);
     ti.row0 = __builtin_amdgcn_readfirstlane(ent.y);
@@ -970,7 +985,7 @@ hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
     gemm_tiled256_table_request(g, &r);
     if (!g.tile_table_ready)
       hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(perm::kThreads), 0, s, g.offsets, g.n_expert, r);
-    blocks = static_cast<unsigned>(8 * r.bpx);
+    blocks = static_cast<unsigned>(8 * (r.bpx + r.steal));
   }
   hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8, A8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
                      row_tiles, col_tiles);
@@ -1011,6 +1026,14 @@ bool gemm_tiled256_table_request(const GroupedGemmArgs& g, TileTableReq* r) {
     r->n_col = col_tiles;
     r->ksplit = ksplit;
     r->bpx = ttab::blocks_per_xcd(row_tiles, col_tiles, ksplit);
+    // The shared pool (tile_table.h) for the down projection only.  The
+    // XCDs run the same tiles 3-4% apart (per-block stamps at C2 T=4096:
+    // full gate/up tiles 88.5-94.6 us, down 155-163 us by XCD); taking the
+    // tail of each XCD's list from a pool measured, per call over 6 x 30
+    // calls: down 730.6 -> 720.3 us at C2 T=4096 and 714.9 -> 694.9 us at
+    // C5 T=4096; on the gate/up projection, whose tiles share more of their
+    // stages in L2, no gain (1464.5 -> 1472.6 us at C2).
+    r->steal = g.epi == EPI_SWIGLU ? 0 : ttab::steal_per_xcd(r->bpx);
     r->kblocks = static_cast<int>(g.K / (g.w_dtype == DT_F8 ? 64 : 32));
     r->ksplit_first64 = gemm_tiled256_split_first64(g);
   }
@@ -1037,7 +1060,7 @@ int gemm_tiled256_split_first64(const GroupedGemmArgs& g) {
 size_t gemm_tiled256_table_bytes(const GroupedGemmArgs& g) {
   TileTableReq r;
   if (!gemm_tiled256_table_request(g, &r)) return 0;
-  return static_cast<size_t>(8) * r.bpx * 16;
+  return (1 + static_cast<size_t>(8) * (r.bpx + r.steal) + static_cast<size_t>(4) * r.steal) * 16;
 }
 
 bool gemm_tiled256_supported(const GroupedGemmArgs& g) {

@@ -192,10 +192,13 @@ hipError_t launch_router_prefill(const void* x, const void* wr, int n_tokens, in
                                  hipStream_t stream);
 
 // A 256-tile GEMM's tile schedule for the permutation to build beside its
-// scatter (gemm_tiled256_table_request fills it; table: 8 * bpx int4 entries).
+// scatter (gemm_tiled256_table_request fills it).  Table: a header int4
+// {pool size, claim counter, 0, 0}, one int4 entry per hardware block
+// (8 * (bpx + steal) of them), then the shared pool (up to 4 * steal).
 struct TileTableReq {
   int* table = nullptr;
   int n_col = 0, ksplit = 1, bpx = 0;
+  int steal = 0;            // blocks per XCD beyond bpx that take their tile from the pool
   int kblocks = 0;          // K stages of a whole tile
   int ksplit_first64 = 32;  // with ksplit == 2: the first piece's share in 64ths
 };

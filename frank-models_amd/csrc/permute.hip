@@ -198,7 +198,8 @@ hipError_t launch_permute(const int* ids, int n_assign, int n_expert, int* order
     const int64_t chunks = ttab::n_chunks(r.n_col, r.ksplit, n_expert);
     if (!r.table || r.n_col <= 0 || r.n_col >= (1 << 16) || r.ksplit <= 0 || r.bpx <= 0 ||
         n_expert > ttab::kMaxExperts || chunks > ttab::kChunks ||
-        r.bpx != ttab::blocks_per_xcd(max_row_tiles(n_assign, n_expert, ttab::kBM), r.n_col, r.ksplit))
+        r.bpx != ttab::blocks_per_xcd(max_row_tiles(n_assign, n_expert, ttab::kBM), r.n_col, r.ksplit) ||
+        (r.steal != 0 && r.steal != ttab::steal_per_xcd(r.bpx)))
       return hipErrorInvalidValue;
     tt.r[i] = r;
   }

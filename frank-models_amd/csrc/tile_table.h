@@ -15,10 +15,13 @@
 // dealt to the XCDs in snake order (0..7, 7..0, ...); each XCD runs its
 // chunks in that order, a chunk's tiles row tile by row tile over its
 // columns, so tiles sharing token rows or a weight slab stay on one L2.
-// Entry b of the table is hardware block b's tile (XCD b % 8, position
+// Entry 1 + b of the table is hardware block b's tile (XCD b % 8, position
 // b / 8 in that XCD's list): {expert, first row, rows, column | split << 16},
-// expert -1 for no tile.  If an XCD's list outgrows the grid, every entry
-// reads -2 and the GEMM falls back to its in-kernel schedule.
+// expert -1 for no tile, kTakeFromPool for a block that takes the next tile
+// of the shared pool (entries 1 + 8 * (bpx + steal) on; entry 0 holds the
+// pool's size and the claim counter, cleared here).  If an XCD's list
+// outgrows the grid, every entry reads -2 and the GEMM falls back to its
+// in-kernel schedule.
 #pragma once
 #include "common.h"
 #include "launch.h"
@@ -29,6 +32,8 @@ namespace {
 namespace ttab {
 
 constexpr int kBM = 256;        // assignment rows per tile
+constexpr int kPoolDiv = 12;    // 1/12 of each XCD's list (its tail) goes to the shared pool
+constexpr int kTakeFromPool = -3;  // block entry: take the next tile of the pool
 constexpr int kChunks = 2048;   // chunks a table covers (permute_block's limit)
 constexpr int kBuckets = 256;
 constexpr int kMaxExperts = 256;
@@ -38,6 +43,11 @@ __host__ __device__ inline int blocks_per_xcd(int row_tiles_bound, int n_col, in
   const int per = (row_tiles_bound * n_col * ksplit + 7) / 8;
   return per + per / 4 + 1;
 }
+
+// Blocks per XCD beyond bpx that take their tile from the pool: the pool
+// holds at most 8 * bpx / kPoolDiv tiles, within its 4 * steal entries.
+__host__ __device__ inline int steal_per_xcd(int bpx) { return (bpx + 5) / 6; }
+static_assert(kPoolDiv >= 12, "the pool's entries: 4 * steal_per_xcd(bpx) >= 8 * bpx / kPoolDiv");
 
 // Column tiles per chunk.  A chunk's tiles run side by side on one XCD; 8
 // columns x an expert's ~4 row tiles share more of each stage's token rows
@@ -148,25 +158,58 @@ __device__ __forceinline__ void build(const int* e_rows_in, int n_expert, const 
   bool fits = true;
 #pragma unroll
   for (int x = 0; x < 8; ++x) fits = fits && pref[x][per_x] <= bpx;
-  const int per_part = (8 * bpx + n_parts - 1) / n_parts;
-  const int b_end = min(8 * bpx, (part + 1) * per_part);
-  for (int b = part * per_part + tid; b < b_end; b += perm::kThreads) {
-    const int x = b % 8, p = b / 8;
-    int4 ent = make_int4(fits ? -1 : -2, 0, 0, 0);
-    if (fits && p < pref[x][per_x]) {
-      int lo = 0, hi = per_x - 1;  // the last m with pref[x][m] <= p
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if (pref[x][mid] <= p) lo = mid; else hi = mid - 1;
-      }
-      const int c = srt[snake_pos(x, lo)];
-      const int e = c % n_expert, g = (c / n_expert) % n_groups, sp = c / (n_expert * n_groups);
-      const int cig = min(gcols, n_col - g * gcols);
-      const int t = p - pref[x][lo];
-      const int r = t / cig;
-      ent = make_int4(e, e_off[e] + r * kBM, min(kBM, e_rows[e] - r * kBM), (g * gcols + t % cig) | (sp << 16));
+  // keep[x]: the tiles XCD x runs as dealt.  With steal slots, the last
+  // 1/kPoolDiv of its list (its cheapest chunks) goes to the shared pool,
+  // from which the blocks past keep[x] on every XCD take one tile each, so
+  // the XCDs that run faster take more (the XCDs of one part run the same
+  // tiles 3-4% apart).
+  __shared__ int keep[8], pbase[9];
+  if (tid == 0) {
+    int acc = 0;
+    for (int x = 0; x < 8; ++x) {
+      const int L = pref[x][per_x];
+      keep[x] = req.steal > 0 ? L - L / kPoolDiv : L;
+      pbase[x] = acc;
+      acc += L - keep[x];
     }
-    table[b] = ent;
+    pbase[8] = acc;
+  }
+  __syncthreads();
+  // tile at position p of XCD x's list
+  auto entry = [&](int x, int p) {
+    int lo = 0, hi = per_x - 1;  // the last m with pref[x][m] <= p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (pref[x][mid] <= p) lo = mid; else hi = mid - 1;
+    }
+    const int c = srt[snake_pos(x, lo)];
+    const int e = c % n_expert, g = (c / n_expert) % n_groups, sp = c / (n_expert * n_groups);
+    const int cig = min(gcols, n_col - g * gcols);
+    const int t = p - pref[x][lo];
+    const int r = t / cig;
+    return make_int4(e, e_off[e] + r * kBM, min(kBM, e_rows[e] - r * kBM), (g * gcols + t % cig) | (sp << 16));
+  };
+  const int n_blocks = 8 * (bpx + req.steal);
+  const int n_ent = 1 + n_blocks + 4 * req.steal;  // header, one per block, pool
+  const int per_part = (n_ent + n_parts - 1) / n_parts;
+  const int i_end = min(n_ent, (part + 1) * per_part);
+  for (int i = part * per_part + tid; i < i_end; i += perm::kThreads) {
+    int4 ent = make_int4(fits ? -1 : -2, 0, 0, 0);
+    if (i == 0) {
+      ent = make_int4(fits ? pbase[8] : 0, 0, 0, 0);  // pool size, claim counter
+    } else if (i <= n_blocks) {
+      const int b = i - 1, x = b % 8, p = b / 8;
+      if (fits && p < keep[x]) ent = entry(x, p);
+      else if (fits && req.steal > 0) ent = make_int4(kTakeFromPool, 0, 0, 0);
+    } else if (fits) {
+      const int j = i - 1 - n_blocks;
+      if (j < pbase[8]) {
+        int x = 0;
+        while (pbase[x + 1] <= j) ++x;
+        ent = entry(x, keep[x] + j - pbase[x]);
+      }
+    }
+    table[i] = ent;
   }
 }
 
