@@ -33,6 +33,7 @@ F32 = 0
 BF16 = 1
 F8E4M3FN = 2
 F8E4M3FN_A8 = 3  # block / sub-layer: e4m3 weights, prefill GEMMs on e4m3 activations
+F8E4M3FN_A8X2 = 4  # the same with each activation as two e4m3 terms (hi + lo)
 
 # fmoe_gemm_path
 PATH_AUTO = 0

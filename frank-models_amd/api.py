@@ -402,11 +402,15 @@ class MoEFFNBlock:
 
     def __init__(self, gate_inp_w, up_exps_w, gate_exps_w, down_exps_w, n_expert, n_expert_used,
                  n_embd, n_ff, normalize_weights, act_dtype=torch.bfloat16, weight_dtype=None,
-                 fp8_activations: bool = False):
+                 fp8_activations=False):
         """``fp8_activations=True`` (e4m3 weights, bf16 activations) runs the
         prefill-sized GEMMs on the fp8 MFMA with activations quantised to e4m3
         per row (the C ABI's FMOE_F8E4M3FN_A8); decode-sized batches are
-        unchanged.  It adds the activations' e4m3 rounding to the result."""
+        unchanged.  It adds the activations' e4m3 rounding to the result.
+        ``fp8_activations="x2"`` carries each activation as two e4m3 terms
+        (hi = e4m3(v), lo = e4m3(v - hi), FMOE_F8E4M3FN_A8X2): the products
+        still run on the fp8 MFMA, and the result keeps the bf16-activation
+        tolerance."""
         self.act = _TORCH_TO_DT[act_dtype]
         wdt = self.act if weight_dtype is None else _dtype_code(weight_dtype)
         self.up = _pack_cache.get(up_exps_w, wdt)
@@ -417,10 +421,13 @@ class MoEFFNBlock:
         self.wdt = self.up.dtype
         if self.act == L.F32 and self.wdt != L.F32:
             raise TypeError("f32 activations need f32 weights")
+        if fp8_activations not in (False, True, "x2"):
+            raise ValueError(f"fp8_activations must be False, True or 'x2', not {fp8_activations!r}")
         if fp8_activations:
             if self.wdt != L.F8E4M3FN or self.act != L.BF16:
                 raise TypeError("fp8 activations need e4m3 weights and bf16 activations")
-            self.wdt = L.F8E4M3FN_A8  # the block's weight dtype code; the packed buffers are unchanged
+            # the block's weight dtype code; the packed buffers are unchanged
+            self.wdt = L.F8E4M3FN_A8X2 if fp8_activations == "x2" else L.F8E4M3FN_A8
         wr, _ = _to_device(gate_inp_w, "gate_inp_w")
         self.wr = wr.to(_DT_TO_TORCH[self.act]).contiguous()
         self.n_expert = int(n_expert)

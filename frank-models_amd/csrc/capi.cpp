@@ -54,11 +54,12 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 bool act_dtype_ok(int dt) { return dt == FMOE_F32 || dt == FMOE_BF16; }
 bool w_dtype_ok(int dt) { return dt == FMOE_F32 || dt == FMOE_BF16 || dt == FMOE_F8E4M3FN; }
-// The block and sub-layer also take FMOE_F8E4M3FN_A8: e4m3fn weights whose
-// prefill GEMMs run on fp8 activations.
-bool block_w_dtype_ok(int dt) { return w_dtype_ok(dt) || dt == FMOE_F8E4M3FN_A8; }
+// The block and sub-layer also take FMOE_F8E4M3FN_A8 and _A8X2: e4m3fn
+// weights whose prefill GEMMs run on fp8 activations (one or two e4m3 terms).
+bool fp8_act_dtype(int dt) { return dt == FMOE_F8E4M3FN_A8 || dt == FMOE_F8E4M3FN_A8X2; }
+bool block_w_dtype_ok(int dt) { return w_dtype_ok(dt) || fp8_act_dtype(dt); }
 // Storage type of the packed weights for a block weight dtype.
-int packed_dtype(int dt) { return dt == FMOE_F8E4M3FN_A8 ? FMOE_F8E4M3FN : dt; }
+int packed_dtype(int dt) { return fp8_act_dtype(dt) ? FMOE_F8E4M3FN : dt; }
 
 bool aligned_for(const void* p, int dt) {
   return reinterpret_cast<uintptr_t>(p) % dtype_bytes(dt) == 0;
@@ -252,6 +253,9 @@ struct BlockLayout {
   // fp8 activations (FMOE_F8E4M3FN_A8, prefill-sized batches): e4m3 token
   // rows and SwiGLU rows, K-blocked, with their per-row scales (0 bytes otherwise)
   size_t xq, xs, hq, hs, hmax, xmax, a8_bytes;
+  // FMOE_F8E4M3FN_A8X2: bytes from the hi codes to the lo codes of x and h
+  // (0 with one term)
+  size_t x_plane, h_plane;
   size_t rpart;          // split router logits, decode or prefill (0 bytes when the shape takes the one-kernel router)
   size_t rpart_bytes;
   // tile schedules of the prefill GEMMs (256-tile kernel; 0 bytes when the shape takes none)
@@ -310,7 +314,7 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   // Prefill-sized bf16 batches: room for the token rows gathered into expert
   // order, K-blocked, so the gate/up GEMM reads whole cache lines.
   const bool prefill = act == FMOE_BF16 && n > 8 * E;
-  const bool a8 = prefill && block_wdt == FMOE_F8E4M3FN_A8 && H % 128 == 0 && F % 128 == 0 && H <= 16384 &&
+  const bool a8 = prefill && fp8_act_dtype(block_wdt) && H % 128 == 0 && F % 128 == 0 && H <= 16384 &&
                   F <= 16384;
   const bool kb_candidate = prefill && !a8 && H % 64 == 0 && F % 64 == 0 && (F + 127) / 128 >= 16;
   L.ttab_g_bytes = 0;
@@ -332,13 +336,19 @@ BlockLayout block_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t F, 
   L.xkb_bytes = kb_candidate ? static_cast<size_t>(n) * H * 2 : 0;
   off += align_up(L.xkb_bytes);
   L.a8_bytes = 0;
+  L.x_plane = L.h_plane = 0;
   L.xq = off;
   if (a8) {
-    off += align_up(static_cast<size_t>(n) * H);
+    const int terms = block_wdt == FMOE_F8E4M3FN_A8X2 ? 2 : 1;
+    if (terms == 2) {
+      L.x_plane = align_up(static_cast<size_t>(n) * H);
+      L.h_plane = align_up(static_cast<size_t>(n) * F);
+    }
+    off += terms * align_up(static_cast<size_t>(n) * H);
     L.xs = off;
     off += align_up(static_cast<size_t>(n) * 4);
     L.hq = off;
-    off += align_up(static_cast<size_t>(n) * F);
+    off += terms * align_up(static_cast<size_t>(n) * F);
     L.hs = off;
     off += align_up(static_cast<size_t>(n) * 4);
     L.hmax = off;
@@ -553,6 +563,8 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
     dk.a_kb_rows = n;
     dk.out_dtype = FMOE_BF16;
     if (L.a8_bytes) {
+      gk.a_lo_plane = static_cast<int64_t>(L.x_plane);
+      dk.a_lo_plane = static_cast<int64_t>(L.h_plane);
       gk.a = at<char>(workspace, L.xq);
       gk.act_dtype = DT_F8;
       gk.a_scale = at<float>(workspace, L.xs);
@@ -629,7 +641,8 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
     FMOE_HIP(launch_row_absmax(c.input, T, static_cast<int>(n_embd), at<unsigned>(workspace, L.xmax),
                                at<unsigned>(workspace, L.hmax), n, s));
     FMOE_HIP(launch_quantize_rows_kb(c.input, order, n, T, static_cast<int>(n_embd), at<unsigned>(workspace, L.xmax),
-                                     at<char>(workspace, L.xq), at<float>(workspace, L.xs), nullptr, s));
+                                     at<char>(workspace, L.xq), at<float>(workspace, L.xs), nullptr, s,
+                                     L.x_plane ? at<char>(workspace, L.xq + L.x_plane) : nullptr));
   }
   if (gather_x) {
     ScopedTimer t(FMOE_TIMER_PERMUTE, s, c.timers);
@@ -642,7 +655,8 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
   if (h_quant) {
     ScopedTimer t(FMOE_TIMER_QUANT, s, c.timers);
     FMOE_HIP(launch_quantize_rows_kb(h, nullptr, n, n, static_cast<int>(n_ff), at<unsigned>(workspace, L.hmax),
-                                     at<char>(workspace, L.hq), at<float>(workspace, L.hs), nullptr, s));
+                                     at<char>(workspace, L.hq), at<float>(workspace, L.hs), nullptr, s,
+                                     L.h_plane ? at<char>(workspace, L.hq + L.h_plane) : nullptr));
     d = dq;
   }
 

@@ -174,6 +174,29 @@ __device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
   return u32x2_t{w[0], w[1]};
 }
 
+// The same codes as e4m3_codes8 (hi), and in lo the codes of each value's
+// remainder, e4m3(v * inv - hi): the two terms hold every bf16 value whose
+// scaled magnitude is at least 2^-2 exactly (hi keeps its top 4 significant
+// bits, the remainder fits the next 4 within lo's exponent range).
+__device__ __forceinline__ void e4m3_codes8_x2(const u32x4_t v, float inv, u32x2_t& hi, u32x2_t& lo) {
+  uint32_t wh[2], wl[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    wh[d] = 0u;
+    wl[d] = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word = v[2 * d + (i >> 1)];
+      const float x = __uint_as_float((i & 1) ? (word & 0xFFFF0000u) : (word << 16)) * inv;
+      const uint32_t h = f32_to_e4m3fn(x);
+      wh[d] |= h << (8 * i);
+      wl[d] |= f32_to_e4m3fn(x - e4m3fn_to_f32(h)) << (8 * i);
+    }
+  }
+  hi = u32x2_t{wh[0], wh[1]};
+  lo = u32x2_t{wl[0], wl[1]};
+}
+
 // Power-of-two scale 2^e of a row whose largest magnitude is amax: the
 // smallest e with amax / 2^e <= 448 (448 = 1.75 * 2^8), clamped to
 // [-126, 126]; 1 for amax = 0.  *inv = 2^-e.  Exact to apply, and each
@@ -236,7 +259,8 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kb_kernel(const bf16_t
                                                                     const unsigned* __restrict__ row_amax,
                                                                     uint8_t* __restrict__ dst_q,
                                                                     float* __restrict__ dst_scale,
-                                                                    unsigned* __restrict__ zero_out) {
+                                                                    unsigned* __restrict__ zero_out,
+                                                                    uint8_t* __restrict__ dst_lo) {
   __shared__ int64_t s_row[16];
   __shared__ float s_inv[16];
   const int lane = threadIdx.x & (kWave - 1);
@@ -293,9 +317,17 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kb_kernel(const bf16_t
   for (int t = 0; t < 8; ++t) {
     const int j = static_cast<int>(blockIdx.y) * 32 + wave + 4 * t;
     if (j < n_pieces) {
-      const u32x2_t a = e4m3_codes8(lo[t], inv), b = e4m3_codes8(hi[t], inv);
-      *reinterpret_cast<u32x4_t*>(dst_q + (static_cast<int64_t>(j) * n_rows + p) * 64 + g * 16) =
-          u32x4_t{a[0], a[1], b[0], b[1]};
+      const int64_t at = (static_cast<int64_t>(j) * n_rows + p) * 64 + g * 16;
+      if (dst_lo) {
+        u32x2_t ah, al, bh, bl;
+        e4m3_codes8_x2(lo[t], inv, ah, al);
+        e4m3_codes8_x2(hi[t], inv, bh, bl);
+        *reinterpret_cast<u32x4_t*>(dst_q + at) = u32x4_t{ah[0], ah[1], bh[0], bh[1]};
+        *reinterpret_cast<u32x4_t*>(dst_lo + at) = u32x4_t{al[0], al[1], bl[0], bl[1]};
+      } else {
+        const u32x2_t a = e4m3_codes8(lo[t], inv), b = e4m3_codes8(hi[t], inv);
+        *reinterpret_cast<u32x4_t*>(dst_q + at) = u32x4_t{a[0], a[1], b[0], b[1]};
+      }
     }
   }
 }
@@ -562,16 +594,16 @@ hipError_t launch_row_absmax(const void* src, int n_rows, int n_cols, unsigned* 
 
 hipError_t launch_quantize_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols,
                                    const unsigned* row_amax, void* dst_q, float* dst_scale, unsigned* zero_out,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, void* dst_lo) {
   if (n_rows <= 0) return hipSuccess;
   if (n_cols <= 0 || n_cols % 64 || n_cols > 16384 || reinterpret_cast<uintptr_t>(src) % 16 ||
-      reinterpret_cast<uintptr_t>(dst_q) % 16 || (order && n_tokens <= 0))
+      reinterpret_cast<uintptr_t>(dst_q) % 16 || reinterpret_cast<uintptr_t>(dst_lo) % 16 || (order && n_tokens <= 0))
     return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>((static_cast<int64_t>(n_rows) + 15) / 16),
                   static_cast<unsigned>((n_cols / 64 + 31) / 32));
   hipLaunchKernelGGL(quantize_rows_kb_kernel, grid, dim3(kThreads), 0, stream,
                      static_cast<const bf16_t*>(src), order, n_rows, n_tokens, n_cols, row_amax,
-                     static_cast<uint8_t*>(dst_q), dst_scale, zero_out);
+                     static_cast<uint8_t*>(dst_q), dst_scale, zero_out, static_cast<uint8_t*>(dst_lo));
   return hipGetLastError();
 }
 

@@ -393,6 +393,7 @@ struct WaveCtx {
   const unsigned char* b_base[4];  // staged weight row blocks, same order
   uint32_t b_lane;
   uint32_t a_kstride;          // bytes between the 32-input blocks of an A row (64, or 64 * rows K-blocked)
+  uint32_t a_plane;            // two-term e4m3 activations: bytes from the hi to the lo codes
   int a_lane;                  // LDS byte offset of this lane's A fragment in a 16-row group
   int wave, wm, wn;
   int KT;                      // stages of 32 inputs in this block's K range
@@ -562,12 +563,16 @@ __device__ __forceinline__ void k_body(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
 // at h * kAStage in the bf16 layout, the 16 fp8 weight blocks after them.
 // One of the 6 global->LDS loads of an fp8 stage (d = 0..3: A half d >> 1,
 // row set d & 1; d = 4, 5: weight blocks).
+// With two-term e4m3 activations (X2) the A halves are the stage's 64-input
+// piece of the hi codes (h = 0) and of the lo codes (h = 1).
+template <bool X2>
 __device__ __forceinline__ void issue_one_f8(const WaveCtx& c, int kt, int buf, int d) {
   unsigned char* st = c.lds + buf * kStageF8;
   if (d < 4) {
     const int h = d >> 1, j = d & 1;
-    __builtin_amdgcn_global_load_lds(c.a_base + (c.a_off[j] + static_cast<uint32_t>(2 * kt + h) * c.a_kstride),
-                                     st + h * kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
+    const uint32_t src = X2 ? h * c.a_plane + c.a_off[j] + static_cast<uint32_t>(kt) * c.a_kstride
+                            : c.a_off[j] + static_cast<uint32_t>(2 * kt + h) * c.a_kstride;
+    __builtin_amdgcn_global_load_lds(c.a_base + src, st + h * kAStage + (c.wave * 2 + j) * 1024, 16, 0, 0);
   } else {
     const int j = d - 4;
     __builtin_amdgcn_global_load_lds(c.b_base[j] + (static_cast<uint32_t>(kt) * 1024 + c.b_lane),
@@ -593,9 +598,10 @@ __device__ __forceinline__ u32x4_t convert_frag(const u32x4_t q) {
 }
 
 // This wave's 6 loads of fp8 stage kt (its share) into buffer buf.
+template <bool X2>
 __device__ __forceinline__ void issue_share_f8(const WaveCtx& c, int kt, int buf) {
 #pragma unroll
-  for (int d = 0; d < 6; ++d) issue_one_f8(c, kt, buf, d);
+  for (int d = 0; d < 6; ++d) issue_one_f8<X2>(c, kt, buf, d);
 }
 
 // A fragments of both 32-input halves and the 8 raw fp8 weight fragments of
@@ -612,10 +618,18 @@ __device__ __forceinline__ void read_stage_f8(const WaveCtx& c, int buf, u32x4_t
 }
 
 // The 64 MFMAs of one fp8 stage, half by half; weight fragment n+1's codes
-// are converted to bf16 while fragment n's MFMAs run.
-template <int NM>
+// are converted to bf16 while fragment n's MFMAs run.  Two-term e4m3
+// activations (X2): one 16x16x128 fp8 MFMA per fragment pair, its first
+// operand the weight codes twice, its second the hi and the lo codes, so
+// the 128 products are w * hi and w * lo over the stage's 64 inputs.
+template <int NM, bool X2>
 __device__ __forceinline__ void multiply_f8(f32x4_t (&acc)[8][4], const u32x4_t (&fa)[2][4], const u32x4_t (&fq)[8]) {
-  if constexpr (NM > 0) {
+  if constexpr (X2) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) acc[n][m] = mfma_f8x2(fq[n], fq[n], fa[0][m], fa[1][m], acc[n][m]);
+  } else if constexpr (NM > 0) {
     u32x4_t cur = convert_frag<0>(fq[0]);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
@@ -647,13 +661,13 @@ __device__ __forceinline__ void multiply_f8(f32x4_t (&acc)[8][4], const u32x4_t 
 // landing.  Loads past the last stage are not issued (those slots wait for
 // everything instead); the prologue re-reads the last stage into buffers
 // that are never read when K has fewer stages than the ring.
-template <int NM, int NSETS, int G>
+template <int NM, int NSETS, int G, bool X2>
 __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]) {
   constexpr int R = kStagesF8;
   const int KT = c.KT;
   u32x4_t fa[2][4], fq[8];
 #pragma unroll
-  for (int s = 0; s < (G == 0 ? R : R - 1); ++s) issue_share_f8(c, s < KT ? s : KT - 1, s);
+  for (int s = 0; s < (G == 0 ? R : R - 1); ++s) issue_share_f8<X2>(c, s < KT ? s : KT - 1, s);
   __builtin_amdgcn_s_waitcnt(wait_vm(6 * (G == 0 ? R - 1 : R - 2), false));
   asm volatile("s_barrier" ::: "memory");
   if constexpr (G == 0) {
@@ -668,7 +682,7 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
     if constexpr (G == 0) {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
-      multiply_f8<NM>(acc, fa, fq);
+      multiply_f8<NM, X2>(acc, fa, fq);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_barrier" ::: "memory");
@@ -676,7 +690,7 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
       if constexpr (NM > 0)
         if (kt + 1 < KT) read_stage_f8<NM, NSETS>(c, rd, fa, fq);
       if (kt + R < KT) {
-        issue_share_f8(c, kt + R, wr);
+        issue_share_f8<X2>(c, kt + R, wr);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(wait_vm(6 * (R - 2), true));
       } else {
@@ -688,7 +702,7 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (NM > 0) read_stage_f8<NM, NSETS>(c, rd, fa, fq);
       if (kt + R - 1 < KT) {
-        issue_share_f8(c, kt + R - 1, wr);
+        issue_share_f8<X2>(c, kt + R - 1, wr);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(wait_vm(6 * (R - 2), true));
       } else {
@@ -698,7 +712,7 @@ __device__ __forceinline__ void k_loop_f8(const WaveCtx& c, f32x4_t (&acc)[8][4]
       asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
-      multiply_f8<NM>(acc, fa, fq);
+      multiply_f8<NM, X2>(acc, fa, fq);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_barrier" ::: "memory");
@@ -751,6 +765,7 @@ __device__ __forceinline__ WaveCtx tile_ctx(const GroupedGemmArgs& g, const Tile
   c.a_base = static_cast<const unsigned char*>(g.a);
   const bool a_kb = g.a_kb_rows > 0;
   c.a_kstride = a_kb ? static_cast<uint32_t>(g.a_kb_rows * 64) : 64u;
+  c.a_plane = static_cast<uint32_t>(g.a_lo_plane);
   // first A piece of this block's K range (bf16 pieces hold 32 inputs, fp8 pieces 64)
   const int64_t kb_first = static_cast<int64_t>(k_first) * (A8 ? 1 : kStageInputs / 32);
 #pragma unroll
@@ -867,9 +882,11 @@ __device__ __forceinline__ void run_k_body(const WaveCtx& c, f32x4_t (&acc)[8][4
 // F8: e4m3 weights.  A8 (with F8): e4m3 activations too, K-blocked in
 // 64-input pieces, on the bf16 loop's ring with 64-input stages.  One tile
 // per block.
-template <int EPI, int NSETS, bool F8, bool A8>
+// X2 (with F8 and A8): two-term e4m3 activations on the fp8 weight loop.
+template <int EPI, int NSETS, bool F8, bool A8, bool X2 = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmArgs g, int n_row_tiles,
                                                                      int n_col_tiles) {
+  static_assert(!X2 || (F8 && A8), "two-term activations: e4m3 weights and activations");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
 
   int col_tile, split;
@@ -920,24 +937,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
 
   EpiRows er;
   epi_rows_first<EPI>(g, ti, er);
-  if constexpr (F8 && !A8) {
+  if constexpr (F8 && (!A8 || X2)) {
     const int groups = (ti.rows + 15) >> 4;
     const int nm = groups > c.wm ? min(4, (groups - c.wm + 3) >> 2) : 0;
     if (wave < 4) {
       switch (nm) {
-        case 4: k_loop_f8<4, NSETS, 0>(c, acc); break;
-        case 3: k_loop_f8<3, NSETS, 0>(c, acc); break;
-        case 2: k_loop_f8<2, NSETS, 0>(c, acc); break;
-        case 1: k_loop_f8<1, NSETS, 0>(c, acc); break;
-        default: k_loop_f8<0, NSETS, 0>(c, acc); break;
+        case 4: k_loop_f8<4, NSETS, 0, X2>(c, acc); break;
+        case 3: k_loop_f8<3, NSETS, 0, X2>(c, acc); break;
+        case 2: k_loop_f8<2, NSETS, 0, X2>(c, acc); break;
+        case 1: k_loop_f8<1, NSETS, 0, X2>(c, acc); break;
+        default: k_loop_f8<0, NSETS, 0, X2>(c, acc); break;
       }
     } else {
       switch (nm) {
-        case 4: k_loop_f8<4, NSETS, 1>(c, acc); break;
-        case 3: k_loop_f8<3, NSETS, 1>(c, acc); break;
-        case 2: k_loop_f8<2, NSETS, 1>(c, acc); break;
-        case 1: k_loop_f8<1, NSETS, 1>(c, acc); break;
-        default: k_loop_f8<0, NSETS, 1>(c, acc); break;
+        case 4: k_loop_f8<4, NSETS, 1, X2>(c, acc); break;
+        case 3: k_loop_f8<3, NSETS, 1, X2>(c, acc); break;
+        case 2: k_loop_f8<2, NSETS, 1, X2>(c, acc); break;
+        case 1: k_loop_f8<1, NSETS, 1, X2>(c, acc); break;
+        default: k_loop_f8<0, NSETS, 1, X2>(c, acc); break;
       }
     }
   } else {
@@ -959,7 +976,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiled256_kernel(GroupedGemmA
     epilogue<EPI, NSETS, F8, A8, false>(g, ti, split, n0, c.wm, c.wn, lane, lds, acc, er);
 }
 
-template <int EPI, int NSETS, bool F8, bool A8>
+template <int EPI, int NSETS, bool F8, bool A8, bool X2 = false>
 hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
   // A table pointer on a GEMM the table does not cover is ignored, and so is
   // one this launcher would have to build itself for a narrow GEMM (its
@@ -967,9 +984,9 @@ hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
   GroupedGemmArgs g = g_in;
   g.ksplit_first64 = gemm_tiled256_split_first64(g);
   if (g.tile_table && gemm_tiled256_table_bytes(g) == 0) g.tile_table = nullptr;
-  constexpr int lds_bytes = F8 && !A8 ? kLdsF8 : kLds;
+  constexpr int lds_bytes = F8 && (!A8 || X2) ? kLdsF8 : kLds;
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS, F8, A8>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tiled256_kernel<EPI, NSETS, F8, A8, X2>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     (void)hipGetLastError();
     return true;
@@ -987,7 +1004,7 @@ hipError_t launch_t(const GroupedGemmArgs& g_in, hipStream_t s) {
       hipLaunchKernelGGL(tile_table_kernel, dim3(1), dim3(perm::kThreads), 0, s, g.offsets, g.n_expert, r);
     blocks = static_cast<unsigned>(8 * (r.bpx + r.steal));
   }
-  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8, A8>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
+  hipLaunchKernelGGL((gemm_tiled256_kernel<EPI, NSETS, F8, A8, X2>), dim3(blocks), dim3(kThreads), lds_bytes, s, g,
                      row_tiles, col_tiles);
   return hipGetLastError();
 }
@@ -1071,6 +1088,11 @@ bool gemm_tiled256_supported(const GroupedGemmArgs& g) {
   // number of 64-input stages per split
   if (a8 && (g.w_dtype != DT_F8 || !g.a_kb_rows || !g.a_scale || g.K % 128 || g.K / 128 < 2 * g.ksplit))
     return false;
+  // two-term activations: the lo codes a whole plane (K * a_kb_rows bytes or
+  // more) after the hi codes, 16-byte aligned, both within 32-bit offsets
+  if (g.a_lo_plane && (!a8 || g.a_lo_plane < g.K * g.a_kb_rows || g.a_lo_plane % 16 ||
+                       g.a_lo_plane + g.K * g.a_kb_rows >= (int64_t(1) << 32)))
+    return false;
   if (!g.order || !g.offsets || g.epi > EPI_SCATTER_WEIGHTED) return false;
   // bf16: an even number of 32-input stages per split; fp8: whole 64-input
   // blocks; at least two stages per split.
@@ -1098,6 +1120,11 @@ hipError_t launch_gemm_tiled256(const GroupedGemmArgs& g, hipStream_t s) {
   if (!gemm_tiled256_supported(g)) return hipErrorNotSupported;
   if (g.n_assign == 0 || g.N == 0) return hipSuccess;
   const bool f8 = g.w_dtype == DT_F8;
+  if (g.act_dtype == DT_F8 && g.a_lo_plane) {
+    if (g.epi == EPI_SWIGLU) return launch_t<EPI_SWIGLU, 2, true, true, true>(g, s);
+    if (g.epi == EPI_SCATTER_WEIGHTED) return launch_t<EPI_SCATTER_WEIGHTED, 1, true, true, true>(g, s);
+    return launch_t<EPI_SCATTER, 1, true, true, true>(g, s);
+  }
   if (g.act_dtype == DT_F8) {
     if (g.epi == EPI_SWIGLU) return launch_t<EPI_SWIGLU, 2, true, true>(g, s);
     if (g.epi == EPI_SCATTER_WEIGHTED) return launch_t<EPI_SCATTER_WEIGHTED, 1, true, true>(g, s);

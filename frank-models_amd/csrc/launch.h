@@ -136,6 +136,10 @@ struct GroupedGemmArgs {
   // 8g..8g+7 and 32+8g..32+8g+7 of the piece (the packed fp8 weights' lane
   // order), each row p dequantised by a_scale[p].
   const float* a_scale = nullptr;
+  // DT_F8 activations as two e4m3 terms per input (hi = e4m3(v), lo =
+  // e4m3(v - hi), one scale per row): the lo codes sit a_lo_plane bytes
+  // after the hi codes, in the same layout (0: one term).
+  int64_t a_lo_plane = 0;
   // SwiGLU epilogue with fp8 activations: atomic max, per output row p, of
   // the bit patterns of |h| (h rounded to bf16, so non-negative floats order
   // as unsigned integers) into row_amax[p], which starts at zero.
@@ -279,12 +283,13 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // n_cols <= 16384.
 // row_amax (may be null): max|v| of each source row as float bits, indexed
 // like src (then the rows are read once); zero_out (may be null): n_rows
-// words set to zero.
+// words set to zero.  With dst_lo, each scaled value v is carried as two
+// terms: dst_q holds hi = e4m3(v), dst_lo (same layout) lo = e4m3(v - hi).
 // launch_row_absmax: amax_out[r] = max|src[r, :]| (float bits) for src
 // [n_rows, n_cols] bf16, n_cols % 8 == 0; also clears zero_out[0, n_zero).
 hipError_t launch_quantize_rows_kb(const void* src, const int* order, int n_rows, int n_tokens, int n_cols,
                                    const unsigned* row_amax, void* dst_q, float* dst_scale, unsigned* zero_out,
-                                   hipStream_t stream);
+                                   hipStream_t stream, void* dst_lo = nullptr);
 hipError_t launch_row_absmax(const void* src, int n_rows, int n_cols, unsigned* amax_out, unsigned* zero_out,
                              int n_zero, hipStream_t stream);
 // dst (K-blocked, kb_offset with n_rows rows) row p = src row order[p] % n_tokens

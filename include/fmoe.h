@@ -55,7 +55,7 @@ typedef enum fmoe_dtype {
   FMOE_BF16 = 1,     /* bfloat16 */
   FMOE_F8E4M3FN = 2, /* OCP FP8 E4M3 (finite, NaN = 0x7F/0xFF), weights only,
                         with float32 per-output-channel scales [n_expert, n_out] */
-  FMOE_F8E4M3FN_A8 = 3 /* block and sub-layer weight dtype only: FMOE_F8E4M3FN
+  FMOE_F8E4M3FN_A8 = 3, /* block and sub-layer weight dtype only: FMOE_F8E4M3FN
                         weights (the same packed buffers and scales) whose
                         prefill-sized GEMMs also quantise their activations to
                         e4m3, one power-of-two scale per row (the smallest 2^e
@@ -64,6 +64,14 @@ typedef enum fmoe_dtype {
                         batches keep bf16 activations.  Adds the activations'
                         e4m3 rounding (about 4.7% relative Frobenius error on
                         Mixtral shapes) to the FMOE_F8E4M3FN result. */
+  FMOE_F8E4M3FN_A8X2 = 4 /* as FMOE_F8E4M3FN_A8, with each activation carried
+                        as two e4m3 terms under its row's scale, hi = e4m3(v)
+                        and lo = e4m3(v - hi), one fp8 MFMA over w * hi + w * lo:
+                        every bf16 activation whose scaled magnitude is at least
+                        2^-2 is represented exactly, so the result holds the
+                        FMOE_F8E4M3FN tolerance (within rounding of the bf16
+                        path) while the products run on the fp8 MFMA, at the
+                        MFMA time of the bf16 path (two terms per input). */
 } fmoe_dtype;
 
 /* Message describing the last failure on this thread ("" if none). */
@@ -73,9 +81,10 @@ const char *fmoe_last_error(void);
  * 2: the kernel-path override (fmoe_set_gemm_path and its enum) moved to
  *    fmoe_diag.h; FMOE_TIMER_QUANT added (FMOE_TIMER_COUNT 10 -> 11); dtype
  *    FMOE_F8E4M3FN_A8 (3); fmoe_moe_ffn_block_noalloc.  Packed-weight
- *    artifacts record the version they were written under. */
+ *    artifacts record the version they were written under.
+ * 3: dtype FMOE_F8E4M3FN_A8X2 (4). */
 int fmoe_abi_version(void);
-#define FMOE_ABI_VERSION 2
+#define FMOE_ABI_VERSION 3
 
 /* Checks that the current HIP device is a gfx950; writes its ordinal and
  * architecture name (arch may be NULL).  FMOE_ERR_NO_DEVICE otherwise. */
@@ -103,7 +112,7 @@ typedef enum fmoe_timer {
   FMOE_TIMER_QKV = 7,     /* decode attention: Q/K/V projection + bias + RoPE */
   FMOE_TIMER_ATTENTION = 8, /* decode attention: context splits + combine */
   FMOE_TIMER_OUT_PROJ = 9,  /* decode attention: output projection + bias */
-  FMOE_TIMER_QUANT = 10,    /* e4m3 quantisation of the GEMM activations (FMOE_F8E4M3FN_A8) */
+  FMOE_TIMER_QUANT = 10,    /* e4m3 quantisation of the GEMM activations (FMOE_F8E4M3FN_A8, _A8X2) */
   FMOE_TIMER_COUNT = 11
 } fmoe_timer;
 int fmoe_timing_enable(int on);

@@ -198,13 +198,17 @@ def moe_ffn_block(
     reference): the GEMM inputs -- the token rows, and the SwiGLU rows after
     rounding to bf16 -- are replaced by their per-row e4m3 quantisation
     (``numerics.fake_quantize_rows_e4m3fn``); routing still uses the
-    unquantised rows."""
+    unquantised rows.  ``act_quant="x2"`` replaces them by their two-term
+    quantisation instead (``numerics.fake_quantize_rows_e4m3fn_x2``)."""
+    if act_quant not in (False, True, "x2"):
+        raise ValueError(f"act_quant must be False, True or 'x2', not {act_quant!r}")
+    fq = _nm.fake_quantize_rows_e4m3fn_x2 if act_quant == "x2" else _nm.fake_quantize_rows_e4m3fn
     x = np.asarray(input, dtype=dtype)
     T, H = x.shape
     if H != n_embd:
         raise ValueError(f"input hidden {H} != n_embd {n_embd}")
     ids, w = router(x, gate_inp_w, n_expert_used, normalize_weights, dtype)
-    xg = _nm.fake_quantize_rows_e4m3fn(x).astype(dtype) if act_quant else x
+    xg = fq(x).astype(dtype) if act_quant else x
     k = int(n_expert_used)
     y = np.zeros((k, T, H), dtype=dtype)
     for e in np.unique(ids):
@@ -216,7 +220,7 @@ def moe_ffn_block(
         gate = xe @ np.ascontiguousarray(gate_exps_w[:, :, int(e)], dtype=dtype).T
         h = swiglu(gate, up)
         if act_quant:
-            h = _nm.fake_quantize_rows_e4m3fn(_nm.bf16_round(h)).astype(dtype)
+            h = fq(_nm.bf16_round(h)).astype(dtype)
         d = h @ np.ascontiguousarray(down_exps_w[:, :, int(e)], dtype=dtype).T
         y[s_idx, t_idx] = d * w[s_idx, t_idx][:, None]
     out = y[0].copy()

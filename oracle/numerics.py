@@ -116,3 +116,24 @@ def fake_quantize_rows_e4m3fn(a: np.ndarray) -> np.ndarray:
     """``decode(q) * scale`` of ``quantize_rows_e4m3fn(a)`` (float32)."""
     q, scale = quantize_rows_e4m3fn(a)
     return (e4m3fn_decode(q) * scale[:, None]).astype(np.float32)
+
+
+def quantize_rows_e4m3fn_x2(a: np.ndarray):
+    """Two-term per-row e4m3fn quantisation (the FMOE_F8E4M3FN_A8X2 GEMM
+    operand; no counterpart in the reference): the row scale of
+    ``quantize_rows_e4m3fn``, ``hi = e4m3fn_encode(a / scale)`` (its codes),
+    and ``lo = e4m3fn_encode(a / scale - decode(hi))``, the rounding
+    remainder as a second code under the same scale.  Returns
+    ``(hi uint8, lo uint8, scale float32)``; the represented value is
+    ``(decode(hi) + decode(lo)) * scale``."""
+    hi, scale = quantize_rows_e4m3fn(a)
+    v = (np.asarray(a, dtype=np.float32) / scale[:, None]).astype(np.float32)
+    lo = e4m3fn_encode((v - e4m3fn_decode(hi)).astype(np.float32))
+    return hi, lo, scale
+
+
+def fake_quantize_rows_e4m3fn_x2(a: np.ndarray) -> np.ndarray:
+    """``(decode(hi) + decode(lo)) * scale`` of ``quantize_rows_e4m3fn_x2(a)``
+    (float32)."""
+    hi, lo, scale = quantize_rows_e4m3fn_x2(a)
+    return ((e4m3fn_decode(hi) + e4m3fn_decode(lo)) * scale[:, None]).astype(np.float32)

@@ -48,7 +48,7 @@ def test_library_exports_every_declared_symbol(fm):
 def test_abi_version(fm):
     text = (Path(__file__).resolve().parents[1] / "include" / "fmoe.h").read_text()
     declared = int(re.search(r"#define FMOE_ABI_VERSION (\d+)", text).group(1))
-    assert declared == 2
+    assert declared == 3
     assert fm.lowlevel.lib().fmoe_abi_version() == declared
 
 
@@ -267,3 +267,19 @@ def test_noalloc_block_rejects_oversize_before_device(fm):
               0, 8, 2, 64, 128, 0, ll.BF16, None) == ll.OK  # no tokens
     assert st(fm, "fmoe_moe_ffn_block_noalloc", fake, None, fake, fake, fake, None, None, None, ll.BF16, fake,
               16, 8, 2, 64, 128, 0, ll.BF16, None) == ll.ERR_INVALID_ARGUMENT  # null router
+
+
+def test_two_term_fp8_activations_workspace(fm):
+    """FMOE_F8E4M3FN_A8X2 takes the FMOE_F8E4M3FN_A8 workspace plus a second
+    code plane for the token rows and for the SwiGLU rows (n * (H + F) bytes
+    at least); decode-sized batches need none of it."""
+    ll = fm.lowlevel
+    lib = ll.lib()
+    T, E, k, H, F = 4096, 8, 2, 4096, 14336
+    one = lib.fmoe_moe_ffn_block_workspace_bytes(T, E, k, H, F, ll.BF16, ll.F8E4M3FN_A8)
+    two = lib.fmoe_moe_ffn_block_workspace_bytes(T, E, k, H, F, ll.BF16, ll.F8E4M3FN_A8X2)
+    assert two - one >= T * k * (H + F)
+    dec = [lib.fmoe_moe_ffn_block_workspace_bytes(16, E, k, H, F, ll.BF16, d)
+           for d in (ll.F8E4M3FN, ll.F8E4M3FN_A8, ll.F8E4M3FN_A8X2)]
+    assert dec[0] == dec[1] == dec[2]
+    assert lib.fmoe_moe_ffn_block_workspace_bytes(T, E, k, H, F, ll.BF16, 5) == 0

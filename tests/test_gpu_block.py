@@ -271,6 +271,61 @@ def test_fp8_activations_decode_keeps_bf16(fm, wl):
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+# ------------------------------------------------------------------ two-term fp8 activations
+# FMOE_F8E4M3FN_A8X2: the prefill GEMMs on the fp8 MFMA with every
+# activation carried as two e4m3 terms under its row's scale.  Held to C5's
+# own criterion against the plain oracle (dequantised weights, bf16
+# activations): element-wise 5e-2 |e| + 5e-2 RMS(e).  Pinned tighter against
+# the oracle on the same two-term rows (bf16 tolerance: the two terms hold
+# the bf16 token and SwiGLU values exactly above 2^-2 of their row scale, so
+# a SwiGLU value one bf16 ulp off moves its row by one bf16 ulp only), and
+# against the bf16-activation block on the same fp8 weights.
+@pytest.mark.parametrize("name,H,F,T", [("C5", 4096, 14336, 4096), ("C5", 512, 1024, 700), ("C3", 512, 256, 900),
+                                        ("C2", 1024, 2048, 300)])
+def test_fp8_x2_activations_prefill(fm, wl, name, H, F, T):
+    cfg = wl.CONFIGS[name] if (H, F) == (wl.CONFIGS[name].n_embd, wl.CONFIGS[name].n_ff) else _scaled(wl, name, H, F)
+    cfg = wl.scaled(cfg, H, F, weights="fp8", rtol=5e-2) if cfg.weights != "fp8" else cfg
+    case = Case(fm, wl, cfg, T)
+    blk = fm.MoEFFNBlock(case.wr, *case.packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                         cfg.normalize, act_dtype=torch.bfloat16, fp8_activations="x2")
+    assert blk.wdt == fm.lowlevel.F8E4M3FN_A8X2
+    out = blk(case.x)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    ids_dev, _, order, offsets = blk.routing(T)
+    c = cfg
+    ref_x2, ids, _ = om.moe_ffn_block(case.x_np, case.wr_np, *case.host_w, c.n_expert, c.n_expert_used, c.n_embd,
+                                      c.n_ff, c.normalize, dtype=np.float32, return_routing=True, act_quant="x2")
+    np.testing.assert_array_equal(ids_dev.cpu().numpy(), ids)
+    ro, roff = om.permute(ids, c.n_expert)
+    np.testing.assert_array_equal(order.cpu().numpy(), ro)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), roff)
+    assert_close_rms(out, ref_x2, 2e-2, what=f"{name} H={H} F={F} T={T} vs the two-term oracle")
+    ref, _, _ = case.oracle(dtype=np.float32)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} F={F} T={T} vs the bf16-activation oracle")
+    bf = case.run()
+    rel = float(np.linalg.norm(out - bf) / np.linalg.norm(bf))
+    rel_ref = float(np.linalg.norm(out - ref) / np.linalg.norm(ref))
+    print(f"two-term fp8 activations {name} H={H} F={F} T={T}: rel Frobenius vs bf16-activation block {rel:.2e}, "
+          f"vs oracle {rel_ref:.2e}, worst |err| / RMS {np.abs(out - ref).max() / np.sqrt(np.mean(ref**2)):.3f}")
+    assert rel <= 1e-2, rel
+    # the fp8 path really ran: its sums differ from the bf16-activation block's
+    assert not np.array_equal(out, bf)
+
+
+def test_fp8_x2_activations_decode_keeps_bf16(fm, wl):
+    """Decode-sized batches stream the weights with bf16 activations either way."""
+    cfg = wl.CONFIGS["C5"]
+    case = Case(fm, wl, cfg, 16)
+    blk = fm.MoEFFNBlock(case.wr, *case.packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                         cfg.normalize, act_dtype=torch.bfloat16, fp8_activations="x2")
+    a = blk(case.x).float().cpu().numpy()
+    np.testing.assert_array_equal(a.view(np.uint32), case.run().view(np.uint32))
+    with pytest.raises(ValueError):
+        fm.MoEFFNBlock(case.wr, *case.packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
+                       cfg.normalize, act_dtype=torch.bfloat16, fp8_activations="x3")
+
+
 # ------------------------------------------------------------------ fused decode down + combine
 # Batches of at most 16 assignments take the down projection and the combine
 # in one launch under the automatic kernel choice; forcing the streaming

@@ -535,6 +535,59 @@ def test_act_quant_block_is_the_block_on_quantised_rows():
     assert 1e-3 < rel < 0.1, rel
 
 
+def test_quantize_rows_e4m3fn_x2_is_exact_on_bf16_rows():
+    """Two-term rows (hi = e4m3(v), lo = e4m3(v - hi) under one power-of-two
+    row scale).  What the arithmetic fixes: a bf16 value v (8 significant
+    bits) scaled into (224, 448] has hi = v rounded to 4 significant bits,
+    so v - hi is a multiple of v's last bit of at most 4 bits, which lo holds
+    exactly while that bit is at least e4m3's smallest step 2^-9, i.e. for
+    |v| >= 2^-2; below, lo rounds to the 2^-9 grid (error at most 2^-10)."""
+    rng = np.random.default_rng(11)
+    a = nm.bf16_round((rng.standard_normal((64, 512)) * rng.uniform(0.01, 100, (64, 1))).astype(np.float32))
+    a[:, :64] *= np.float32(2.0**-12)  # some tiny entries, below the exact range
+    hi, lo, s = nm.quantize_rows_e4m3fn_x2(a)
+    q1, s1 = nm.quantize_rows_e4m3fn(a)
+    np.testing.assert_array_equal(hi, q1)  # hi is the one-term quantisation
+    np.testing.assert_array_equal(s, s1)
+    v = a / s[:, None]
+    d = nm.fake_quantize_rows_e4m3fn_x2(a) / s[:, None]
+    big = np.abs(v) >= 2.0**-2
+    assert big.mean() > 0.5 and (~big).any()
+    np.testing.assert_array_equal(d[big], v[big])
+    assert np.all(np.abs(d - v)[~big] <= 2.0**-10)
+    # lo is at most half an ulp of hi: 2^-4 of the value
+    assert np.all(np.abs(nm.e4m3fn_decode(lo)) <= 2.0**-4 * np.abs(v) * (1 + 1e-6) + 2.0**-10)
+    # planted mistakes: lo coded from v (not its remainder), or one term only
+    wrong = (nm.e4m3fn_decode(hi) + nm.e4m3fn_decode(nm.e4m3fn_encode(v))) * s[:, None]
+    assert not np.allclose(wrong, a, rtol=1e-3)
+    assert not np.array_equal(nm.fake_quantize_rows_e4m3fn(a)[big], a[big])
+
+
+def test_act_quant_x2_block_is_the_block_on_two_term_rows():
+    """E = k = 1: the two-term block is the dense SwiGLU FFN on the two-term
+    token rows and bf16-rounded SwiGLU rows, and since those rows are bf16
+    values represented exactly (above 2^-2 of their scale), it stays within
+    bf16-level rounding of the unquantised block, unlike the one-term block."""
+    rng = np.random.default_rng(12)
+    T, H, F = 24, 64, 128
+    x = nm.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    wr = np.zeros((1, H), np.float32)
+    up, gate = ((rng.standard_normal((F, H, 1)) * 0.05).astype(np.float32) for _ in range(2))
+    down = (rng.standard_normal((H, F, 1)) * 0.05).astype(np.float32)
+    out = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, dtype=np.float64, act_quant="x2")
+    xq = nm.fake_quantize_rows_e4m3fn_x2(x).astype(np.float64)
+    g, u = xq @ gate[:, :, 0].T.astype(np.float64), xq @ up[:, :, 0].T.astype(np.float64)
+    h = nm.fake_quantize_rows_e4m3fn_x2(nm.bf16_round(g * u / (1 + np.exp(-u)))).astype(np.float64)
+    np.testing.assert_allclose(out, h @ down[:, :, 0].T.astype(np.float64), rtol=1e-12, atol=1e-12)
+    plain = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, dtype=np.float64)
+    one = om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, dtype=np.float64, act_quant=True)
+    rel2 = np.linalg.norm(out - plain) / np.linalg.norm(plain)
+    rel1 = np.linalg.norm(one - plain) / np.linalg.norm(plain)
+    assert rel2 < 5e-3 and rel2 < rel1 / 5, (rel2, rel1)
+    with pytest.raises(ValueError):
+        om.moe_ffn_block(x, wr, up, gate, down, 1, 1, H, F, False, act_quant="x3")
+
+
 def _branchfree_e4m3(x):
     """The kernels' branch-free float -> e4m3fn encoder (common.h
     f32_to_e4m3fn), step for step in NumPy integer arithmetic."""
