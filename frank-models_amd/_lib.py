@@ -82,6 +82,7 @@ SIGNATURES = {
     "fmoe_set_gemm_path": (_c_int, [_c_int]),
     "fmoe_get_gemm_path": (_c_int, []),
     "fmoe_last_gemm_path": (_c_int, []),
+    "fmoe_quantize_rows_e4m3": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "fmoe_timing_enable": (_c_int, [_c_int]),
     "fmoe_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64), _c_int]),
     "fmoe_swiglu": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _vp]),

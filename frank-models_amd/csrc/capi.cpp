@@ -972,6 +972,20 @@ int fmoe_set_gemm_path(int path) {
 
 int fmoe_get_gemm_path(void) { return g_path.load(); }
 
+int fmoe_quantize_rows_e4m3(const void* src, int64_t n_rows, int64_t n_cols, void* dst_hi, void* dst_lo,
+                            float* dst_scale, void* stream) {
+  FMOE_TRY(check_dims("n_rows", n_rows, 0, kMaxDim));
+  FMOE_TRY(check_dims("n_cols", n_cols, 64, 16384));
+  if (n_cols % 64) return fail(FMOE_ERR_SHAPE, "n_cols=%lld is not a multiple of 64", static_cast<long long>(n_cols));
+  if (n_rows == 0) return ok();
+  if (!src || !dst_hi || !dst_scale) return fail(FMOE_ERR_INVALID_ARGUMENT, "null pointer");
+  FMOE_TRY(ensure_device());
+  FMOE_HIP(launch_quantize_rows_kb(src, nullptr, static_cast<int>(n_rows), static_cast<int>(n_rows),
+                                   static_cast<int>(n_cols), nullptr, dst_hi, dst_scale, nullptr,
+                                   static_cast<hipStream_t>(stream), dst_lo));
+  return ok();
+}
+
 int fmoe_last_gemm_path(void) { return g_last_path; }
 
 int fmoe_timing_enable(int on) {

@@ -160,16 +160,21 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kb_kernel(const bf16_t* 
   }
 }
 
-// 8 bf16 values times inv -> 8 e4m3fn codes in two dwords (element order).
+// 8 bf16 values times inv -> 8 e4m3fn codes in two dwords (element order),
+// two values per v_cvt_pk_fp8_f32 (round to nearest even).  The row scale
+// keeps every scaled value within +-448, so the instruction's overflow
+// behaviour never applies; the codes equal f32_to_e4m3fn's (checked against
+// the oracle on every e4m3 value, every tie and its neighbours).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
 __device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
   uint32_t w[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
-    const uint32_t c0 = f32_to_e4m3fn(__uint_as_float(v[2 * d] << 16) * inv);
-    const uint32_t c1 = f32_to_e4m3fn(__uint_as_float(v[2 * d] & 0xFFFF0000u) * inv);
-    const uint32_t c2 = f32_to_e4m3fn(__uint_as_float(v[2 * d + 1] << 16) * inv);
-    const uint32_t c3 = f32_to_e4m3fn(__uint_as_float(v[2 * d + 1] & 0xFFFF0000u) * inv);
-    w[d] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d]) * inv, bf16_hi(v[2 * d]) * inv, 0, false);
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d + 1]) * inv, bf16_hi(v[2 * d + 1]) * inv, c, true);
+    w[d] = static_cast<uint32_t>(c);
   }
   return u32x2_t{w[0], w[1]};
 }
@@ -177,23 +182,22 @@ __device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
 // The same codes as e4m3_codes8 (hi), and in lo the codes of each value's
 // remainder, e4m3(v * inv - hi): the two terms hold every bf16 value whose
 // scaled magnitude is at least 2^-2 exactly (hi keeps its top 4 significant
-// bits, the remainder fits the next 4 within lo's exponent range).
+// bits, the remainder fits the next 4 within lo's exponent range).  hi is
+// decoded back exactly with v_cvt_pk_f32_fp8.
 __device__ __forceinline__ void e4m3_codes8_x2(const u32x4_t v, float inv, u32x2_t& hi, u32x2_t& lo) {
-  uint32_t wh[2], wl[2];
+  hi = e4m3_codes8(v, inv);
+  uint32_t wl[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
-    wh[d] = 0u;
-    wl[d] = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t word = v[2 * d + (i >> 1)];
-      const float x = __uint_as_float((i & 1) ? (word & 0xFFFF0000u) : (word << 16)) * inv;
-      const uint32_t h = f32_to_e4m3fn(x);
-      wh[d] |= h << (8 * i);
-      wl[d] |= f32_to_e4m3fn(x - e4m3fn_to_f32(h)) << (8 * i);
-    }
+    const int h = static_cast<int>(hi[d]);
+    const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(h, false);
+    const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(h, true);
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d]) * inv - h01[0], bf16_hi(v[2 * d]) * inv - h01[1], 0,
+                                            false);
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d + 1]) * inv - h23[0], bf16_hi(v[2 * d + 1]) * inv - h23[1],
+                                        c, true);
+    wl[d] = static_cast<uint32_t>(c);
   }
-  hi = u32x2_t{wh[0], wh[1]};
   lo = u32x2_t{wl[0], wl[1]};
 }
 

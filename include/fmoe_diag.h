@@ -10,6 +10,7 @@
  */
 #ifndef FMOE_DIAG_H_
 #define FMOE_DIAG_H_
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -34,6 +35,17 @@ int fmoe_set_gemm_path(int path);
 int fmoe_get_gemm_path(void);
 /* The family used by the last grouped GEMM launched on this thread. */
 int fmoe_last_gemm_path(void);
+/* The row quantiser of the fp8-activation GEMMs (FMOE_F8E4M3FN_A8 / _A8X2),
+ * exposed so tests can compare its codes with the oracle bit for bit: rows
+ * of src [n_rows, n_cols] bf16 (n_cols % 64 == 0, <= 16384), each scaled by
+ * the smallest power of two 2^e with max|row| / 2^e <= 448 (dst_scale[r] =
+ * 2^e), hi = e4m3(v) into dst_hi and, when dst_lo is not NULL, lo =
+ * e4m3(v - hi) into dst_lo, both K-blocked in 64-input pieces (piece j of
+ * row r at byte (j * n_rows + r) * 64, its 16-byte chunk g holding inputs
+ * 64j + 8g + [0, 8) then 64j + 32 + 8g + [0, 8)).  Device pointers, 16-byte
+ * aligned.  No counterpart in the reference. */
+int fmoe_quantize_rows_e4m3(const void *src, int64_t n_rows, int64_t n_cols, void *dst_hi, void *dst_lo,
+                            float *dst_scale, void *stream);
 
 #ifdef __cplusplus
 }

@@ -347,3 +347,62 @@ def test_moe_ffn_block_reference_cases(fm, case):
     out = fm.moe_ffn_block(x, wr, up, gate, down, E, k, H, F, norm)
     assert out.shape == (T, H) and out.dtype == np.float32
     assert_close(out, om.moe_ffn_block_literal(x, wr, up, gate, down, E, k, H, F, norm), rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------------------------ e4m3 row quantiser
+def _unblock_e4m3(q, n_rows, n_cols):
+    """K-blocked 64-input pieces (chunk g: inputs 8g..8g+7, 32+8g..32+8g+7)
+    -> [n_rows, n_cols] codes in input order."""
+    q = q.reshape(n_cols // 64, n_rows, 4, 2, 8)  # piece, row, chunk g, half, byte
+    out = np.empty((n_rows, n_cols // 64, 2, 4, 8), np.uint8)  # row, piece, half, g, byte
+    out[:] = q.transpose(1, 0, 3, 2, 4)
+    return out.reshape(n_rows, n_cols)
+
+
+def _quantizer_rows():
+    """bf16 rows whose scaled values hit every e4m3 value, every midpoint
+    between neighbours (the round-to-nearest-even ties), one bf16 ulp either
+    side of each midpoint, and the subnormal range, at several row scales and
+    both signs; then random rows of mixed magnitudes and an all-zero row."""
+    vals = nm.E4M3FN_VALUES[:127].astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    b = lambda a: nm.bf16_round(np.asarray(a, np.float32))
+    pts = np.concatenate([vals, mids, b(mids) * (1 + 2.0**-7), b(mids) * (1 - 2.0**-8), np.linspace(0, 2.0**-6, 40)])
+    pts = b(pts)
+    n_cols = 512
+    rows = []
+    for s in (-20, -3, 0, 5):
+        for sign in (1.0, -1.0):
+            for off in range(0, len(pts), n_cols - 1):
+                r = np.zeros(n_cols, np.float32)
+                chunk = pts[off:off + n_cols - 1]
+                r[0] = 448.0  # fixes the row scale at 2^s
+                r[1:1 + len(chunk)] = sign * chunk
+                rows.append(b(r * np.float32(2.0**s)))
+    rng = np.random.default_rng(21)
+    for _ in range(40):
+        rows.append(b(rng.standard_normal(n_cols) * 10.0 ** rng.uniform(-6, 4)))
+    rows.append(np.zeros(n_cols, np.float32))
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("two_terms", [False, True])
+def test_row_quantizer_codes_match_the_oracle(fm, two_terms):
+    a = _quantizer_rows()
+    n_rows, n_cols = a.shape
+    src = torch.from_numpy(a).to("cuda", torch.bfloat16)
+    hi = torch.zeros(n_rows * n_cols, dtype=torch.uint8, device="cuda")
+    lo = torch.zeros_like(hi)
+    sc = torch.zeros(n_rows, dtype=torch.float32, device="cuda")
+    ll = fm.lowlevel
+    ll.check(ll.lib().fmoe_quantize_rows_e4m3(src.data_ptr(), n_rows, n_cols, hi.data_ptr(),
+                                              lo.data_ptr() if two_terms else None, sc.data_ptr(),
+                                              torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    rh, rl, rs = nm.quantize_rows_e4m3fn_x2(src.float().cpu().numpy())
+    np.testing.assert_array_equal(sc.cpu().numpy(), rs)
+    np.testing.assert_array_equal(_unblock_e4m3(hi.cpu().numpy(), n_rows, n_cols), rh)
+    if two_terms:
+        np.testing.assert_array_equal(_unblock_e4m3(lo.cpu().numpy(), n_rows, n_cols), rl)
+    else:
+        assert not lo.any()
