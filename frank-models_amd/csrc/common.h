@@ -133,6 +133,64 @@ __device__ __forceinline__ float absmax_bf16x8(const u32x4_t v) {
   return m;
 }
 
+// ---------------------------------------------------------------- e4m3 activation codes
+// 8 bf16 values times inv -> 8 e4m3fn codes in two dwords (element order),
+// two values per v_cvt_pk_fp8_f32 (round to nearest even).  The row scale
+// keeps every scaled value within +-448, so the instruction's overflow
+// behaviour never applies; the codes equal f32_to_e4m3fn's (checked against
+// the oracle on every e4m3 value, every tie and its neighbours).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+__device__ __forceinline__ u32x2_t e4m3_codes8(const u32x4_t v, float inv) {
+  uint32_t w[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d]) * inv, bf16_hi(v[2 * d]) * inv, 0, false);
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d + 1]) * inv, bf16_hi(v[2 * d + 1]) * inv, c, true);
+    w[d] = static_cast<uint32_t>(c);
+  }
+  return u32x2_t{w[0], w[1]};
+}
+
+// The same codes as e4m3_codes8 (hi), and in lo the codes of each value's
+// remainder, e4m3(v * inv - hi): the two terms hold every bf16 value whose
+// scaled magnitude is at least 2^-2 exactly (hi keeps its top 4 significant
+// bits, the remainder fits the next 4 within lo's exponent range).  hi is
+// decoded back exactly with v_cvt_pk_f32_fp8.
+__device__ __forceinline__ void e4m3_codes8_x2(const u32x4_t v, float inv, u32x2_t& hi, u32x2_t& lo) {
+  hi = e4m3_codes8(v, inv);
+  uint32_t wl[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const int h = static_cast<int>(hi[d]);
+    const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(h, false);
+    const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(h, true);
+    int c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d]) * inv - h01[0], bf16_hi(v[2 * d]) * inv - h01[1], 0,
+                                            false);
+    c = __builtin_amdgcn_cvt_pk_fp8_f32(bf16_lo(v[2 * d + 1]) * inv - h23[0], bf16_hi(v[2 * d + 1]) * inv - h23[1],
+                                        c, true);
+    wl[d] = static_cast<uint32_t>(c);
+  }
+  lo = u32x2_t{wl[0], wl[1]};
+}
+
+// Power-of-two scale 2^e of a row whose largest magnitude is amax: the
+// smallest e with amax / 2^e <= 448 (448 = 1.75 * 2^8), clamped to
+// [-126, 126]; 1 for amax = 0.  *inv = 2^-e.  Exact to apply, and each
+// value's rounding depends only on the value and its binade.
+__device__ __forceinline__ float pow2_scale(float amax, float* inv) {
+  if (!(amax > 0.f)) {
+    *inv = 1.f;
+    return 1.f;
+  }
+  const uint32_t ab = __float_as_uint(amax);
+  int e = static_cast<int>(ab >> 23) - 127 - 8 + ((ab & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+  e = min(max(e, -126), 126);
+  *inv = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+  return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
 // ---------------------------------------------------------------- waves
 // Maximum over each 16-lane row of a wave (DPP row rotations; every lane of
 // the row must take part and gets the result).
