@@ -66,7 +66,7 @@ RES_SCALE = {"C1": (0.25, 4.0), "C2": (0.1, 1.5), "C3": (0.25, 4.0), "C4": (0.02
 
 
 class SubCase:
-    def __init__(self, fm, wl, cfg, T, scale_range=None):
+    def __init__(self, fm, wl, cfg, T, scale_range=None, fp8_activations=False):
         self.cfg, self.T = cfg, T
         res, nw, wr, eps, _ = wl.sublayer_inputs(cfg, T, scale_range=scale_range or RES_SCALE[cfg.name[:2]])
         act = torch.bfloat16 if cfg.act == "bf16" else torch.float32
@@ -89,7 +89,7 @@ class SubCase:
             packed = [fm.pack_expert_weights(w) for w in (up, gate, down)]
             self.host_w = [w.float().cpu().numpy() for w in (up, gate, down)]
         self.block = fm.MoEFFNBlock(wr_t, *packed, cfg.n_expert, cfg.n_expert_used, cfg.n_embd, cfg.n_ff,
-                                    cfg.normalize, act_dtype=act)
+                                    cfg.normalize, act_dtype=act, fp8_activations=fp8_activations)
 
     def run(self, out=None):
         o = self.block.sublayer(self.res if out is None else out, self.nw, self.eps, out=out)
@@ -164,6 +164,21 @@ def test_sublayer_one_token_fused(fm, wl, name, scale):
     buf = case.res.clone()
     again = case.run(out=buf)
     np.testing.assert_array_equal(out.view(np.uint32), again.view(np.uint32))
+
+
+def test_sublayer_two_term_fp8_activations(fm, wl):
+    """The sub-layer with fp8 weights and two-term e4m3 activations at a
+    prefill size (both GEMMs on the fp8 MFMA, the residual added in the
+    combine): within C5's tolerance of the oracle on the dequantised weights
+    with bf16 activations, and in place equal to out of place."""
+    cfg = wl.scaled(wl.CONFIGS["C5"], 512, 1024)
+    case = SubCase(fm, wl, cfg, 300, fp8_activations="x2")
+    assert case.block.wdt == fm.lowlevel.F8E4M3FN_A8X2
+    a = case.run()
+    case.check(a)
+    buf = case.res.clone()
+    b = case.run(out=buf)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_sublayer_in_place_equals_out_of_place(fm, wl):
