@@ -59,14 +59,26 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // size D at position pos: angle pos * freq_scale / freq_base^(2i/D) in
 // double precision (components/position/rope.mlir:38-104,
 // oracles/position.py:6-50).
-__device__ __forceinline__ void rope_pair(float x0, float x1, int64_t pos, int i, int D, double freq_base,
-                                          double freq_scale, float& y0, float& y1) {
+// rope_cos_sin gives the pair's (cos, sin) rounded to float, rope_apply the
+// rotation; split so a kernel can compute the angles ahead of its data.  The
+// rotation's fused multiply-adds are written out so that every kernel that
+// applies it rounds the same way (left to the compiler, the contraction of
+// a * c - b * s may pick either product).
+__device__ __forceinline__ float2 rope_cos_sin(int64_t pos, int i, int D, double freq_base, double freq_scale) {
   const double freq = freq_scale / pow(freq_base, static_cast<double>(2 * i) / D);
   double sn, cs;
   sincos(static_cast<double>(pos) * freq, &sn, &cs);
-  const float cf = static_cast<float>(cs), sf = static_cast<float>(sn);
-  y0 = x0 * cf - x1 * sf;
-  y1 = x0 * sf + x1 * cf;
+  return float2{static_cast<float>(cs), static_cast<float>(sn)};
+}
+
+__device__ __forceinline__ void rope_apply(float x0, float x1, float2 cs, float& y0, float& y1) {
+  y0 = __builtin_fmaf(x0, cs.x, -(x1 * cs.y));
+  y1 = __builtin_fmaf(x0, cs.y, x1 * cs.x);
+}
+
+__device__ __forceinline__ void rope_pair(float x0, float x1, int64_t pos, int i, int D, double freq_base,
+                                          double freq_scale, float& y0, float& y1) {
+  rope_apply(x0, x1, rope_cos_sin(pos, i, D, freq_base, freq_scale), y0, y1);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {

@@ -59,9 +59,11 @@ __device__ __forceinline__ int64_t a_source_row(const GroupedGemmArgs& g, int p)
 // (each element is read and written by the same lane).  EPI_QKV_ROPE: the
 // column groups of 4 lie inside one of the q | k | v parts (nq, nkv
 // multiples of 4) and hold two RoPE pairs of one head (head_dim even).
-template <int EPI>
+// CS: the pairs' (cos, sin) come precomputed in cs0 / cs1 (rope_cos_sin of
+// the same position and pair), else they are computed here.
+template <int EPI, bool CS = false>
 __device__ __forceinline__ void store4_proj(const GroupedGemmArgs& g, int p, int64_t n, float v0, float v1,
-                                            float v2, float v3) {
+                                            float v2, float v3, float2 cs0 = float2{}, float2 cs1 = float2{}) {
   const ProjEpilogue& e = g.pe;
   if (EPI == EPI_LINEAR) {
     if (e.bias) v0 += e.bias[n], v1 += e.bias[n + 1], v2 += e.bias[n + 2], v3 += e.bias[n + 3];
@@ -88,11 +90,16 @@ __device__ __forceinline__ void store4_proj(const GroupedGemmArgs& g, int p, int
     const int64_t c = is_q ? n : n - nq;
     const float* b = is_q ? e.bias : e.bias_k;
     if (b) v0 += b[c], v1 += b[c + 1], v2 += b[c + 2], v3 += b[c + 3];
-    const int64_t pos = e.positions[p];
-    const int i0 = static_cast<int>(c % e.head_dim) / 2;
     float y0, y1, y2, y3;
-    rope_pair(v0, v1, pos, i0, e.head_dim, e.freq_base, e.freq_scale, y0, y1);
-    rope_pair(v2, v3, pos, i0 + 1, e.head_dim, e.freq_base, e.freq_scale, y2, y3);
+    if (CS) {
+      rope_apply(v0, v1, cs0, y0, y1);
+      rope_apply(v2, v3, cs1, y2, y3);
+    } else {
+      const int64_t pos = e.positions[p];
+      const int i0 = static_cast<int>(c % e.head_dim) / 2;
+      rope_pair(v0, v1, pos, i0, e.head_dim, e.freq_base, e.freq_scale, y0, y1);
+      rope_pair(v2, v3, pos, i0 + 1, e.head_dim, e.freq_base, e.freq_scale, y2, y3);
+    }
     if (is_q)
       *reinterpret_cast<float4*>(e.q_out + static_cast<int64_t>(p) * nq + c) = float4{y0, y1, y2, y3};
     else
@@ -523,69 +530,103 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
 // once per launch), as gemm_stream_kernel's, so the weights do not push the
 // token rows and the next kernel's data out of the caches.
 constexpr int kNonTemporal = 2;
+// The Q/K/V kernel's block has two more waves: they compute the RoPE
+// (cos, sin) of each (row, pair) of the block's 16 columns into LDS while
+// the four streaming waves wait on their loads, so the epilogue only
+// rotates.  The angles are rope_cos_sin's, so the results are unchanged.
+constexpr int kRopeWaves = 2;
+constexpr int kRopeItems = kStreamRows * kStreamRows / 2;  // rows x pairs
+static_assert(kRopeItems == kRopeWaves * kWave, "one (row, pair) per angle lane");
 
-template <int D>
+template <int EPI>
+constexpr int stream_lds_threads() {
+  return kThreads + (EPI == EPI_QKV_ROPE ? kRopeWaves * kWave : 0);
+}
+
+template <int D, int EPI>
 constexpr int stream_lds_bytes() {
-  return kStreamWaves * D * 2048 + (kStreamWaves - 1) * kWave * 16;
+  return kStreamWaves * D * 2048 + (kStreamWaves - 1) * kWave * 16 + (EPI == EPI_QKV_ROPE ? kRopeItems * 8 : 0);
 }
 
 template <int EPI, int D>
-__global__ __launch_bounds__(kThreads) void gemm_stream_lds_kernel(GroupedGemmArgs g) {
+__global__ __launch_bounds__(kThreads + kRopeWaves * kWave) void gemm_stream_lds_kernel(GroupedGemmArgs g) {
   static_assert(EPI == EPI_LINEAR || EPI == EPI_QKV_ROPE, "fused one-weight projection epilogues");
   static_assert((D & (D - 1)) == 0 && 2 * D <= 62, "ring slots: a power of two, loads within the vmcnt range");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   f32x4_t* partial = reinterpret_cast<f32x4_t*>(lds + kStreamWaves * D * 2048);  // [kStreamWaves - 1][kWave]
+  float2* rope_cs = reinterpret_cast<float2*>(lds + kStreamWaves * D * 2048 + (kStreamWaves - 1) * kWave * 16);
   const int ct = blockIdx.x;
   const int count = g.n_assign;  // <= 16 rows, in order (one expert, no grouping arrays)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop control
   const int64_t N = g.N;
-  const int ksteps = static_cast<int>(g.K / 32);
-  const int ks_begin = wave * ksteps / kStreamWaves;
-  const int n = (wave + 1) * ksteps / kStreamWaves - ks_begin;
   const int r = lane & 15;
-  const unsigned char* wsrc =
-      static_cast<const unsigned char*>(g.w0) + (static_cast<int64_t>(ct) * ksteps + ks_begin) * 1024 + lane * 16;
-  const unsigned char* tsrc = reinterpret_cast<const unsigned char*>(
-      static_cast<const bf16_t*>(g.a) + static_cast<int64_t>(r < count ? r : 0) * g.lda + (lane >> 4) * 8 +
-      static_cast<int64_t>(ks_begin) * 32);
-  unsigned char* ring = lds + wave * D * 2048;
-  auto issue = [&](int i) __attribute__((always_inline)) {
-    unsigned char* slot = ring + (i & (D - 1)) * 2048;
-    __builtin_amdgcn_global_load_lds(wsrc + static_cast<int64_t>(i) * 1024, slot, 16, 0, kNonTemporal);
-    __builtin_amdgcn_global_load_lds(tsrc + static_cast<int64_t>(i) * 64, slot + 1024, 16, 0, 0);
-  };
-  const int pre = n < D ? n : D;
-  for (int i = 0; i < pre; ++i) issue(i);
   f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < n; ++i) {
-    // step i's two loads are done once at most 2 (D - 1) younger ones are
-    // in flight (loads complete in order); near the end, all of them
-    if (i + D <= n)
-      __builtin_amdgcn_s_waitcnt(wait_vm(2 * D - 2, false));
-    else
-      __builtin_amdgcn_s_waitcnt(wait_vm(0, false));
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    const unsigned char* slot = ring + (i & (D - 1)) * 2048;
-    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(slot + lane * 16);
-    const u32x4_t t = *reinterpret_cast<const u32x4_t*>(slot + 1024 + lane * 16);
-    acc = mfma16(w, t, acc);
-    // the slot is refilled only after its reads have returned (the MFMA
-    // above waits for them)
-    __builtin_amdgcn_sched_barrier(0);
-    if (i + D < n) issue(i + D);
+  if (EPI == EPI_QKV_ROPE && wave >= kStreamWaves) {
+    // item = row * 8 + pair: columns 2 pair, 2 pair + 1 of the block, in the
+    // q or k part (v columns take no rotation)
+    const ProjEpilogue& e = g.pe;
+    const int item = tid - kThreads;
+    const int rr = item >> 3;
+    const int64_t n = static_cast<int64_t>(ct) * kStreamRows + 2 * (item & 7);
+    if (rr < count && n < static_cast<int64_t>(e.nq) + e.nkv) {
+      const int64_t c = n < e.nq ? n : n - e.nq;
+      rope_cs[item] = rope_cos_sin(e.positions[rr], static_cast<int>(c % e.head_dim) / 2, e.head_dim, e.freq_base,
+                                   e.freq_scale);
+    }
+  } else {
+    const int ksteps = static_cast<int>(g.K / 32);
+    const int ks_begin = wave * ksteps / kStreamWaves;
+    const int n = (wave + 1) * ksteps / kStreamWaves - ks_begin;
+    const unsigned char* wsrc =
+        static_cast<const unsigned char*>(g.w0) + (static_cast<int64_t>(ct) * ksteps + ks_begin) * 1024 + lane * 16;
+    const unsigned char* tsrc = reinterpret_cast<const unsigned char*>(
+        static_cast<const bf16_t*>(g.a) + static_cast<int64_t>(r < count ? r : 0) * g.lda + (lane >> 4) * 8 +
+        static_cast<int64_t>(ks_begin) * 32);
+    unsigned char* ring = lds + wave * D * 2048;
+    auto issue = [&](int i) __attribute__((always_inline)) {
+      unsigned char* slot = ring + (i & (D - 1)) * 2048;
+      __builtin_amdgcn_global_load_lds(wsrc + static_cast<int64_t>(i) * 1024, slot, 16, 0, kNonTemporal);
+      __builtin_amdgcn_global_load_lds(tsrc + static_cast<int64_t>(i) * 64, slot + 1024, 16, 0, 0);
+    };
+    const int pre = n < D ? n : D;
+    for (int i = 0; i < pre; ++i) issue(i);
+    for (int i = 0; i < n; ++i) {
+      // step i's two loads are done once at most 2 (D - 1) younger ones are
+      // in flight (loads complete in order); near the end, all of them
+      if (i + D <= n)
+        __builtin_amdgcn_s_waitcnt(wait_vm(2 * D - 2, false));
+      else
+        __builtin_amdgcn_s_waitcnt(wait_vm(0, false));
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      const unsigned char* slot = ring + (i & (D - 1)) * 2048;
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(slot + lane * 16);
+      const u32x4_t t = *reinterpret_cast<const u32x4_t*>(slot + 1024 + lane * 16);
+      acc = mfma16(w, t, acc);
+      // the slot is refilled only after its reads have returned (the MFMA
+      // above waits for them)
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + D < n) issue(i + D);
+    }
   }
 
   // Partial sums of waves 1..3 -> LDS; wave 0 adds them in wave order.
-  if (wave > 0) partial[(wave - 1) * kWave + lane] = acc;
+  if (wave > 0 && wave < kStreamWaves) partial[(wave - 1) * kWave + lane] = acc;
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
     for (int w = 1; w < kStreamWaves; ++w) acc += partial[(w - 1) * kWave + lane];
     const int64_t col = static_cast<int64_t>(ct) * kStreamRows + 4 * (lane >> 4);
-    if (r < count && col < N) store4<EPI>(g, r, col, acc[0], acc[1], acc[2], acc[3]);
+    if (r < count && col < N) {
+      if (EPI == EPI_QKV_ROPE) {
+        const int pr = r * 8 + 2 * (lane >> 4);  // the lane's two pairs
+        store4_proj<EPI, true>(g, r, col, acc[0], acc[1], acc[2], acc[3], rope_cs[pr], rope_cs[pr + 1]);
+      } else {
+        store4<EPI>(g, r, col, acc[0], acc[1], acc[2], acc[3]);
+      }
+    }
   }
 }
 
@@ -842,20 +883,20 @@ hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
     constexpr int kDepth = 8;
     static const bool configured = [] {
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_lds_kernel<EPI_LINEAR, kDepth>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes<kDepth>());
+                                hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes<kDepth, EPI_LINEAR>());
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_lds_kernel<EPI_QKV_ROPE, kDepth>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes<kDepth>());
+                                hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes<kDepth, EPI_QKV_ROPE>());
       (void)hipGetLastError();
       return true;
     }();
     (void)configured;
     const dim3 lgrid(static_cast<unsigned>(col_tiles));
     if (g.epi == EPI_LINEAR)
-      hipLaunchKernelGGL((gemm_stream_lds_kernel<EPI_LINEAR, kDepth>), lgrid, dim3(kThreads),
-                         stream_lds_bytes<kDepth>(), s, g);
+      hipLaunchKernelGGL((gemm_stream_lds_kernel<EPI_LINEAR, kDepth>), lgrid,
+                         dim3(stream_lds_threads<EPI_LINEAR>()), (stream_lds_bytes<kDepth, EPI_LINEAR>()), s, g);
     else
-      hipLaunchKernelGGL((gemm_stream_lds_kernel<EPI_QKV_ROPE, kDepth>), lgrid, dim3(kThreads),
-                         stream_lds_bytes<kDepth>(), s, g);
+      hipLaunchKernelGGL((gemm_stream_lds_kernel<EPI_QKV_ROPE, kDepth>), lgrid,
+                         dim3(stream_lds_threads<EPI_QKV_ROPE>()), (stream_lds_bytes<kDepth, EPI_QKV_ROPE>()), s, g);
     return hipGetLastError();
   }
   if (rows <= 16)
