@@ -190,6 +190,9 @@ int pick_path(const GroupedGemmArgs& g, int* variant_out) {
 int run_grouped_gemm(GroupedGemmArgs g, hipStream_t s, int* ksplit_used = nullptr) {
   int variant = TILED_AUTO;
   const int path = pick_path(g, &variant);
+  // Routing in the GEMM's blocks: only the streaming kernel computes it.
+  if (g.rp.part && path != FMOE_PATH_STREAM)
+    return fail(FMOE_ERR_HIP, "routed gate/up GEMM: the streaming kernel is not the chosen family");
   g.ksplit = 1;
   if ((path == FMOE_PATH_TILED || path == FMOE_PATH_TILED_LARGE) && variant == TILED_256 && g.split_stride > 0)
     g.ksplit = gemm_tiled256_ksplit(g);
@@ -477,7 +480,9 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
 
   // Steps 1-4: router logits, softmax, top-k, renormalisation (mlir:50-128),
   // then the slot-major assignments grouped by expert (replaces the gather,
-  // mul_mat_id.mlir:50-61).  Decode-sized batches run both as two launches.
+  // mul_mat_id.mlir:50-61).  Decode-sized batches run both as two launches,
+  // or (at most 4 tokens) as the logits launch plus the gate/up GEMM's
+  // blocks; the launches follow the GEMM setup below.
   const bool router16 = reinterpret_cast<uintptr_t>(c.input) % 16 == 0 &&
                         reinterpret_cast<uintptr_t>(c.w_router) % 16 == 0;
   const int H32 = static_cast<int>(n_embd), E32 = static_cast<int>(n_expert), k32 = static_cast<int>(n_expert_used);
@@ -485,20 +490,6 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
                              L.rpart_bytes >= router_decode_scratch_bytes(T, H32, E32, k32, act_dtype);
   const bool split_router = router16 && !decode_router && router_prefill_scratch_bytes(T, H32, E32, k32, act_dtype) > 0 &&
                             L.rpart_bytes >= router_prefill_scratch_bytes(T, H32, E32, k32, act_dtype);
-  if (decode_router) {
-    ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
-    FMOE_HIP(launch_router_decode(c.input, c.w_router, T, static_cast<int>(n_embd), static_cast<int>(n_expert),
-                                  static_cast<int>(n_expert_used), c.normalize_weights != 0, act_dtype,
-                                  at<float>(workspace, L.rpart), ids, rw, order, offsets, err, s));
-  } else {
-    ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
-    if (split_router)
-      FMOE_HIP(launch_router_prefill(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype,
-                                     at<float>(workspace, L.rpart), ids, rw, s));
-    else
-      FMOE_HIP(launch_router(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype, ids, rw,
-                             s));
-  }
 
   // Steps 5-8: up and gate projections + SwiGLU (mlir:130-156), h[p, :] per sorted row p.
   GroupedGemmArgs g;
@@ -612,6 +603,50 @@ int run_block(const BlockCall& c, const BlockLayout& L) {
         if (need > 0 && need <= tb.bytes) tb.x->tile_table = at<int>(workspace, tb.at);
       }
     }
+  }
+
+  // The router.  Decode batches of at most 4 tokens (k * n_tokens <= 64)
+  // whose gate/up GEMM takes the streaming kernel under the automatic choice
+  // run their softmax, top-k and grouping in that GEMM's blocks
+  // (RoutePrologue: the router's own top-k code, so the same ids, weights
+  // and rows), which saves the one-wave top-k launch; the router launch
+  // then writes the split logits only.
+  if (decode_router) {
+    ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
+    const int nv = (E32 + 15) / 16;
+    const int rnv = nv <= 1 ? 1 : nv <= 4 ? 4 : nv <= 8 ? 8 : 0;
+    int v = 0;
+    GroupedGemmArgs gr = g;
+    RoutePrologue& rp = gr.rp;
+    rp.part = at<float>(workspace, L.rpart);
+    rp.n_split = router_decode_splits(H32);
+    rp.k = k32;
+    rp.normalize = c.normalize_weights != 0;
+    rp.nv = rnv;
+    rp.ids = ids;
+    rp.weights = rw;
+    rp.order = order;
+    rp.offsets = offsets;
+    rp.err_count = err;
+    if (g_path.load(std::memory_order_relaxed) == FMOE_PATH_AUTO && T <= 4 && k32 * T <= 64 && rnv > 0 &&
+        pick_path(g, &v) == FMOE_PATH_STREAM && gemm_stream_routed_ok(gr)) {
+      int n_split = 0;
+      FMOE_HIP(launch_router_split_logits(c.input, c.w_router, T, H32, E32, k32, act_dtype,
+                                          at<float>(workspace, L.rpart), &n_split, s));
+      if (n_split != rp.n_split) return fail(FMOE_ERR_HIP, "split logits: %d splits, %d expected", n_split, rp.n_split);
+      g = gr;
+    } else {
+      FMOE_HIP(launch_router_decode(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype,
+                                    at<float>(workspace, L.rpart), ids, rw, order, offsets, err, s));
+    }
+  } else {
+    ScopedTimer t(FMOE_TIMER_ROUTER, s, c.timers);
+    if (split_router)
+      FMOE_HIP(launch_router_prefill(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype,
+                                     at<float>(workspace, L.rpart), ids, rw, s));
+    else
+      FMOE_HIP(launch_router(c.input, c.w_router, T, H32, E32, k32, c.normalize_weights != 0, act_dtype, ids, rw,
+                             s));
   }
 
   if (!decode_router) {

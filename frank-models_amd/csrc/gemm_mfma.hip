@@ -30,6 +30,10 @@
 // fused with the slot-ordered combine (down_combine_small_kernel).
 #include "common.h"
 #include "launch.h"
+#include "router_topk.h"
+
+#include <mutex>
+#include <unordered_map>
 
 namespace fmoe {
 namespace {
@@ -375,18 +379,84 @@ constexpr int stream_waves_per_eu() {
   return EPI == EPI_QKV_ROPE ? 2 : U > kStreamUnroll ? 2 : NSETS == 2 ? 3 : kStreamTiles == 1 ? 5 : 4;
 }
 
-template <int EPI, int NSETS, bool F8, int kStreamTiles, int U = kStreamUnroll>
+// RNV > 0 (one-tile gate/up kernels of decode batches of at most 4 tokens,
+// GroupedGemmArgs::rp): the block computes the routing itself from the
+// router's split partial logits.  Wave 0 runs the router's top-k
+// (wave_topk4_splits, RNV experts per row lane), marks the selected experts
+// in LDS, and block row a = blockIdx.x / col_tiles takes the a-th selected
+// expert in ascending order (found with wave ballots), with its rows in the
+// stable order: the flat ids f of that expert ascending, row r reading token
+// f % n_tokens, as the permutation would order them.  Blocks past the
+// selected experts exit.  Block 0 also stores ids, weights, order, offsets
+// and the invalid-id count for the down projection and the caller.
+template <int EPI, int NSETS, bool F8, int kStreamTiles, int U = kStreamUnroll, int RNV = 0>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<EPI, NSETS, kStreamTiles, U>())))
 void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
+  static_assert(RNV == 0 || (EPI == EPI_SWIGLU && kStreamTiles == 1), "routing in the one-tile gate/up kernel only");
   __shared__ f32x4_t partial[kStreamWaves - 1][kStreamTiles][NSETS][kWave];
-  const int e = blockIdx.x / col_tiles;
-  const int ct = blockIdx.x - e * col_tiles;
-  const int row_begin = g.offsets ? g.offsets[e] : 0;
-  const int count = g.offsets ? g.offsets[e + 1] - row_begin : g.n_assign;
-  if (count == 0) return;  // block-uniform
+  __shared__ float r_lg[RNV > 0 ? 4 * (16 * RNV + 1) : 1];
+  __shared__ int r_idl[RNV > 0 ? kWave : 1];
+  __shared__ int r_flag[RNV > 0 ? 256 : 1];
+  __shared__ int r_tok[RNV > 0 ? 16 : 1];
+  __shared__ int r_meta[RNV > 0 ? 3 : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int ct = blockIdx.x - (blockIdx.x / col_tiles) * col_tiles;
+  int e, row_begin, count;
+  if constexpr (RNV > 0) {
+    const RoutePrologue& rp = g.rp;
+    const int T = g.n_tokens, E = g.n_expert, n = rp.k * T;
+    const bool pub = blockIdx.x == 0;
+    if (wave == 0)
+      wave_topk4_splits<RNV>(rp.part, rp.n_split, T, E, rp.k, rp.normalize != 0, r_lg, pub ? rp.ids : nullptr,
+                             pub ? rp.weights : nullptr, r_idl);
+    for (int i = tid; i < E; i += kThreads) r_flag[i] = 0;
+    __syncthreads();
+    if (wave == 0) {
+      // ids outside [0, E) (the top-k's sentinel when probabilities are NaN)
+      // mark nothing and take no rows
+      if (lane < n && r_idl[lane] >= 0 && r_idl[lane] < E) r_flag[r_idl[lane]] = 1;
+      if (pub) {
+        wave_permute(r_idl, n, E, rp.order, rp.offsets);
+        if (lane == 0) rp.err_count[0] = 0;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int a = blockIdx.x / col_tiles;
+      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+      int sel = -1, below = 0;
+      for (int c0 = 0; c0 < E; c0 += kWave) {
+        const int c = c0 + lane;
+        const bool f = c < E && r_flag[c] != 0;
+        const uint64_t m = __ballot(f);
+        const uint64_t hit = __ballot(f && below + __popcll(m & lt) == a);
+        if (hit && sel < 0) sel = c0 + __builtin_ctzll(hit);
+        below += __popcll(m);
+      }
+      const int fe = lane < n ? r_idl[lane] : 0x7FFFFFFF;
+      const uint64_t mine = __ballot(lane < n && fe == sel);
+      const uint64_t lower = __ballot(lane < n && fe < sel);
+      // at most n_tokens rows (distinct experts per token), within the one tile
+      const int rank = __popcll(mine & lt);
+      if (lane < n && fe == sel && rank < 16) r_tok[rank] = lane % T;
+      if (lane == 0) {
+        r_meta[0] = sel;
+        r_meta[1] = __popcll(lower);
+        r_meta[2] = sel >= 0 ? min(__popcll(mine), 16) : 0;
+      }
+    }
+    __syncthreads();
+    e = r_meta[0];
+    row_begin = r_meta[1];
+    count = r_meta[2];
+  } else {
+    e = blockIdx.x / col_tiles;
+    row_begin = g.offsets ? g.offsets[e] : 0;
+    count = g.offsets ? g.offsets[e + 1] - row_begin : g.n_assign;
+  }
+  if (count == 0) return;  // block-uniform
   const int64_t N = g.N, K = g.K;
   const int64_t n_base = static_cast<int64_t>(ct) * kStreamRows;
   const int64_t nblocks = N / 16;
@@ -422,7 +492,8 @@ void gemm_stream_kernel(GroupedGemmArgs g, int col_tiles) {
     for (int mt = 0; mt < kStreamTiles; ++mt) {
       const int r = m0 + mt * 16 + (lane & 15);
       r_ok[mt] = r < count;
-      arow[mt] = static_cast<const bf16_t*>(g.a) + a_source_row(g, row_begin + (r_ok[mt] ? r : 0)) * g.lda + kq;
+      const int64_t src = RNV > 0 ? r_tok[r_ok[mt] ? r : 0] : a_source_row(g, row_begin + (r_ok[mt] ? r : 0));
+      arow[mt] = static_cast<const bf16_t*>(g.a) + src * g.lda + kq;
     }
     f32x4_t acc[kStreamTiles][NSETS];
 #pragma unroll
@@ -868,9 +939,83 @@ void launch_stream_tiles(const GroupedGemmArgs& g, hipStream_t s, dim3 grid, int
     hipLaunchKernelGGL((gemm_stream_kernel<EPI_SCATTER, 1, F8, TILES>), grid, dim3(kThreads), 0, s, g, col_tiles);
 }
 
+// The one-tile gate/up kernel with the routing in its blocks
+// (GroupedGemmArgs::rp): one block row per selected expert (at most
+// k * n_tokens of them), the trip length chosen as launch_stream_tiles does.
+// Every block pays the top-k (about 3 us) before its first weight load, so
+// the launch is taken only while its grid fits one round of resident blocks
+// (measured, cold calls: C4 T=1, 528 blocks in one round, 38.6 -> 37.1 us;
+// C4 T=4, 2112 blocks in about four rounds, 79.4 -> 85.2 us).
+template <bool F8, int RNV, int U>
+const void* routed_kernel() {
+  return reinterpret_cast<const void*>(gemm_stream_kernel<EPI_SWIGLU, 2, F8, 1, U, RNV>);
+}
+
+template <bool F8, int RNV>
+const void* routed_kernel_for(unsigned blocks) {
+  if constexpr (!F8) {
+    if (!(blocks > 2 * 256 && blocks <= 3 * 256)) return routed_kernel<F8, RNV, 16>();
+  }
+  return routed_kernel<F8, RNV, kStreamUnroll>();
+}
+
+template <bool F8>
+const void* routed_kernel_nv(int nv, unsigned blocks) {
+  if (nv == 1) return routed_kernel_for<F8, 1>(blocks);
+  if (nv == 4) return routed_kernel_for<F8, 4>(blocks);
+  if (nv == 8) return routed_kernel_for<F8, 8>(blocks);
+  return nullptr;
+}
+
+// Blocks of `kernel` one round of the device holds (occupancy x CUs), cached.
+int round_blocks(const void* kernel) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, int> cache;
+  std::lock_guard<std::mutex> lk(mu);
+  const auto it = cache.find(kernel);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, dev = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
+      hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return cache[kernel] = per_cu * cus;
+}
+
+// The routed launch's kernel, or nullptr when the arguments do not qualify
+// or its grid would not fit one round.
+const void* routed_launch(const GroupedGemmArgs& g, unsigned* grid_out) {
+  const RoutePrologue& rp = g.rp;
+  const int rows = g.max_rows_per_expert > 0 ? g.max_rows_per_expert : g.n_assign;
+  if (!rp.part || g.epi != EPI_SWIGLU || rows > 16 || g.ksplit > 1 || g.n_tokens < 1 || g.n_tokens > 4 ||
+      rp.k < 1 || rp.k * g.n_tokens > kWave || g.n_expert > 256 || g.n_expert > 16 * rp.nv || rp.n_split < 1 ||
+      !rp.ids || !rp.weights || !rp.order || !rp.offsets || !rp.err_count || !gemm_stream_supported(g))
+    return nullptr;
+  const int col_tiles = static_cast<int>((g.N + kStreamRows - 1) / kStreamRows);
+  const int n_rows = g.n_expert < rp.k * g.n_tokens ? g.n_expert : rp.k * g.n_tokens;
+  const unsigned blocks = static_cast<unsigned>(col_tiles * n_rows);
+  const void* k = g.w_dtype == DT_F8 ? routed_kernel_nv<true>(rp.nv, blocks) : routed_kernel_nv<false>(rp.nv, blocks);
+  if (!k || static_cast<int64_t>(blocks) > round_blocks(k)) return nullptr;
+  *grid_out = blocks;
+  return k;
+}
+
+template <bool F8>
+hipError_t launch_stream_routed(const GroupedGemmArgs& g, hipStream_t s, int col_tiles) {
+  unsigned blocks = 0;
+  const void* k = routed_launch(g, &blocks);
+  if (!k) return hipErrorNotSupported;
+  GroupedGemmArgs a = g;
+  void* args[] = {&a, &col_tiles};
+  return hipLaunchKernel(k, dim3(blocks), dim3(kThreads), args, 0, s);
+}
+
 template <bool F8>
 hipError_t launch_stream_t(const GroupedGemmArgs& g, hipStream_t s) {
   const int col_tiles = static_cast<int>((g.N + kStreamRows - 1) / kStreamRows);
+  if (g.rp.part) return launch_stream_routed<F8>(g, s, col_tiles);
   const dim3 grid(static_cast<unsigned>(col_tiles * g.n_expert));
   // Rows one pass must cover to read each expert's weights once.
   const int rows = g.max_rows_per_expert > 0 ? g.max_rows_per_expert : g.n_assign;
@@ -926,6 +1071,11 @@ bool proj_epilogue_ok(const GroupedGemmArgs& g) {
          al8(e.k_out) && al8(e.v_out) && e.nq > 0 && e.nkv > 0 && e.nq % 4 == 0 && e.nkv % 4 == 0 &&
          e.head_dim > 0 && e.head_dim % 4 == 0 && e.nq % e.head_dim == 0 && e.nkv % e.head_dim == 0 &&
          g.N == static_cast<int64_t>(e.nq) + 2 * e.nkv;
+}
+
+bool gemm_stream_routed_ok(const GroupedGemmArgs& g) {
+  unsigned blocks = 0;
+  return routed_launch(g, &blocks) != nullptr;
 }
 
 bool gemm_stream_supported(const GroupedGemmArgs& g) {

@@ -86,6 +86,27 @@ struct ProjEpilogue {
   void* v_out = nullptr;            // [rows, nkv] bf16
 };
 
+// Routing computed inside the streaming gate/up GEMM of decode batches of
+// at most 4 tokens (launch_router_split_logits wrote the partial logits):
+// every block sums the n_split partials, runs the router's softmax + top-k
+// (the same code as router_topk_permute_wave_kernel, so the same ids and
+// weights) and takes the expert of its block row; block 0 also stores ids,
+// weights, the grouping (order, offsets) and the invalid-id count (0) for
+// the launches that follow, which no block of the GEMM reads.  nv: experts
+// per row lane of the top-k (n_expert <= 16 nv; 1, 4 or 8).
+struct RoutePrologue {
+  const float* part = nullptr;  // [n_split][n_tokens][n_expert]; nullptr: no routing here
+  int n_split = 0;
+  int k = 0;
+  int normalize = 0;
+  int nv = 0;
+  int* ids = nullptr;           // [k][n_tokens]
+  float* weights = nullptr;     // [k][n_tokens]
+  int* order = nullptr;         // [k * n_tokens]
+  int* offsets = nullptr;       // [n_expert + 1]
+  int* err_count = nullptr;
+};
+
 struct GroupedGemmArgs {
   const void* a = nullptr;      // A operand base, act_dtype
   int64_t lda = 0;              // elements between A rows
@@ -152,6 +173,7 @@ struct GroupedGemmArgs {
   int* tile_table = nullptr;
   bool tile_table_ready = false;
   ProjEpilogue pe;              // EPI_LINEAR / EPI_QKV_ROPE only
+  RoutePrologue rp;             // streaming gate/up GEMM of decode batches only
 };
 
 // Element offset of (row, col) in a K-blocked bf16 matrix of `rows` rows.
@@ -183,6 +205,13 @@ size_t router_decode_scratch_bytes(int n_tokens, int n_embd, int n_expert, int k
 hipError_t launch_router_decode(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k,
                                 bool normalize, int dtype, float* part, int* ids, float* weights, int* order,
                                 int* offsets, int* err_count, hipStream_t stream);
+// The first of those launches alone (the split partial logits into part,
+// n_split_out = their count), for callers that run the top-k themselves
+// (RoutePrologue).  hipErrorNotSupported when the inputs do not qualify.
+hipError_t launch_router_split_logits(const void* x, const void* wr, int n_tokens, int n_embd, int n_expert, int k,
+                                      int dtype, float* part, int* n_split_out, hipStream_t stream);
+// The column splits launch_router_split_logits uses for n_embd inputs.
+int router_decode_splits(int n_embd);
 
 // Prefill batches (bf16, n_tokens > kDecodeMaxTokens, 32 < n_expert <= 128,
 // n_embd % 128 == 0, k <= 16): router logits over 64-token tiles and
@@ -241,6 +270,9 @@ hipError_t launch_down_combine_small(const GroupedGemmArgs& d, const void* resid
                                      int n_tokens, int k, hipStream_t stream);
 bool gemm_tiled_supported(const GroupedGemmArgs& g);
 bool gemm_stream_supported(const GroupedGemmArgs& g);
+// Whether the streaming gate/up GEMM takes g with its routing (g.rp set):
+// the shape qualifies and the grid fits one round of resident blocks.
+bool gemm_stream_routed_ok(const GroupedGemmArgs& g);
 // 256x256-tile bf16 kernel (gemm_tiled256.hip); launch_gemm_tiled uses it
 // when it applies.
 bool gemm_tiled256_supported(const GroupedGemmArgs& g);

@@ -101,9 +101,10 @@ int fmoe_device_check(int *device, char *arch, size_t arch_len);
  * e4m3 quantisation passes under FMOE_TIMER_QUANT), so per-call times are
  * the sums divided by the number of calls, not by the region counts. */
 typedef enum fmoe_timer {
-  FMOE_TIMER_ROUTER = 0,
+  FMOE_TIMER_ROUTER = 0,  /* router logits + softmax + top-k (decode batches whose gate/up GEMM
+                             routes in its blocks: the logits only; GATE_UP holds the rest) */
   FMOE_TIMER_PERMUTE = 1,
-  FMOE_TIMER_GATE_UP = 2, /* grouped GEMM: gate + up projections + SwiGLU */
+  FMOE_TIMER_GATE_UP = 2, /* grouped GEMM: gate + up projections + SwiGLU (+ the top-k, see ROUTER) */
   FMOE_TIMER_DOWN = 3,    /* grouped GEMM: down projection + routing weight (decode batches of
                              at most 16 assignments: + the slot-ordered combine, one launch) */
   FMOE_TIMER_COMBINE = 4, /* slot-ordered sum (+ residual); no launch where DOWN includes it */

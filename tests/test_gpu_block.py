@@ -178,6 +178,36 @@ def test_decode_one_wave_router_shapes(fm, wl, name, H, F, T, E, k):
     assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
 
 
+# Decode batches of at most 4 tokens on the automatic kernel choice run the
+# top-k and the grouping inside the gate/up GEMM's blocks (one launch fewer);
+# a forced streaming kernel keeps the one-wave top-k launch.  The two give the
+# same output, ids, weights, order and offsets bit for bit: 1, 4 and 8
+# experts per top-k lane (8; 20 and 64; 100 and 128 experts), k up to 16 (64
+# assignments), renormalisation, fp8 weights, 1-4 tokens; 200 experts (more
+# than 8 per lane) keep the launch on both paths.
+@pytest.mark.parametrize("name,H,F,T,E,k,normalize", [
+    ("C2", 256, 128, 1, 8, 2, False), ("C4", 256, 128, 3, 20, 3, True), ("C4", 512, 128, 4, 64, 6, False),
+    ("C4", 256, 64, 4, 64, 16, True), ("C3", 256, 128, 1, 128, 8, True), ("C3", 384, 128, 2, 100, 5, False),
+    ("C5", 256, 128, 1, 8, 2, False), ("C3", 256, 64, 2, 200, 8, True),
+])
+def test_decode_routing_in_gate_up(fm, wl, gemm_path, name, H, F, T, E, k, normalize):
+    cfg = _scaled(wl, name, H, F, n_expert=E, n_expert_used=k, normalize=normalize, margin=1e-4)
+    case = Case(fm, wl, cfg, T)
+    got = {}
+    for p in ("auto", "stream"):
+        _set_path(gemm_path, p)
+        out = case.run()
+        routing = case.block.routing(T)
+        got[p] = [out.view(np.uint32)] + [t.cpu().numpy().view(np.uint32) for t in routing]
+    for what, a, b in zip(("output", "ids", "weights", "order", "offsets"), got["auto"], got["stream"]):
+        np.testing.assert_array_equal(a, b, err_msg=f"{name} T={T} E={E} k={k}: {what}")
+    _set_path(gemm_path, "auto")
+    out = case.run()
+    ref, ids, _ = case.oracle(dtype=np.float32)
+    _check_routing(case, ids)
+    assert_close_rms(out, ref, cfg.rtol, what=f"{name} H={H} T={T} E={E} k={k}")
+
+
 # Prefill GEMMs with at least 16 column tiles (gate/up: n_ff >= 2048; down:
 # n_embd >= 4096) take their tiles from a per-launch schedule table that the
 # permutation builds: uniform and Zipf-skewed routing, a ragged batch, (C5)
