@@ -26,6 +26,9 @@
 //           pass, 8 input steps of loads in flight per wave (16 for the
 //           one-tile bf16 gate/up kernel); one-weight projections of at most
 //           16 rows stream through a ring in LDS instead (gemm_stream_lds_kernel).
+//           For decode batches of at most 4 tokens the gate/up kernel can run
+//           the router's top-k and grouping in its own blocks (RoutePrologue),
+//           one launch fewer.
 // And, for decode batches of at most 16 assignments, the down projection
 // fused with the slot-ordered combine (down_combine_small_kernel).
 #include "common.h"
