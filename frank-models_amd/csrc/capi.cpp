@@ -118,8 +118,11 @@ hipEvent_t take_event() {
     g_event_pool.pop_back();
     return e;
   }
+  // Timing-only events: no system-scope release when recorded, so a record
+  // neither writes back and invalidates the caches nor slows the launches
+  // that follow (the readback waits on the event and reads its timestamps).
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 
