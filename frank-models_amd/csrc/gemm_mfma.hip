@@ -35,8 +35,9 @@
 #include "launch.h"
 #include "router_topk.h"
 
+#include <map>
 #include <mutex>
-#include <unordered_map>
+#include <utility>
 
 namespace fmoe {
 namespace {
@@ -970,21 +971,27 @@ const void* routed_kernel_nv(int nv, unsigned blocks) {
   return nullptr;
 }
 
-// Blocks of `kernel` one round of the device holds (occupancy x CUs), cached.
+// Blocks of `kernel` one round of the current device holds (occupancy x
+// CUs), cached per device.
 int round_blocks(const void* kernel) {
   static std::mutex mu;
-  static std::unordered_map<const void*, int> cache;
+  static std::map<std::pair<int, const void*>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
   std::lock_guard<std::mutex> lk(mu);
-  const auto it = cache.find(kernel);
+  const auto key = std::make_pair(dev, kernel);
+  const auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  int per_cu = 0, dev = 0, cus = 0;
+  int per_cu = 0, cus = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
-      hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
     (void)hipGetLastError();
     return 0;
   }
-  return cache[kernel] = per_cu * cus;
+  return cache[key] = per_cu * cus;
 }
 
 // The routed launch's kernel, or nullptr when the arguments do not qualify
