@@ -225,8 +225,8 @@ def _time_oracle(fn, runs):
     return sorted(times)[len(times) // 2]
 
 
-# The literal form's rows (BASELINE.md's CPU plan): where the gathered weight
-# copies of one projection take at most 8 GB.
+# The literal form's rows: every configuration and token count where the
+# gathered weight copies of one projection take at most 8 GB.
 LITERAL_ROWS = [("C1", 32), ("C4", 1), ("C4", 4), ("C4", 16), ("C4", 64), ("C3", 64), ("C2", 16)]
 LITERAL_BUDGET = 8e9
 
